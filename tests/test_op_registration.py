@@ -1,0 +1,94 @@
+"""The drop-in surface: the extension modules register the reference's torch-op
+namespaces with byte-identical schemas (reference csrc/v1/wkv/torch_bindings.cpp:
+231-258, csrc/rwkv7/torch_bindings.cpp:36-50), the Python wrappers keep the
+reference's names and signatures (vkwr/_ops/v1/v1_wkv_ops.py, vkwr/_ops/rwkv7_ops.py),
+and CPU tensors are refused by the dispatcher as in the reference (CUDA-only impls)."""
+import inspect
+
+import pytest
+import torch
+
+import vkwr_amd  # noqa: F401
+from vkwr_amd._ops import rwkv7_ops
+from vkwr_amd._ops.v1 import v1_wkv_ops
+
+# The reference's schema strings (the interface itself, kept identical on purpose).
+REF_SCHEMAS = {
+    "vkwr_v1_wkv": [
+        "wkv_seq_fp16(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
+        "wkv_seq_w0_fp16(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor w0, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
+        "wkv_one_fp16(int B, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
+        "wkv_one_w0_fp16(int B, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor w0, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
+        "wkv_forward_fp32(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y) -> ()",
+        "wkv_forward_seq_fp32(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y) -> ()",
+        "wkv_forward_small_fp32(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y) -> ()",
+        "wkv_forward_block_fp32(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y) -> ()",
+        "advance_i32(Tensor(a!) x, int amount) -> ()",
+    ],
+    "vkwr_rwkv7": [
+        "forward_seq(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
+        "forward_one(int B, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
+        "spmv_forward(int D, int C, Tensor vec, Tensor mat, Tensor(a!) out) -> ()",
+    ],
+}
+
+
+def _cases():
+    for ns, schemas in REF_SCHEMAS.items():
+        for s in schemas:
+            yield ns, s
+
+
+@pytest.mark.parametrize("ns,schema", list(_cases()))
+def test_schema_identical(ns, schema):
+    name = schema.split("(", 1)[0]
+    op = getattr(getattr(torch.ops, ns), name).default
+    want = torch._C.parse_schema(f"{ns}::{schema}")
+    assert str(op._schema) == str(want)
+
+
+REF_WRAPPERS = {
+    v1_wkv_ops: {
+        "wkv_seq_fp16": "B, T, C, H, state, r, w, k, v, a, b",
+        "wkv_seq_w0_fp16": "B, T, C, H, state, r, w, w0, k, v, a, b",
+        "wkv_one_fp16": "B, C, H, state, r, w, k, v, a, b",
+        "wkv_one_w0_fp16": "B, C, H, state, r, w, w0, k, v, a, b",
+        "wkv_forward_fp32": "B, T, C, H, state, r, w, k, v, a, b",
+        "wkv_forward_seq_fp32": "B, T, C, H, state, r, w, k, v, a, b",
+        "wkv_forward_small_fp32": "B, T, C, H, state, r, w, k, v, a, b",
+        "wkv_forward_block_fp32": "B, T, C, H, state, r, w, k, v, a, b",
+        "advance_i32": "x, amount",
+    },
+    rwkv7_ops: {
+        "rwkv7_fwd_seq": "B, T, C, state, r, w, k, v, a, b, elapsed_t",
+        "rwkv7_fwd_one": "B, C, state, r, w, k, v, a, b, elapsed_t",
+        "spmv_forward": "vec, mat",
+    },
+}
+
+
+@pytest.mark.parametrize("mod,name", [(m, n) for m, d in REF_WRAPPERS.items() for n in d])
+def test_wrapper_signature(mod, name):
+    params = ", ".join(inspect.signature(getattr(mod, name)).parameters)
+    assert params == REF_WRAPPERS[mod][name]
+    assert v1_wkv_ops.HEAD_SIZE == 64 and rwkv7_ops.HEAD_SIZE == 64
+
+
+def test_cpu_tensors_rejected_by_dispatcher():
+    B, T, C, H = 1, 1, 64, 1
+    state = torch.zeros(B, H, 64, 64)
+    x = torch.zeros(B, T, C, dtype=torch.float16)
+    with pytest.raises(NotImplementedError):
+        torch.ops.vkwr_v1_wkv.wkv_forward_fp32(B, T, C, H, state, x, x, x, x, x, x, x.clone())
+    with pytest.raises(NotImplementedError):
+        torch.ops.vkwr_v1_wkv.advance_i32(torch.zeros(4, dtype=torch.int32), 1)
+
+
+def test_validate_slots_host_check():
+    v1_wkv_ops.validate_slots(torch.tensor([3, 1, 0], dtype=torch.int32), 4)
+    with pytest.raises(RuntimeError):
+        v1_wkv_ops.validate_slots(torch.tensor([3, 3], dtype=torch.int32), 4)
+    with pytest.raises(RuntimeError):
+        v1_wkv_ops.validate_slots(torch.tensor([4], dtype=torch.int32), 4)
+    with pytest.raises(RuntimeError):
+        v1_wkv_ops.validate_slots(torch.tensor([-1], dtype=torch.int32), 4)

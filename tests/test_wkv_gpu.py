@@ -1,0 +1,377 @@
+"""GPU parity of the WKV-7 kernels against the CPU oracle, through the torch ops.
+
+Bar (north_star): state gather/scatter and slot indexing bit-exact; y within
+max-abs 2e-2 / mean-rel 5e-3 (fp16); final fp32 state within max-abs 1e-3.
+The kernels perform the oracle's IEEE operations in the oracle's order, so the
+tests below demand (and report) bit equality, which implies those tolerances.
+Also restated: the reference's own WKV unit tests
+(reference tests/ops/test_v1_wkv_ops.py:161-466).
+"""
+import os
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.wkv_inputs import make_state, make_wkv_inputs
+
+pytestmark = pytest.mark.gpu
+
+Y_MAX_ABS, Y_MEAN_REL, STATE_MAX_ABS = 2e-2, 5e-3, 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_threads():
+    orc.set_threads(min(16, len(os.sched_getaffinity(0))))
+
+
+def _dev(xs, device):
+    return [torch.from_numpy(np.ascontiguousarray(x)).to(device) for x in xs]
+
+
+def _check_y(y_gpu, y_ref, what):
+    yg = y_gpu.detach().cpu().numpy().astype(np.float64)
+    yr = y_ref.astype(np.float64)
+    err = np.abs(yg - yr)
+    mean_rel = err.sum() / max(np.abs(yr).sum(), 1e-30)
+    assert err.max() <= Y_MAX_ABS and mean_rel <= Y_MEAN_REL, (what, err.max(), mean_rel)
+    assert np.array_equal(y_gpu.detach().cpu().numpy().view(np.uint16), y_ref.view(np.uint16)), (
+        what, "y not bit-identical", int((yg != yr).sum()))
+
+
+def _check_state(s_gpu, s_ref, what):
+    sg = s_gpu.detach().cpu().numpy()
+    assert np.abs(sg.astype(np.float64) - s_ref.astype(np.float64)).max() <= STATE_MAX_ABS, what
+    assert np.array_equal(sg.view(np.uint8), s_ref.view(np.uint8)), (what, "state not bit-identical")
+
+
+# ---------------------------------------------------------------- fp32 dense
+
+FP32_CASES = [
+    # (B, T, H, dist, state_std)
+    (1, 1, 1, "realistic", 0.0),
+    (1, 4, 2, "realistic", 0.0),
+    (2, 8, 4, "realistic", 0.1),
+    (1, 16, 2, "realistic", 0.1),
+    (3, 5, 3, "baseline", 0.1),
+    (2, 128, 12, "baseline", 0.0),
+]
+
+
+@pytest.mark.parametrize("mode", ["wkv_forward_fp32", "wkv_forward_seq_fp32", "wkv_forward_small_fp32", "wkv_forward_block_fp32"])
+@pytest.mark.parametrize("B,T,H,dist,std", FP32_CASES)
+def test_fp32_dense_matches_oracle(gpu, mode, B, T, H, dist, std):
+    if mode != "wkv_forward_fp32" and T > 16:
+        pytest.skip("large case runs once, under the default mode")
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    C = H * 64
+    ins = make_wkv_inputs(B, T, H, seed=B * 100 + T, dist=dist)
+    S0 = make_state(B, H, seed=T, std=std)
+    S_ref = S0.copy()
+    y_ref = orc.wkv_fp32(B, T, C, H, S_ref, *ins)
+    state = torch.from_numpy(S0).to(gpu)
+    y = getattr(ops, mode)(B, T, C, H, state, *_dev(ins, gpu))
+    torch.cuda.synchronize()
+    _check_y(y, y_ref, mode)
+    _check_state(state, S_ref, mode)
+
+
+# ---------------------------------------------------------------- slot pool
+
+
+def test_slots_config1_steps_match_oracle(gpu):
+    """BASELINE config 1 at full size: pool 512 x H=32, 128 distinct slots, 3 decode steps."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    P, B, H = 512, 128, 32
+    C = H * 64
+    pool_np = make_state(P, H, seed=1)
+    slots_np = np.random.default_rng(1).permutation(P)[:B].astype(np.int32)
+    pool = torch.from_numpy(pool_np).to(gpu)
+    slots = torch.from_numpy(slots_np).to(gpu)
+    ops.validate_slots(slots, P)
+    for step in range(3):
+        ins = make_wkv_inputs(B, 1, H, seed=1000 + step)
+        y_ref = orc.wkv_fp32_slots(B, 1, C, H, pool_np, slots_np.astype(np.int64), *ins)
+        y = ops.wkv_one_slots_fp32(B, C, H, pool, slots, *_dev([x.reshape(B, C) for x in ins], gpu))
+        torch.cuda.synchronize()
+        _check_y(y.view(B, 1, C), y_ref, f"slots step {step}")
+    _check_state(pool, pool_np, "pool after 3 steps")  # includes the 384 untouched slots
+
+
+def test_slots_equal_gather_dense_scatter(gpu):
+    """Fused slot op == index_select -> wkv_forward_fp32 -> index_copy_, bitwise, T=3."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    P, B, T, H = 40, 9, 3, 4
+    C = H * 64
+    pool = torch.from_numpy(make_state(P, H, seed=2)).to(gpu)
+    pool2 = pool.clone()
+    slots = torch.randperm(P, generator=torch.Generator().manual_seed(2))[:B].to(torch.int32).to(gpu)
+    ins = _dev(make_wkv_inputs(B, T, H, seed=2), gpu)
+    y1 = ops.wkv_forward_slots_fp32(B, T, C, H, pool, slots, *ins, validate=True)
+    st = pool2.index_select(0, slots.long())
+    y2 = ops.wkv_forward_fp32(B, T, C, H, st, *ins)
+    pool2.index_copy_(0, slots.long(), st)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(pool, pool2)
+
+
+def test_slots_out_of_range_is_skipped(gpu):
+    """A slot outside [0,P) (device-side bounds check): NaN y rows, pool bitwise unchanged."""
+    P, B, H = 8, 3, 2
+    C = H * 64
+    pool = torch.from_numpy(make_state(P, H, seed=3)).to(gpu)
+    before = pool.clone()
+    slots = torch.tensor([1, P + 5, 4], dtype=torch.int32, device=gpu)
+    ins = _dev(make_wkv_inputs(B, 1, H, seed=3), gpu)
+    y = torch.empty(B, 1, C, dtype=torch.float16, device=gpu)
+    torch.ops.vkwr_v1_wkv.wkv_forward_slots_fp32(B, 1, C, H, pool, slots, *ins, y)
+    torch.cuda.synchronize()
+    assert torch.isnan(y[1]).all() and not torch.isnan(y[0]).any() and not torch.isnan(y[2]).any()
+    untouched = [0, 2, 3, 5, 6, 7]
+    assert torch.equal(pool[untouched], before[untouched])
+    with pytest.raises(RuntimeError):
+        from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+        ops.wkv_forward_slots_fp32(B, 1, C, H, pool, slots, *ins, validate=True)
+
+
+def test_prefill_config2_reduced_matches_oracle(gpu):
+    """BASELINE config 2 shape (T=1024, H=32) at B=2, slots gathered from a pool."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    P, B, T, H = 16, 2, 1024, 32
+    C = H * 64
+    pool_np = make_state(P, H, seed=4)
+    slots_np = np.array([11, 3], dtype=np.int32)
+    ins = make_wkv_inputs(B, T, H, seed=4)
+    pool = torch.from_numpy(pool_np).to(gpu)
+    y = ops.wkv_forward_slots_fp32(B, T, C, H, pool, torch.from_numpy(slots_np).to(gpu), *_dev(ins, gpu))
+    y_ref = orc.wkv_fp32_slots(B, T, C, H, pool_np, slots_np.astype(np.int64), *ins)
+    torch.cuda.synchronize()
+    _check_y(y, y_ref, "prefill B=2 T=1024")
+    _check_state(pool, pool_np, "prefill pool")
+
+
+def test_prefill_config2_full_equals_decode_steps(gpu):
+    """BASELINE config 2 at full size (B=8,T=1024,H=32): one prefill call == 1024 decode
+    calls, bitwise (size-independent property; the oracle covers B=2 above)."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, H = 8, 1024, 32
+    C = H * 64
+    g = torch.Generator(device=gpu).manual_seed(5)
+    ins = [torch.randn(B, T, C, device=gpu, generator=g).half() for _ in range(6)]
+    ins[4] = -torch.nn.functional.normalize(ins[2].float().view(B, T, H, 64), dim=-1).reshape(B, T, C).half()
+    ins[5] = (-ins[4].float() * torch.sigmoid(torch.randn(B, T, C, device=gpu, generator=g))).half()
+    s1 = (torch.randn(B, H, 64, 64, device=gpu, generator=g) * 0.1).contiguous()
+    s2 = s1.clone()
+    y1 = ops.wkv_forward_fp32(B, T, C, H, s1, *ins)
+    y2 = torch.empty_like(y1)
+    for t in range(T):
+        y2[:, t:t + 1] = ops.wkv_forward_fp32(B, 1, C, H, s2, *(x[:, t:t + 1].contiguous() for x in ins))
+    torch.cuda.synchronize()
+    assert torch.equal(s1, s2)
+    assert torch.equal(y1, y2)
+
+
+# ---------------------------------------------------------------- fp16 family
+
+FP16_CASES = [(1, 1, 1), (1, 4, 1), (2, 8, 2), (4, 4, 4), (1, 16, 2), (3, 7, 3)]
+
+
+@pytest.mark.parametrize("variant", ["seq", "seq_w0", "one", "one_w0", "legacy_seq", "legacy_one"])
+@pytest.mark.parametrize("B,T,H", FP16_CASES)
+def test_fp16_family_matches_oracle(gpu, variant, B, T, H):
+    if variant.endswith("one"):
+        T = 1
+    if variant in ("one", "one_w0") and T != 1:
+        T = 1
+    C = H * 64
+    ins = make_wkv_inputs(B, T, H, seed=7 * B + T, dist="realistic")
+    S0 = make_state(B, H, seed=B + T, std=0.1, dtype=np.float16)
+    el = np.random.default_rng(B * T).integers(0, 1 << 30, size=B).astype(np.int32)
+    w0 = (np.random.default_rng(T).standard_normal(C) * 0.1).astype(np.float16) if "w0" in variant else None
+    legacy = variant.startswith("legacy")
+    S_ref = S0.copy()
+    y_ref = orc.wkv_fp16(B, T, C, H, S_ref, *ins, el, w0=w0, legacy=legacy)
+
+    state = torch.from_numpy(S0).to(gpu)
+    d = _dev(ins, gpu)
+    elt = torch.from_numpy(el).to(gpu)
+    y = torch.empty(B, T, C, dtype=torch.float16, device=gpu)
+    ns = torch.ops.vkwr_v1_wkv
+    if variant == "seq":
+        ns.wkv_seq_fp16(B, T, C, H, state, *d, y, elt)
+    elif variant == "seq_w0":
+        ns.wkv_seq_w0_fp16(B, T, C, H, state, d[0], d[1], torch.from_numpy(w0).to(gpu), *d[2:], y, elt)
+    elif variant == "one":
+        y = y.view(B, C)
+        ns.wkv_one_fp16(B, C, H, state, *(x.view(B, C) for x in d), y, elt)
+    elif variant == "one_w0":
+        y = y.view(B, C)
+        dd = [x.view(B, C) for x in d]
+        ns.wkv_one_w0_fp16(B, C, H, state, dd[0], dd[1], torch.from_numpy(w0).to(gpu), *dd[2:], y, elt)
+    elif variant == "legacy_seq":
+        torch.ops.vkwr_rwkv7.forward_seq(B, T, C, H, state, *d, y, elt)
+    else:
+        y = y.view(B, C)
+        torch.ops.vkwr_rwkv7.forward_one(B, C, H, state, *(x.view(B, C) for x in d), y, elt)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().reshape(B, T, C).view(np.uint16), y_ref.view(np.uint16)), variant
+    assert np.array_equal(state.cpu().numpy().view(np.uint16), S_ref.view(np.uint16)), variant
+
+
+def test_fp16_w0_one_token_state_shape_from_reference_tests(gpu):
+    """The reference tests pass w0 as [B,T,C]; only the first C values are used."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, C = 2, 8, 128
+    H = C // 64
+    state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
+    r, w, k, v, a, b = _dev(make_wkv_inputs(B, T, H, seed=9, dist="realistic"), gpu)
+    w0 = (torch.randn(B, T, C, device=gpu) * 0.1).half()
+    y, el = ops.wkv_seq_w0_fp16(B, T, C, H, state, r, w, w0, k, v, a, b)
+    state2 = torch.zeros_like(state)
+    y2, _ = ops.wkv_seq_w0_fp16(B, T, C, H, state2, r, w, w0.reshape(-1)[:C].contiguous(), k, v, a, b)
+    assert torch.equal(y, y2) and torch.equal(state, state2)
+
+
+def test_legacy_state_as_1_c_64(gpu):
+    """The legacy golden test reshapes the state to [1,C,64] (reference test_monkey_patch.py:39-43)."""
+    from vkwr_amd._ops import rwkv7_ops
+
+    C = 128
+    ins = _dev(make_wkv_inputs(1, 3, 2, seed=10, dist="realistic"), gpu)
+    st_a = torch.zeros(1, C, 64, dtype=torch.float16, device=gpu)
+    st_b = torch.zeros(1, 2, 64, 64, dtype=torch.float16, device=gpu)
+    el = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ya = rwkv7_ops.rwkv7_fwd_seq(1, 3, C, st_a, *ins, el)
+    yb = rwkv7_ops.rwkv7_fwd_seq(1, 3, C, st_b, *ins, el)
+    assert torch.equal(ya, yb) and torch.equal(st_a.view(-1), st_b.view(-1))
+
+
+# ---------------------------------------------------------------- reference unit tests, restated
+
+
+def _fp16_inputs(B, T, C, device):
+    return [torch.randn(B, T, C, dtype=torch.float16, device=device) for _ in range(6)]
+
+
+@pytest.mark.parametrize("B,T,C", [(1, 1, 64), (1, 4, 64), (2, 8, 128), (4, 4, 256), (1, 16, 128)])
+def test_ref_wkv_seq_fp16_basic(gpu, B, T, C):
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    H = C // 64
+    state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
+    y, el = ops.wkv_seq_fp16(B, T, C, H, state, *_fp16_inputs(B, T, C, gpu))
+    assert y.shape == (B, T, C) and y.dtype == torch.float16 and y.device.type == "cuda"
+    assert el.shape == (B,) and el.dtype == torch.int32
+
+
+def test_ref_fp16_not_nan_mutation_zero_determinism(gpu):
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, C = 2, 8, 256
+    H = C // 64
+    state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
+    ins = _dev(make_wkv_inputs(B, T, H, seed=1, dist="realistic"), gpu)
+    y, _ = ops.wkv_seq_fp16(B, T, C, H, state, *ins)
+    assert not torch.isnan(y).any() and not torch.isinf(y).any()
+    assert not torch.equal(state, torch.zeros_like(state))
+    z = torch.zeros(1, 4, 128, dtype=torch.float16, device=gpu)
+    y0, _ = ops.wkv_seq_fp16(1, 4, 128, 2, torch.zeros(1, 2, 64, 64, dtype=torch.float16, device=gpu), z, z, z, z, z, z)
+    assert not torch.isnan(y0).any()
+    s1 = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
+    s2 = torch.zeros_like(s1)
+    y1, _ = ops.wkv_seq_fp16(B, T, C, H, s1, *[x.clone() for x in ins])
+    y2, _ = ops.wkv_seq_fp16(B, T, C, H, s2, *[x.clone() for x in ins])
+    torch.testing.assert_close(y1, y2, atol=0, rtol=0)
+    yo1, _ = ops.wkv_one_fp16(B, C, H, s1.clone(), *[x[:, 0].contiguous() for x in ins])
+    yo2, _ = ops.wkv_one_fp16(B, C, H, s1.clone(), *[x[:, 0].contiguous() for x in ins])
+    torch.testing.assert_close(yo1, yo2, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("fn", ["wkv_forward_fp32", "wkv_forward_seq_fp32", "wkv_forward_small_fp32", "wkv_forward_block_fp32"])
+def test_ref_fp32_basic_mutation_zero(gpu, fn):
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, C = 2, 8, 256
+    H = C // 64
+    state = torch.zeros(B, H, 64, 64, dtype=torch.float32, device=gpu)
+    y = getattr(ops, fn)(B, T, C, H, state, *_dev(make_wkv_inputs(B, T, H, seed=2, dist="realistic"), gpu))
+    assert y.shape == (B, T, C) and y.dtype == torch.float16 and not torch.isnan(y).any()
+    assert not torch.equal(state, torch.zeros_like(state))
+    z = torch.zeros(1, 4, 128, dtype=torch.float16, device=gpu)
+    y0 = getattr(ops, fn)(1, 4, 128, 2, torch.zeros(1, 2, 64, 64, device=gpu), z, z, z, z, z, z)
+    assert not torch.isnan(y0).any()
+
+
+def test_ref_validation_errors(gpu):
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, C, H = 1, 4, 100, 2
+    state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
+    with pytest.raises(RuntimeError):
+        ops.wkv_seq_fp16(B, T, C, H, state, *_fp16_inputs(B, T, C, gpu))
+    B, T, C, H = 1, 4, 128, 2
+    bad_state = torch.zeros(B, C, 64, dtype=torch.float16, device=gpu)
+    y = torch.empty(B, T, C, dtype=torch.float16, device=gpu)
+    with pytest.raises(RuntimeError):
+        torch.ops.vkwr_v1_wkv.wkv_forward_fp32(B, T, C, H, bad_state, *_fp16_inputs(B, T, C, gpu), y)
+    with pytest.raises(RuntimeError):  # fp32 inputs where fp16 is required
+        ins = [x.float() for x in _fp16_inputs(B, T, C, gpu)]
+        torch.ops.vkwr_v1_wkv.wkv_forward_fp32(B, T, C, H, torch.zeros(B, H, 64, 64, device=gpu), *ins, y)
+    with pytest.raises(RuntimeError):  # non-contiguous input
+        ins = _fp16_inputs(B, T, 2 * C, gpu)
+        ins = [x[:, :, ::2] for x in ins]
+        torch.ops.vkwr_v1_wkv.wkv_forward_fp32(B, T, C, H, torch.zeros(B, H, 64, 64, device=gpu), *ins, y)
+    with pytest.raises(RuntimeError):
+        ops.advance_i32(torch.zeros(4, dtype=torch.int64, device=gpu), 1)
+    with pytest.raises(RuntimeError):
+        ops.advance_i32(torch.zeros(2, 4, dtype=torch.int32, device=gpu), 1)
+
+
+def test_ref_advance_i32(gpu):
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    x = torch.zeros(4, dtype=torch.int32, device=gpu)
+    assert ops.advance_i32(x, 5) is None
+    assert (x == 5).all()
+    x = torch.zeros(2, dtype=torch.int32, device=gpu)
+    ops.advance_i32(x, 3)
+    ops.advance_i32(x, 7)
+    assert (x == 10).all()
+    x = torch.full((3,), 100, dtype=torch.int32, device=gpu)
+    ops.advance_i32(x, -10)
+    assert (x == 90).all()
+    x = torch.zeros(4, dtype=torch.int32, device=gpu)
+    ops.advance_i32(x, 2 ** 30)
+    assert (x == 2 ** 30).all()
+    x = torch.tensor([2 ** 31 - 1, -5], dtype=torch.int32, device=gpu)
+    ops.advance_i32(x, 1)
+    assert x.tolist() == [-(2 ** 31), -4]
+    big = torch.arange(100003, dtype=torch.int32, device=gpu)
+    ops.advance_i32(big, -7)
+    assert torch.equal(big, torch.arange(100003, dtype=torch.int32, device=gpu) - 7)
+
+
+def test_ref_wkv_seq_fp16_performance(gpu):
+    """Liveness bound of the reference (tests/ops/test_v1_wkv_ops.py:454-466): < 200 ms/call."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, C = 2, 64, 1024
+    H = C // 64
+    state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
+    ins = _dev(make_wkv_inputs(B, T, H, seed=3, dist="realistic"), gpu)
+    ops.wkv_seq_fp16(B, T, C, H, state.clone(), *ins)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(30):
+        ops.wkv_seq_fp16(B, T, C, H, state.clone(), *[x.clone() for x in ins])
+    torch.cuda.synchronize()
+    assert (time.perf_counter() - t0) / 30 * 1000 < 200.0

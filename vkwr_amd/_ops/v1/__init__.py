@@ -1,0 +1,2 @@
+def import_all_v1_ops():
+    from vkwr_amd._ops.v1 import v1_wkv_ops  # noqa: F401

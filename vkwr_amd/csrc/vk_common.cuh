@@ -1,0 +1,83 @@
+// Device helpers shared by the vkwr_amd HIP kernels (gfx950 / CDNA4, wave64).
+//
+// All floating-point code here is compiled with -ffp-contract=off: every fused
+// multiply-add is an explicit __builtin_fmaf / elementwise fma, so results are
+// reproducible bit for bit by any implementation that performs the same IEEE
+// operations in the same order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vk {
+
+constexpr int kHead = 64;  // RWKV-7 head size (the only one the ops accept)
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// RWKV-7 decay constants: -e^{-1/2}*log2(e) and -log2(e)
+// (reference csrc/v1/wkv/wkv_fp32_v2.cu:14-15; model math, not library constants).
+constexpr float kDecayC1 = -0.8750387749145276f;
+constexpr float kDecayC2 = -1.4426950408889634f;
+constexpr float kTwoNeg41 = 4.547473508864641e-13f;
+
+// 2^x from correctly rounded operations only: range reduction by rint, the
+// degree-7 Taylor polynomial of 2^f = e^{f ln 2} on |f| <= 1/2 in Horner form
+// with FMA, then an exact power-of-two scale.  Max relative error ~6e-8.
+// Results below 2^-126 return 0 (the decay only adds them to 1).
+__device__ __forceinline__ float exp2_det(float x) {
+  if (x != x) return x;
+  if (x >= 128.0f) return __builtin_huge_valf();
+  if (x < -126.0f) return 0.0f;
+  const float n = __builtin_rintf(x);
+  const float f = x - n;
+  float p = 1.525273380405984e-05f;
+  p = __builtin_fmaf(p, f, 1.5403530393381608e-04f);
+  p = __builtin_fmaf(p, f, 1.3333558146428443e-03f);
+  p = __builtin_fmaf(p, f, 9.618129107628477e-03f);
+  p = __builtin_fmaf(p, f, 5.550410866482158e-02f);
+  p = __builtin_fmaf(p, f, 2.402265069591007e-01f);
+  p = __builtin_fmaf(p, f, 6.931471805599453e-01f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+// Per-channel decay d = exp(-e^{-1/2} * sigmoid(w)), written in the reference's
+// exp2 form (wkv_fp32_v2.cu:27-29) with an IEEE division.
+__device__ __forceinline__ float decay(float w) {
+  const float e = exp2_det(kDecayC2 * w);
+  const float den = 1.0f + e;
+  const float q = kDecayC1 / den;
+  return exp2_det(q);
+}
+
+// Dither of the fp16-state family (wkv_fp16_v2.cu:23-25): a Knuth
+// multiplicative hash of the phase, wrapped to int32, scaled by 2^-41.
+__device__ __forceinline__ float rotator(uint32_t phase) {
+  const uint32_t m = 2654435769u * phase;
+  return kTwoNeg41 * (float)(int32_t)m;
+}
+
+// fp16 decay delta of the fp16-state family (wkv_fp16_v2.cu:27-30):
+// fp16_rn((d - 1) + rot).
+__device__ __forceinline__ _Float16 w_delta(float w, uint32_t phase) {
+  float d = decay(w) - 1.0f;
+  d = d + rotator(phase);
+  return (_Float16)d;
+}
+
+__device__ __forceinline__ float h2f(uint16_t bits) {
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// The LDS address space, for the direct global->LDS (DMA) loads of gfx950.
+#define VK_LDS __attribute__((address_space(3)))
+
+// One 16-byte-per-lane global->LDS transfer: lane L's 16 bytes at `gsrc` land
+// at `lds_base + 16*L`.  `lds_base` must be wave-uniform.
+__device__ __forceinline__ void dma16(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (VK_LDS void*)lds_base, 16, 0, 0);
+}
+
+}  // namespace vk

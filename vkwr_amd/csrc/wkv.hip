@@ -1,0 +1,392 @@
+// RWKV-7 WKV (generalised delta rule) kernels for gfx950.
+//
+// Work decomposition: one 64-lane wavefront (one workgroup) per (sequence,
+// head).  Lane i owns row i of the head's 64x64 state in VGPRs for the whole
+// call, so the two per-token dot products
+//     sa_i = sum_j S_ij a_j        y_i = sum_j S'_ij r_j
+// are lane-local FMA chains in j order, exactly the reference's per-thread
+// loop (csrc/v1/wkv/wkv_fp32_v2.cu:103-117), and need no cross-lane traffic.
+// The per-token channel vectors (r, decay, k, a, b) are produced one channel
+// per lane, staged in LDS and read back as broadcasts (uniform-address
+// ds_read_b128).
+//
+// State I/O: the row-per-lane layout would make lane i touch bytes
+// [256 i, 256 i + 256) of the head -- a 256-byte lane stride, uncoalesced.
+// Instead each lane issues 16-byte direct-to-LDS loads (global_load_lds_dwordx4)
+// whose addresses cover one contiguous 1 KiB block per instruction, placing
+// chunk q (16 bytes) of row i at LDS slot i*16 + (q ^ (i & 15)).  Row-per-lane
+// LDS reads then hit 16 distinct bank groups per 16 lanes.  The write-back is
+// the mirror image (LDS transpose, then contiguous 1 KiB global stores).
+// The fp16-state family uses the same scheme on 8 KiB (128-byte rows, 8
+// chunks per row, slot i*8 + (q ^ ((i >> 1) & 7))).
+
+#include "vk_capi.h"
+#include "vk_common.cuh"
+
+namespace vk {
+namespace {
+
+struct Fp32Args {
+  int T, C, H, n_slots;
+  float* state;
+  const int32_t* slots;
+  const _Float16 *r, *w, *k, *v, *a, *b;
+  _Float16* y;
+};
+
+template <bool kSlots>
+__global__ __launch_bounds__(64) void wkv7_fp32_kernel(Fp32Args p) {
+  __shared__ f4 st[1024];  // one head's state (16 KiB); reused for token vectors
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const size_t tok0 = (size_t)bi * p.T * p.C + (size_t)h * kHead + lane;
+
+  size_t sidx = (size_t)bi;
+  if constexpr (kSlots) {
+    const int s = p.slots[bi];
+    if (s < 0 || s >= p.n_slots) {
+      for (int t = 0; t < p.T; ++t) p.y[tok0 + (size_t)t * p.C] = (_Float16)__builtin_nanf("");
+      return;
+    }
+    sidx = (size_t)s;
+  }
+  float* S = p.state + (sidx * p.H + h) * (kHead * kHead);
+
+  // ---- state: HBM -> LDS (swizzled), one contiguous KiB per instruction
+  const int sub = lane & 15;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const int row = 4 * c + (lane >> 4);
+    const int q = sub ^ (row & 15);
+    dma16(S + row * kHead + q * 4, &st[c * 64]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  float s[kHead];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const f4 x = st[lane * 16 + (q ^ sub)];
+    s[4 * q + 0] = x.x;
+    s[4 * q + 1] = x.y;
+    s[4 * q + 2] = x.z;
+    s[4 * q + 3] = x.w;
+  }
+  __syncthreads();
+
+  // ---- token loop; token vectors double-buffered inside the staging tile
+  float* vec = reinterpret_cast<float*>(st);
+  _Float16 xr = p.r[tok0], xw = p.w[tok0], xk = p.k[tok0];
+  _Float16 xv = p.v[tok0], xa = p.a[tok0], xb = p.b[tok0];
+  for (int t = 0; t < p.T; ++t) {
+    float* vb = vec + (t & 1) * (5 * kHead);
+    vb[lane] = (float)xr;
+    vb[kHead + lane] = decay((float)xw);
+    vb[2 * kHead + lane] = (float)xk;
+    vb[3 * kHead + lane] = (float)xa;
+    vb[4 * kHead + lane] = (float)xb;
+    const float vi = (float)xv;
+    if (t + 1 < p.T) {
+      const size_t o = tok0 + (size_t)(t + 1) * p.C;
+      xr = p.r[o];
+      xw = p.w[o];
+      xk = p.k[o];
+      xv = p.v[o];
+      xa = p.a[o];
+      xb = p.b[o];
+    }
+    __syncthreads();
+    const f4* R4 = reinterpret_cast<const f4*>(vb);
+    const f4* D4 = R4 + 16;
+    const f4* K4 = R4 + 32;
+    const f4* A4 = R4 + 48;
+    const f4* B4 = R4 + 64;
+
+    float sa = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const f4 a4 = A4[q];
+      sa = __builtin_fmaf(s[4 * q + 0], a4.x, sa);
+      sa = __builtin_fmaf(s[4 * q + 1], a4.y, sa);
+      sa = __builtin_fmaf(s[4 * q + 2], a4.z, sa);
+      sa = __builtin_fmaf(s[4 * q + 3], a4.w, sa);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const f4 d4 = D4[q], b4 = B4[q], k4 = K4[q], r4 = R4[q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = s[4 * q + e] * d4[e];
+        x = __builtin_fmaf(sa, b4[e], x);
+        x = __builtin_fmaf(k4[e], vi, x);
+        s[4 * q + e] = x;
+        acc = __builtin_fmaf(x, r4[e], acc);
+      }
+    }
+    // Keep acc an fp32 value: without this the compiler may fold fma + cvt into
+    // v_fma_mixlo_f16, which rounds once instead of f32-then-f16.
+    asm volatile("" : "+v"(acc));
+    p.y[tok0 + (size_t)t * p.C] = (_Float16)acc;
+  }
+
+  // ---- state: registers -> LDS (swizzled) -> HBM, contiguous KiB per store
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    st[lane * 16 + (q ^ sub)] = f4{s[4 * q + 0], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]};
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const int row = 4 * c + (lane >> 4);
+    const int q = sub ^ (row & 15);
+    *reinterpret_cast<f4*>(S + row * kHead + q * 4) = st[c * 64 + lane];
+  }
+}
+
+struct Fp16Args {
+  int T, C, H;
+  _Float16* state;
+  const _Float16 *r, *w, *w0, *k, *v, *a, *b;
+  _Float16* y;
+  const int32_t* elapsed;
+};
+
+// fp16-state recurrence.  kLegacy = false: vkwr_v1_wkv::wkv_*_fp16 semantics
+// (wkv_fp16_v2.cu:259-291): hfma2 nesting s = fma(s, wd, fma(k, v, fma(sa, b, s))),
+// dither phase elapsed + channel + t, optional w0.  kLegacy = true:
+// vkwr_rwkv7::forward_* (state_fwd_fp16.cu:57-83): s += s*wd + k*v + sa*b with
+// separately rounded fp16 operations, dither phase elapsed + t.
+template <bool kLegacy>
+__global__ __launch_bounds__(64) void wkv7_fp16_kernel(Fp16Args p) {
+  __shared__ f4 st[512];  // one head's fp16 state (8 KiB); reused for token vectors
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const size_t tok0 = (size_t)bi * p.T * p.C + (size_t)h * kHead + lane;
+  _Float16* S = p.state + (size_t)bh * (kHead * kHead);
+
+  const int sub = lane & 7;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int row = 8 * c + (lane >> 3);
+    const int q = sub ^ ((row >> 1) & 7);
+    dma16(S + row * kHead + q * 8, &st[c * 64]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int sw = (lane >> 1) & 7;
+  h2 s[32];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const f4 x = st[lane * 8 + (q ^ sw)];
+    const h2* hx = reinterpret_cast<const h2*>(&x);
+    s[4 * q + 0] = hx[0];
+    s[4 * q + 1] = hx[1];
+    s[4 * q + 2] = hx[2];
+    s[4 * q + 3] = hx[3];
+  }
+  __syncthreads();
+
+  const uint32_t el = (uint32_t)p.elapsed[bi];
+  const uint32_t chan = (uint32_t)(h * kHead + lane);
+  float w0f = 0.0f;
+  if (!kLegacy && p.w0 != nullptr) w0f = (float)p.w0[chan];
+
+  _Float16* vec = reinterpret_cast<_Float16*>(st);
+  _Float16 xr = p.r[tok0], xw = p.w[tok0], xk = p.k[tok0];
+  _Float16 xv = p.v[tok0], xa = p.a[tok0], xb = p.b[tok0];
+  for (int t = 0; t < p.T; ++t) {
+    _Float16* vb = vec + (t & 1) * (5 * kHead);
+    float wf = (float)xw;
+    uint32_t phase;
+    if constexpr (kLegacy) {
+      phase = el + (uint32_t)t;
+    } else {
+      if (p.w0 != nullptr) wf = wf + w0f;
+      phase = el + chan + (uint32_t)t;
+    }
+    vb[lane] = xr;
+    vb[kHead + lane] = w_delta(wf, phase);
+    vb[2 * kHead + lane] = xk;
+    vb[3 * kHead + lane] = xa;
+    vb[4 * kHead + lane] = xb;
+    const _Float16 vi = xv;
+    if (t + 1 < p.T) {
+      const size_t o = tok0 + (size_t)(t + 1) * p.C;
+      xr = p.r[o];
+      xw = p.w[o];
+      xk = p.k[o];
+      xv = p.v[o];
+      xa = p.a[o];
+      xb = p.b[o];
+    }
+    __syncthreads();
+    const h2* R2 = reinterpret_cast<const h2*>(vb);
+    const h2* W2 = R2 + 32;
+    const h2* K2 = R2 + 64;
+    const h2* A2 = R2 + 96;
+    const h2* B2 = R2 + 128;
+
+    h2 sa2 = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      if constexpr (kLegacy) {
+        sa2 = sa2 + A2[m] * s[m];
+      } else {
+        sa2 = __builtin_elementwise_fma(A2[m], s[m], sa2);
+      }
+    }
+    const _Float16 sa = sa2.x + sa2.y;
+    const h2 sav = {sa, sa};
+    const h2 vv = {vi, vi};
+    h2 y2 = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      if constexpr (kLegacy) {
+        const h2 t1 = s[m] * W2[m];
+        const h2 t2 = K2[m] * vv;
+        const h2 t3 = t1 + t2;
+        const h2 t4 = sav * B2[m];
+        const h2 t5 = t3 + t4;
+        s[m] = s[m] + t5;
+        y2 = y2 + s[m] * R2[m];
+      } else {
+        const h2 in1 = __builtin_elementwise_fma(sav, B2[m], s[m]);
+        const h2 in2 = __builtin_elementwise_fma(K2[m], vv, in1);
+        s[m] = __builtin_elementwise_fma(s[m], W2[m], in2);
+        y2 = __builtin_elementwise_fma(s[m], R2[m], y2);
+      }
+    }
+    p.y[tok0 + (size_t)t * p.C] = y2.x + y2.y;
+  }
+
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    f4 x;
+    h2* hx = reinterpret_cast<h2*>(&x);
+    hx[0] = s[4 * q + 0];
+    hx[1] = s[4 * q + 1];
+    hx[2] = s[4 * q + 2];
+    hx[3] = s[4 * q + 3];
+    st[lane * 8 + (q ^ sw)] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int row = 8 * c + (lane >> 3);
+    const int q = sub ^ ((row >> 1) & 7);
+    *reinterpret_cast<f4*>(S + row * kHead + q * 8) = st[c * 64 + lane];
+  }
+}
+
+__global__ __launch_bounds__(256) void advance_i32_kernel(int32_t* x, int64_t n, int32_t amount) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = (int32_t)((uint32_t)x[i] + (uint32_t)amount);
+}
+
+int check_wkv_dims(const char* fn, int B, int T, int C, int H) {
+  VK_REQUIRE(B >= 0 && T >= 0 && H >= 0, "%s: negative size (B=%d T=%d H=%d)", fn, B, T, H);
+  VK_REQUIRE(C == H * kHead, "%s: only head size 64 is supported (C=%d H=%d)", fn, C, H);
+  VK_REQUIRE((int64_t)B * H <= 0x7fffffff, "%s: B*H too large", fn);
+  return VKWR_OK;
+}
+
+}  // namespace
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vkwr_wkv7_fp32_forward(int B, int T, int C, int H, int mode, float* state,
+                                      const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                                      const uint16_t* v, const uint16_t* a, const uint16_t* b,
+                                      uint16_t* y, void* stream) {
+  clear_error();
+  if (int e = check_wkv_dims("vkwr_wkv7_fp32_forward", B, T, C, H)) return e;
+  VK_REQUIRE(mode >= 0 && mode <= 3, "vkwr_wkv7_fp32_forward: mode must be 0..3 (got %d)", mode);
+  if (B == 0 || H == 0 || T == 0) return VKWR_OK;
+  VK_REQUIRE(state && r && w && k && v && a && b && y, "vkwr_wkv7_fp32_forward: null pointer");
+  Fp32Args p{T, C, H, B, state, nullptr,
+             reinterpret_cast<const _Float16*>(r), reinterpret_cast<const _Float16*>(w),
+             reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
+             reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
+             reinterpret_cast<_Float16*>(y)};
+  hipLaunchKernelGGL(wkv7_fp32_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  return check_launch("vkwr_wkv7_fp32_forward");
+}
+
+extern "C" int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* pool, int n_slots,
+                                            const int32_t* slots, const uint16_t* r,
+                                            const uint16_t* w, const uint16_t* k, const uint16_t* v,
+                                            const uint16_t* a, const uint16_t* b, uint16_t* y,
+                                            void* stream) {
+  clear_error();
+  if (int e = check_wkv_dims("vkwr_wkv7_fp32_forward_slots", B, T, C, H)) return e;
+  VK_REQUIRE(n_slots >= 0, "vkwr_wkv7_fp32_forward_slots: negative pool size");
+  if (B == 0 || H == 0 || T == 0) return VKWR_OK;
+  VK_REQUIRE(pool && slots && r && w && k && v && a && b && y,
+             "vkwr_wkv7_fp32_forward_slots: null pointer");
+  Fp32Args p{T, C, H, n_slots, pool, slots,
+             reinterpret_cast<const _Float16*>(r), reinterpret_cast<const _Float16*>(w),
+             reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
+             reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
+             reinterpret_cast<_Float16*>(y)};
+  hipLaunchKernelGGL(wkv7_fp32_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  return check_launch("vkwr_wkv7_fp32_forward_slots");
+}
+
+static int launch_fp16(const char* fn, bool legacy, int B, int T, int C, int H, uint16_t* state,
+                       const uint16_t* r, const uint16_t* w, const uint16_t* w0, const uint16_t* k,
+                       const uint16_t* v, const uint16_t* a, const uint16_t* b, uint16_t* y,
+                       const int32_t* elapsed_t, void* stream) {
+  clear_error();
+  if (int e = check_wkv_dims(fn, B, T, C, H)) return e;
+  if (B == 0 || H == 0 || T == 0) return VKWR_OK;
+  VK_REQUIRE(state && r && w && k && v && a && b && y && elapsed_t, "%s: null pointer", fn);
+  Fp16Args p{T, C, H, reinterpret_cast<_Float16*>(state),
+             reinterpret_cast<const _Float16*>(r), reinterpret_cast<const _Float16*>(w),
+             reinterpret_cast<const _Float16*>(w0), reinterpret_cast<const _Float16*>(k),
+             reinterpret_cast<const _Float16*>(v), reinterpret_cast<const _Float16*>(a),
+             reinterpret_cast<const _Float16*>(b), reinterpret_cast<_Float16*>(y), elapsed_t};
+  if (legacy) {
+    hipLaunchKernelGGL(wkv7_fp16_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  } else {
+    hipLaunchKernelGGL(wkv7_fp16_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  }
+  return check_launch(fn);
+}
+
+extern "C" int vkwr_wkv7_fp16_forward(int B, int T, int C, int H, uint16_t* state,
+                                      const uint16_t* r, const uint16_t* w, const uint16_t* w0,
+                                      const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                      const uint16_t* b, uint16_t* y, const int32_t* elapsed_t,
+                                      void* stream) {
+  return launch_fp16("vkwr_wkv7_fp16_forward", false, B, T, C, H, state, r, w, w0, k, v, a, b, y,
+                     elapsed_t, stream);
+}
+
+extern "C" int vkwr_rwkv7_forward(int B, int T, int C, int H, uint16_t* state, const uint16_t* r,
+                                  const uint16_t* w, const uint16_t* k, const uint16_t* v,
+                                  const uint16_t* a, const uint16_t* b, uint16_t* y,
+                                  const int32_t* elapsed_t, void* stream) {
+  return launch_fp16("vkwr_rwkv7_forward", true, B, T, C, H, state, r, w, nullptr, k, v, a, b, y,
+                     elapsed_t, stream);
+}
+
+extern "C" int vkwr_advance_i32(int32_t* x, int64_t n, int32_t amount, void* stream) {
+  clear_error();
+  VK_REQUIRE(n >= 0, "vkwr_advance_i32: negative length");
+  if (n == 0) return VKWR_OK;
+  VK_REQUIRE(x != nullptr, "vkwr_advance_i32: null pointer");
+  const int64_t blocks = (n + 255) / 256;
+  VK_REQUIRE(blocks <= 0x7fffffff, "vkwr_advance_i32: too many elements");
+  hipLaunchKernelGGL(advance_i32_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     x, n, amount);
+  return check_launch("vkwr_advance_i32");
+}
