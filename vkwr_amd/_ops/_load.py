@@ -8,6 +8,6 @@ def load_ext(name):
     except ImportError as e:  # pragma: no cover - exercised only on a broken install
         raise ImportError(
             f"vkwr_amd native extension '{name}' is not built or cannot be loaded ({e}). "
-            "Build it with `python -m vkwr_amd._build` (gfx950 HIP kernels); "
+            "Build it with `python vkwr_amd/_build.py` (gfx950 HIP kernels); "
             "there is no CPU fallback."
         ) from e
