@@ -31,7 +31,8 @@ HBM_PEAK_GBS = 8000.0
 # Algorithmic bytes per step: fp32 state read + write, 6 fp16 inputs, fp16 y, int32 slots.
 STATE_BYTES = B_ACTIVE * H * HEAD * HEAD * 4
 STEP_BYTES = 2 * STATE_BYTES + 6 * B_ACTIVE * C * 2 + B_ACTIVE * C * 2 + B_ACTIVE * 4
-PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "wkv7_fp32_slots_decode_c1.md")
+COLD_SLOTS = 2048  # cold-cache variant: 1 GiB pool
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "wkv7_fp32_step_kernel_decode_c1.md")
 
 
 def parse_args():
@@ -41,6 +42,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target length of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every step directly instead of replaying a HIP graph (for counter runs); "
+                         "skips the cache variants")
     return ap.parse_args()
 
 
@@ -73,6 +77,18 @@ def read_traffic():
     except OSError:
         pass
     return None
+
+
+def copy_calibration(dev, n_bytes=256 << 20, reps=3):
+    """A plain device copy of known size (torch's copy kernel), run before the timed
+    region so that a counter run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) sees a
+    reference dispatch that moves exactly n_bytes each way."""
+    src = torch.empty(n_bytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def capture(step_fn, n_steps, stream):
@@ -142,41 +158,77 @@ def main():
         x = inputs[i]
         op(B_ACTIVE, 1, C, H, pool, sl, x[0], x[1], x[2], x[3], x[4], x[5], y)
 
+    copy_calibration(dev)
     for i in range(W):
         step(K + i)
     torch.cuda.synchronize()
 
     stream = torch.cuda.Stream()
-    graph = capture(step, K, stream)
-    graph.replay()  # one untimed replay (first replay uploads the graph)
-    torch.cuda.synchronize()
-
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-        graph.replay()
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = ev0.elapsed_time(ev1)
-    ms_per_step = gpu_ms / K
-    gbs = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
+    variants = {}
+    if args.eager:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            for i in range(K):
+                step(i)
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_per_step = ev0.elapsed_time(ev1) / K
+    else:
+        graph = capture(step, K, stream)
+        graph.replay()  # one untimed replay (first replay uploads the graph)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            graph.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_per_step = ev0.elapsed_time(ev1) / K
+        del graph
 
-    # Cold(er)-cache variant: rotate 4 disjoint 128-slot sets (the whole 256 MiB pool).
-    sets = [perm[i * B_ACTIVE:(i + 1) * B_ACTIVE].to(torch.int32).to(dev) for i in range(4)]
-    kc = min(K, 400)
-    graph_c = capture(lambda i: step(i, sets[i % 4]), kc, stream)
-    graph_c.replay()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-        graph_c.replay()
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    cold_ms = ev0.elapsed_time(ev1) / kc
-    del graph, graph_c
+        def timed_graph(fn, n):
+            g = capture(fn, n, stream)
+            g.replay()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                ev0.record(stream)
+                g.replay()
+                ev1.record(stream)
+            torch.cuda.synchronize()
+            return ev0.elapsed_time(ev1) / n
+
+        # (1) 4 disjoint 128-slot sets of the same 512-slot pool cycled (256 MiB touched).
+        sets = [perm[i * B_ACTIVE:(i + 1) * B_ACTIVE].to(torch.int32).to(dev) for i in range(4)]
+        kc = min(K, 400)
+        ms_rot = timed_graph(lambda i: step(i, sets[i % 4]), kc)
+        variants["rotating_4_slot_sets"] = {
+            "ms_per_step": round(ms_rot, 5), "GB/s": round(STEP_BYTES / (ms_rot * 1e-3) / 1e9, 2),
+            "note": "4 disjoint 128-slot sets of the 512-slot pool cycled (256 MiB touched)"}
+        # (2) cold: a 2048-slot pool (1 GiB, 4x the 256 MB Infinity Cache), 16 disjoint sets cycled.
+        del sets
+        big = torch.empty(COLD_SLOTS, H, HEAD, HEAD, dtype=torch.float32, device=dev).normal_(0.0, 0.1)
+        bperm = torch.randperm(COLD_SLOTS, generator=gen)
+        bsets = [bperm[i * B_ACTIVE:(i + 1) * B_ACTIVE].to(torch.int32).to(dev)
+                 for i in range(COLD_SLOTS // B_ACTIVE)]
+
+        def cold_step(i):
+            x = inputs[i]
+            op(B_ACTIVE, 1, C, H, big, bsets[i % len(bsets)], x[0], x[1], x[2], x[3], x[4], x[5], y)
+
+        ms_cold = timed_graph(cold_step, kc)
+        variants["cold_1GiB_pool"] = {
+            "ms_per_step": round(ms_cold, 5), "GB/s": round(STEP_BYTES / (ms_cold * 1e-3) / 1e9, 2),
+            "frac_of_peak": round(STEP_BYTES / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": f"{COLD_SLOTS}-slot pool (1 GiB), {len(bsets)} disjoint 128-slot sets cycled: "
+                    "every step's state comes from HBM, not the Infinity Cache"}
+        del big
+    variants["wall_s_timed_region"] = round(wall, 4)
+    gbs = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
 
     traffic = read_traffic()
     result = {
@@ -194,17 +246,12 @@ def main():
         "data": "synthetic (seeded; BASELINE config 0/1 distributions, resident in HBM)",
         "config": {"workload": "wkv7_decode_slot_pool (BASELINE config 1)", "pool_slots": P_SLOTS,
                    "active_seqs": B_ACTIVE, "heads": H, "head_size": HEAD, "T": 1,
-                   "state": "fp32", "io": "fp16", "timing": "HIP graph of K steps, HIP events"},
+                   "state": "fp32", "io": "fp16", "timing": ("eager launches" if args.eager else "HIP graph of K steps") + ", HIP events on the launch stream"},
         "tokens_per_s": round(B_ACTIVE / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": STEP_BYTES},
-        "variants": {
-            "rotating_4_slot_sets": {"ms_per_step": round(cold_ms, 5),
-                                     "GB/s": round(STEP_BYTES / (cold_ms * 1e-3) / 1e9, 2),
-                                     "note": "4 disjoint 128-slot sets cycled: 256 MiB working set"},
-            "wall_s_timed_region": round(wall, 4),
-        },
+        "variants": variants,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

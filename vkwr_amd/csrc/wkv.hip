@@ -13,11 +13,17 @@
 // State I/O: the row-per-lane layout would make lane i touch bytes
 // [256 i, 256 i + 256) of the head -- a 256-byte lane stride, uncoalesced.
 // Instead each lane issues 16-byte direct-to-LDS loads (global_load_lds_dwordx4)
-// whose addresses cover one contiguous 1 KiB block per instruction, placing
-// chunk q (16 bytes) of row i at LDS slot i*16 + (q ^ (i & 15)).  Row-per-lane
-// LDS reads then hit 16 distinct bank groups per 16 lanes.  The write-back is
-// the mirror image (LDS transpose, then contiguous 1 KiB global stores).
-// The fp16-state family uses the same scheme on 8 KiB (128-byte rows, 8
+// whose addresses cover whole 128-byte lines.  The fp32 state (16 KiB per head)
+// goes through an 8 KiB LDS tile in two phases, one column half (128 bytes of
+// every row) per phase: chunk q (16 bytes) of row i's half lands at LDS slot
+// i*8 + (q ^ (i & 7)), so the row-per-lane reads that follow hit 8 distinct
+// 16-byte bank groups per 8 lanes.  The write-back is the mirror image (LDS
+// transpose, then 128-byte-line global stores), again one half at a time.
+// Halving the tile from 16 to 8 KiB doubles the waves an MI355X CU can hold
+// (160 KiB LDS): a 128-sequence x 32-head decode step (4096 waves) is then
+// resident in one round instead of 1.6, which measured 21.9 us against
+// 26.1 us per step for a single 16 KiB phase.
+// The fp16-state family stages its 8 KiB head in one phase (128-byte rows, 8
 // chunks per row, slot i*8 + (q ^ ((i >> 1) & 7))).
 
 #include "vk_capi.h"
@@ -34,60 +40,159 @@ struct Fp32Args {
   _Float16* y;
 };
 
+// ---- fp32 state staging: HBM <-> LDS (swizzled) <-> VGPRs, one column half
+// per phase (see the State I/O note above).  `st` is the 8 KiB tile.
+__device__ __forceinline__ void load_state_fp32(const float* S, f4* st, float* s, int lane) {
+  const int sub = lane & 7;
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int row = 8 * c + (lane >> 3);
+      dma16(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4, &st[c * 64]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const f4 x = st[lane * 8 + (q ^ sub)];
+      const int j = ph * 32 + 4 * q;
+      s[j + 0] = x.x;
+      s[j + 1] = x.y;
+      s[j + 2] = x.z;
+      s[j + 3] = x.w;
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ void store_state_fp32(float* S, f4* st, const float* s, int lane) {
+  const int sub = lane & 7;
+  __syncthreads();
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int j = ph * 32 + 4 * q;
+      st[lane * 8 + (q ^ sub)] = f4{s[j + 0], s[j + 1], s[j + 2], s[j + 3]};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int row = 8 * c + (lane >> 3);
+      *reinterpret_cast<f4*>(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4) = st[c * 64 + lane];
+    }
+    __syncthreads();
+  }
+}
+
+// One token of the fp32-state recurrence for row `lane` (state row in s[]).
+// vb: 5*64 floats of LDS for the token's channel vectors (r, decay, k, a, b),
+// written here one channel per lane and read back as broadcasts.
+__device__ __forceinline__ _Float16 token_fp32(float* s, float* vb, int lane, _Float16 xr,
+                                               _Float16 xw, _Float16 xk, _Float16 xv,
+                                               _Float16 xa, _Float16 xb) {
+  vb[lane] = (float)xr;
+  vb[kHead + lane] = decay((float)xw);
+  vb[2 * kHead + lane] = (float)xk;
+  vb[3 * kHead + lane] = (float)xa;
+  vb[4 * kHead + lane] = (float)xb;
+  const float vi = (float)xv;
+  __syncthreads();
+  const f4* R4 = reinterpret_cast<const f4*>(vb);
+  const f4* D4 = R4 + 16;
+  const f4* K4 = R4 + 32;
+  const f4* A4 = R4 + 48;
+  const f4* B4 = R4 + 64;
+
+  float sa = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const f4 a4 = A4[q];
+    sa = __builtin_fmaf(s[4 * q + 0], a4.x, sa);
+    sa = __builtin_fmaf(s[4 * q + 1], a4.y, sa);
+    sa = __builtin_fmaf(s[4 * q + 2], a4.z, sa);
+    sa = __builtin_fmaf(s[4 * q + 3], a4.w, sa);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const f4 d4 = D4[q], b4 = B4[q], k4 = K4[q], r4 = R4[q];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = s[4 * q + e] * d4[e];
+      x = __builtin_fmaf(sa, b4[e], x);
+      x = __builtin_fmaf(k4[e], vi, x);
+      s[4 * q + e] = x;
+      acc = __builtin_fmaf(x, r4[e], acc);
+    }
+  }
+  // Keep acc an fp32 value: without this the compiler may fold fma + cvt into
+  // v_fma_mixlo_f16, which rounds once instead of f32-then-f16.
+  asm volatile("" : "+v"(acc));
+  return (_Float16)acc;
+}
+
+// Resolves the state block of (sequence bi, head h); with slots, an entry
+// outside [0, n_slots) yields nullptr (the caller writes NaN rows, skips the pool).
 template <bool kSlots>
-__global__ __launch_bounds__(64) void wkv7_fp32_kernel(Fp32Args p) {
-  __shared__ f4 st[1024];  // one head's state (16 KiB); reused for token vectors
+__device__ __forceinline__ float* state_block(const Fp32Args& p, int bi, int h) {
+  size_t sidx = (size_t)bi;
+  if constexpr (kSlots) {
+    const int sl = p.slots[bi];
+    if (sl < 0 || sl >= p.n_slots) return nullptr;
+    sidx = (size_t)sl;
+  }
+  return p.state + (sidx * p.H + h) * (kHead * kHead);
+}
+
+// Decode step (T == 1).  At most 128 VGPRs (4 waves per SIMD, 16 per CU):
+// with the 8 KiB LDS tile a 4096-wave step then fits on the 256 CUs in one
+// round.  The token's inputs are loaded before the state so that their
+// latency overlaps the state transfer.
+template <bool kSlots>
+__global__ __launch_bounds__(64, 4) void wkv7_fp32_step_kernel(Fp32Args p) {
+  __shared__ f4 st[512];
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const size_t tok = (size_t)bi * p.C + (size_t)h * kHead + lane;
+  const _Float16 xr = p.r[tok], xw = p.w[tok], xk = p.k[tok];
+  const _Float16 xv = p.v[tok], xa = p.a[tok], xb = p.b[tok];
+  float* S = state_block<kSlots>(p, bi, h);
+  if (S == nullptr) {
+    p.y[tok] = (_Float16)__builtin_nanf("");
+    return;
+  }
+  float s[kHead];
+  load_state_fp32(S, st, s, lane);
+  p.y[tok] = token_fp32(s, reinterpret_cast<float*>(st), lane, xr, xw, xk, xv, xa, xb);
+  store_state_fp32(S, st, s, lane);
+}
+
+// T tokens; the next token's inputs are loaded while the current one computes,
+// and the token vectors are double-buffered inside the staging tile.
+template <bool kSlots>
+__global__ __launch_bounds__(64) void wkv7_fp32_seq_kernel(Fp32Args p) {
+  __shared__ f4 st[512];
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int bi = bh / p.H;
   const int h = bh - bi * p.H;
   const size_t tok0 = (size_t)bi * p.T * p.C + (size_t)h * kHead + lane;
-
-  size_t sidx = (size_t)bi;
-  if constexpr (kSlots) {
-    const int s = p.slots[bi];
-    if (s < 0 || s >= p.n_slots) {
-      for (int t = 0; t < p.T; ++t) p.y[tok0 + (size_t)t * p.C] = (_Float16)__builtin_nanf("");
-      return;
-    }
-    sidx = (size_t)s;
+  float* S = state_block<kSlots>(p, bi, h);
+  if (S == nullptr) {
+    for (int t = 0; t < p.T; ++t) p.y[tok0 + (size_t)t * p.C] = (_Float16)__builtin_nanf("");
+    return;
   }
-  float* S = p.state + (sidx * p.H + h) * (kHead * kHead);
-
-  // ---- state: HBM -> LDS (swizzled), one contiguous KiB per instruction
-  const int sub = lane & 15;
-#pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    const int row = 4 * c + (lane >> 4);
-    const int q = sub ^ (row & 15);
-    dma16(S + row * kHead + q * 4, &st[c * 64]);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  float s[kHead];
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const f4 x = st[lane * 16 + (q ^ sub)];
-    s[4 * q + 0] = x.x;
-    s[4 * q + 1] = x.y;
-    s[4 * q + 2] = x.z;
-    s[4 * q + 3] = x.w;
-  }
-  __syncthreads();
-
-  // ---- token loop; token vectors double-buffered inside the staging tile
-  float* vec = reinterpret_cast<float*>(st);
   _Float16 xr = p.r[tok0], xw = p.w[tok0], xk = p.k[tok0];
   _Float16 xv = p.v[tok0], xa = p.a[tok0], xb = p.b[tok0];
+  float s[kHead];
+  load_state_fp32(S, st, s, lane);
+  float* vec = reinterpret_cast<float*>(st);
   for (int t = 0; t < p.T; ++t) {
-    float* vb = vec + (t & 1) * (5 * kHead);
-    vb[lane] = (float)xr;
-    vb[kHead + lane] = decay((float)xw);
-    vb[2 * kHead + lane] = (float)xk;
-    vb[3 * kHead + lane] = (float)xa;
-    vb[4 * kHead + lane] = (float)xb;
-    const float vi = (float)xv;
+    const _Float16 cr = xr, cw = xw, ck = xk, cv = xv, ca = xa, cb = xb;
     if (t + 1 < p.T) {
       const size_t o = tok0 + (size_t)(t + 1) * p.C;
       xr = p.r[o];
@@ -97,53 +202,18 @@ __global__ __launch_bounds__(64) void wkv7_fp32_kernel(Fp32Args p) {
       xa = p.a[o];
       xb = p.b[o];
     }
-    __syncthreads();
-    const f4* R4 = reinterpret_cast<const f4*>(vb);
-    const f4* D4 = R4 + 16;
-    const f4* K4 = R4 + 32;
-    const f4* A4 = R4 + 48;
-    const f4* B4 = R4 + 64;
-
-    float sa = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const f4 a4 = A4[q];
-      sa = __builtin_fmaf(s[4 * q + 0], a4.x, sa);
-      sa = __builtin_fmaf(s[4 * q + 1], a4.y, sa);
-      sa = __builtin_fmaf(s[4 * q + 2], a4.z, sa);
-      sa = __builtin_fmaf(s[4 * q + 3], a4.w, sa);
-    }
-    float acc = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const f4 d4 = D4[q], b4 = B4[q], k4 = K4[q], r4 = R4[q];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = s[4 * q + e] * d4[e];
-        x = __builtin_fmaf(sa, b4[e], x);
-        x = __builtin_fmaf(k4[e], vi, x);
-        s[4 * q + e] = x;
-        acc = __builtin_fmaf(x, r4[e], acc);
-      }
-    }
-    // Keep acc an fp32 value: without this the compiler may fold fma + cvt into
-    // v_fma_mixlo_f16, which rounds once instead of f32-then-f16.
-    asm volatile("" : "+v"(acc));
-    p.y[tok0 + (size_t)t * p.C] = (_Float16)acc;
+    p.y[tok0 + (size_t)t * p.C] =
+        token_fp32(s, vec + (t & 1) * (5 * kHead), lane, cr, cw, ck, cv, ca, cb);
   }
+  store_state_fp32(S, st, s, lane);
+}
 
-  // ---- state: registers -> LDS (swizzled) -> HBM, contiguous KiB per store
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    st[lane * 16 + (q ^ sub)] = f4{s[4 * q + 0], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]};
-  }
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    const int row = 4 * c + (lane >> 4);
-    const int q = sub ^ (row & 15);
-    *reinterpret_cast<f4*>(S + row * kHead + q * 4) = st[c * 64 + lane];
+template <bool kSlots>
+void launch_fp32(const Fp32Args& p, int B, hipStream_t stream) {
+  if (p.T == 1) {
+    hipLaunchKernelGGL(wkv7_fp32_step_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(wkv7_fp32_seq_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   }
 }
 
@@ -317,7 +387,7 @@ extern "C" int vkwr_wkv7_fp32_forward(int B, int T, int C, int H, int mode, floa
              reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
              reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
              reinterpret_cast<_Float16*>(y)};
-  hipLaunchKernelGGL(wkv7_fp32_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  launch_fp32<false>(p, B, (hipStream_t)stream);
   return check_launch("vkwr_wkv7_fp32_forward");
 }
 
@@ -337,7 +407,7 @@ extern "C" int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* p
              reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
              reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
              reinterpret_cast<_Float16*>(y)};
-  hipLaunchKernelGGL(wkv7_fp32_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  launch_fp32<true>(p, B, (hipStream_t)stream);
   return check_launch("vkwr_wkv7_fp32_forward_slots");
 }
 
