@@ -99,6 +99,133 @@ VKWR_EXPORT int vkwr_rwkv7_forward(int B, int T, int C, int H, uint16_t* state, 
  * vkwr_v1_wkv::advance_i32 (csrc/v1/wkv/torch_bindings.cpp:224-228). */
 VKWR_EXPORT int vkwr_advance_i32(int32_t* x, int64_t n, int32_t amount, void* stream);
 
+/* ------------------------------------------------------------- LayerNorm */
+
+/* Row LayerNorm, fp16 in/out, fp32 statistics (two passes over the row held
+ * in registers), y = (v - mean) * rstd * weight + bias with
+ * rstd = 1/sqrt(var + eps), var the biased variance.
+ *   x, y [rows, C]; residual NULL or [rows, C]: v = x + residual (fp32), and
+ *   then x_out (if not NULL) receives fp16(v); the statistics use the fp32 v.
+ *   0 < C <= 8192.
+ * Replaces layer_norm_f16_cuda / _small_cuda / _small512_cuda and
+ * add_layer_norm_f16_cuda (csrc/v1/norm/norm_ops.cu:878-954, 975-1012), reached
+ * from vkwr_v1_norm::layer_norm_f16{,_small,_small512}, add_layer_norm_f16
+ * (csrc/v1/norm/torch_bindings.cpp:8-40, 64-77). */
+VKWR_EXPORT int vkwr_layer_norm_f16(int64_t rows, int C, const uint16_t* x,
+                                    const uint16_t* residual, const uint16_t* weight,
+                                    const uint16_t* bias, float eps, uint16_t* x_out,
+                                    uint16_t* y, void* stream);
+
+/* LayerNorm of the last token of each sequence: y[b] = LN(x[b,T-1] + residual[b,T-1]).
+ *   x, residual [B,T,C]; y [B,C].
+ * Replaces add_last_layer_norm_f16_cuda (csrc/v1/norm/norm_ops.cu:1014-1043),
+ * reached from vkwr_v1_norm::add_last_layer_norm_f16 (torch_bindings.cpp:79-91). */
+VKWR_EXPORT int vkwr_add_last_layer_norm_f16(int B, int T, int C, const uint16_t* x,
+                                             const uint16_t* residual, const uint16_t* weight,
+                                             const uint16_t* bias, float eps, uint16_t* y,
+                                             void* stream);
+
+/* LayerNorm of a bf16 embedding table into fp16: out [V,C] = LN(emb [V,C]) with
+ * bf16 weight/bias.
+ * Replaces emb_ln0_bf16_to_f16_cuda (csrc/v1/norm/norm_ops.cu:956-973), reached
+ * from vkwr_v1_norm::emb_ln0_bf16_to_f16 (torch_bindings.cpp:42-52). */
+VKWR_EXPORT int vkwr_emb_ln0_bf16_to_f16(int64_t V, int C, const uint16_t* emb,
+                                         const uint16_t* weight, const uint16_t* bias,
+                                         float eps, uint16_t* out, void* stream);
+
+/* Decode-step fused residual add + LayerNorm + token-shift lerp (T = 1).
+ *   x, residual [rows, C]; shift_state [rows, C] (in place); n_mix = 1 or 6
+ *   mix vectors mix[i] [C]; outputs x_out [rows, C] = fp16(x + residual) and
+ *   out[i] [rows, C] = fp16(y + (prev - y) * mix[i]), where y = fp16(LN(x + residual))
+ *   and prev = shift_state at entry; then shift_state = y.
+ * Replaces add_layer_norm_cmix_mix_f16{,_cfg,_scalar_stats}_cuda and
+ * add_layer_norm_tmix_mix6_f16{,_cfg,_scalar_stats}_cuda
+ * (csrc/v1/norm/norm_ops.cu:1045-1340), reached from the vkwr_v1_norm ops of the
+ * same names (torch_bindings.cpp:93-229). */
+VKWR_EXPORT int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* x,
+                                            const uint16_t* residual, uint16_t* shift_state,
+                                            const uint16_t* weight, const uint16_t* bias,
+                                            int n_mix, const uint16_t* const* mix, float eps,
+                                            uint16_t* x_out, uint16_t* const* out, void* stream);
+
+/* out = x + y elementwise (fp32 add, fp16 round), n elements.
+ * Replaces add_f16_cuda (csrc/v1/norm/norm_ops.cu:866-876), reached from
+ * vkwr_v1_norm::add_f16 (torch_bindings.cpp:54-62). */
+VKWR_EXPORT int vkwr_add_f16(int64_t n, const uint16_t* x, const uint16_t* y, uint16_t* out,
+                             void* stream);
+
+/* ----------------------------------------------------------- token shift */
+
+/* Token-shift lerp over T tokens: for each output i,
+ * out[i][b,t,c] = fp16(x + (prev - x) * mix[i][c]) where prev is shift_state[b]
+ * at t = 0 (its value at entry) and x[b,t-1] after; then shift_state[b] = x[b,T-1].
+ *   x [B,T,C]; shift_state [B,C] (in place); n_mix = 1 or 6 vectors mix[i] [C];
+ *   out[i] [B,T,C].  half_math = 1 evaluates the lerp in fp16 (subtract, then
+ *   fused multiply-add), as the reference's half_math option does.
+ * Replaces tmix_mix6{,_cfg,_t1_c4096}_cuda and cmix_mix{,_cfg}_cuda
+ * (csrc/v1/mix/mix_ops.cu:867-1013, 1280-1324), reached from vkwr_v1_mix::
+ * tmix_mix6{,_cfg,_t1_c4096} and cmix_mix{,_cfg} (mix/torch_bindings.cpp:8-74,
+ * 246-276).  Unlike the reference (which reads shift_state at t = 0 and writes
+ * it at t = T-1 from different threads), prev at t = 0 is always the entry value. */
+VKWR_EXPORT int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
+                                         uint16_t* shift_state, int n_mix,
+                                         const uint16_t* const* mix, uint16_t* const* out,
+                                         int half_math, void* stream);
+
+/* Per-head key normalisation and in-context learning-rate gate of RWKV-7 time mix:
+ *   u = k * k_k; kk = u / max(||u||_2 over the head, 1e-12); a = sigmoid(a0 + a12);
+ *   new_k = k * (a * k_a + (1 - k_a)); neg_kk = -kk; kka = kk * a.
+ *   k, a12, new_k, neg_kk, kka [B,T,C]; k_k, a0, k_a [C]; C = 64 H.
+ *   If shift_state is not NULL (T must be 1): shift_state [B,C] = x [B,1,C].
+ * Replaces tmix_kk_a_gate_cuda (csrc/v1/mix/mix_ops.cu:1015-1049), reached from
+ * vkwr_v1_mix::tmix_kk_a_gate{,_update_shift} (mix/torch_bindings.cpp:76-115). */
+VKWR_EXPORT int vkwr_tmix_kk_a_gate_f16(int B, int T, int C, int H, const uint16_t* k,
+                                        const uint16_t* k_k, const uint16_t* a0,
+                                        const uint16_t* a12, const uint16_t* k_a,
+                                        const uint16_t* x, uint16_t* shift_state,
+                                        uint16_t* new_k, uint16_t* neg_kk, uint16_t* kka,
+                                        void* stream);
+
+/* Per-head GroupNorm of the WKV output plus the r.k bonus and the output gate:
+ *   out = ((x - mean_h) * rstd_h * weight + bias + (sum_h r*k*r_k) * v) * g,
+ *   statistics over the 64 channels of each head, eps = 64e-5.
+ *   x, r, k, v, g, out [B,T,C]; r_k, weight, bias [C]; C = 64 H.
+ * Replaces tmix_lnx_rkvres_xg_cuda (csrc/v1/mix/mix_ops.cu:1051-1083), reached
+ * from vkwr_v1_mix::tmix_lnx_rkvres_xg (mix/torch_bindings.cpp:117-135). */
+VKWR_EXPORT int vkwr_tmix_groupnorm_bonus_gate_f16(int B, int T, int C, int H,
+                                                   const uint16_t* x, const uint16_t* r,
+                                                   const uint16_t* k, const uint16_t* v,
+                                                   const uint16_t* r_k, const uint16_t* weight,
+                                                   const uint16_t* bias, const uint16_t* g,
+                                                   uint16_t* out, void* stream);
+
+/* Value-residual gate: out = v + (v_first - v) * sigmoid(v0 + v12).
+ *   v, v_first, v12, out [rows, C]; v0 [C].
+ * Replaces tmix_vres_gate_cuda (csrc/v1/mix/mix_ops.cu:1085-1104), reached from
+ * vkwr_v1_mix::tmix_vres_gate (mix/torch_bindings.cpp:137-147). */
+VKWR_EXPORT int vkwr_tmix_vres_gate_f16(int64_t rows, int C, const uint16_t* v,
+                                        const uint16_t* v_first, const uint16_t* v0,
+                                        const uint16_t* v12, uint16_t* out, void* stream);
+
+enum {
+  VKWR_ACT_RELU_SQUARE = 0, /* max(x, 0)^2 */
+  VKWR_ACT_TANH = 1,
+  VKWR_ACT_SIGMOID = 2
+};
+
+/* out = act(x) elementwise, n elements, fp32 math.
+ * Replaces relu_square_cuda / act_tanh_cuda / act_sigmoid_cuda
+ * (csrc/v1/mix/mix_ops.cu:1326-1363), reached from vkwr_v1_mix::relu_square,
+ * act_tanh, act_sigmoid (mix/torch_bindings.cpp:278-300). */
+VKWR_EXPORT int vkwr_activation_f16(int act, int64_t n, const uint16_t* x, uint16_t* out,
+                                    void* stream);
+
+/* out[i] = x[i] + vec[i mod C], n elements (n a multiple of C).
+ * Replaces add_vec_cuda (csrc/v1/mix/mix_ops.cu:1365-1378), reached from
+ * vkwr_v1_mix::add_vec (mix/torch_bindings.cpp:302-309). */
+VKWR_EXPORT int vkwr_add_vec_f16(int64_t n, int C, const uint16_t* x, const uint16_t* vec,
+                                 uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

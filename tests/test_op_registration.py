@@ -3,7 +3,10 @@ namespaces with byte-identical schemas (reference csrc/v1/wkv/torch_bindings.cpp
 231-258, csrc/rwkv7/torch_bindings.cpp:36-50), the Python wrappers keep the
 reference's names and signatures (vkwr/_ops/v1/v1_wkv_ops.py, vkwr/_ops/rwkv7_ops.py),
 and CPU tensors are refused by the dispatcher as in the reference (CUDA-only impls)."""
+import importlib
 import inspect
+import json
+import os
 
 import pytest
 import torch
@@ -11,6 +14,14 @@ import torch
 import vkwr_amd  # noqa: F401
 from vkwr_amd._ops import rwkv7_ops
 from vkwr_amd._ops.v1 import v1_wkv_ops
+
+# Reference interface data for the other namespaces (see tests/golden/README.md).
+_IFACE = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "ref_interface.json")))
+# Namespaces (and their wrapper modules) this build registers.
+BUILT = {"vkwr_v1_norm": "v1_norm_ops", "vkwr_v1_mix": "v1_mix_ops"}
+# Ops of a built namespace that are not registered yet (skipped, not passed).
+PENDING = {"cmix_sparse_one", "cmix_sparse_rows", "cmix_sparse_down_one", "cmix_sparse_down_rows",
+           "cmix_sparse_down_relu_one", "cmix_sparse_down_relu_rows", "cmix_sparse_down_relu_rows_t512"}
 
 # The reference's schema strings (the interface itself, kept identical on purpose).
 REF_SCHEMAS = {
@@ -37,11 +48,16 @@ def _cases():
     for ns, schemas in REF_SCHEMAS.items():
         for s in schemas:
             yield ns, s
+    for ns in BUILT:
+        for s in _IFACE["schemas"][ns]:
+            yield ns, s
 
 
 @pytest.mark.parametrize("ns,schema", list(_cases()))
 def test_schema_identical(ns, schema):
     name = schema.split("(", 1)[0]
+    if name in PENDING:
+        pytest.skip(f"{ns}::{name} not built yet")
     op = getattr(getattr(torch.ops, ns), name).default
     want = torch._C.parse_schema(f"{ns}::{schema}")
     assert str(op._schema) == str(want)
@@ -72,6 +88,30 @@ def test_wrapper_signature(mod, name):
     params = ", ".join(inspect.signature(getattr(mod, name)).parameters)
     assert params == REF_WRAPPERS[mod][name]
     assert v1_wkv_ops.HEAD_SIZE == 64 and rwkv7_ops.HEAD_SIZE == 64
+
+
+def _iface_wrappers():
+    for ns, modname in BUILT.items():
+        for name, params in _IFACE["wrappers"][modname].items():
+            if name != "_":  # fake-registration functions
+                yield modname, name, params
+
+
+@pytest.mark.parametrize("modname,name,params", list(_iface_wrappers()))
+def test_wrapper_signature_iface(modname, name, params):
+    if name in PENDING:
+        pytest.skip(f"{name} not built yet")
+    mod = importlib.import_module(f"vkwr_amd._ops.v1.{modname}")
+    assert ", ".join(inspect.signature(getattr(mod, name)).parameters) == params
+
+
+def test_no_extra_ops_in_built_namespaces():
+    """Every op registered in a rebuilt reference namespace is one of the reference's."""
+    for ns in BUILT:
+        ref = {s.split("(", 1)[0] for s in _IFACE["schemas"][ns]}
+        mine = {n.split("::", 1)[1].split(".", 1)[0] for n in torch._C._dispatch_get_all_op_names()
+                if n.startswith(ns + "::")}
+        assert mine <= ref, sorted(mine - ref)
 
 
 def test_cpu_tensors_rejected_by_dispatcher():

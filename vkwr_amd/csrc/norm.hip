@@ -1,0 +1,315 @@
+// LayerNorm family for gfx950: plain, residual-add, last-token, bf16 embedding
+// table, and the decode-step fusion of residual add + LayerNorm + token-shift
+// lerp (1 or 6 mix vectors).
+//
+// One 256-lane workgroup (4 waves) per row.  The row (at most 8192 values) is
+// read once into VGPRs -- 16-byte loads of 8 fp16 values per lane when C is a
+// multiple of 8 and the tensors are 16-byte aligned, scalar loads otherwise --
+// and the two statistics passes (mean, then the centred sum of squares) run on
+// the registers, so HBM sees each input byte once and each output byte once.
+// Reductions use a fixed order (wave butterfly + wave-ordered block sum), so
+// results are run-to-run deterministic.
+//
+// Roofline: HBM.  Algorithmic bytes per row of C channels: plain LN 4C (read
+// x, write y); residual add 8C; decode fusion with n mix vectors
+// 2C (x) + 2C (residual) + 2C (shift read) + 2C (shift write) + 2C (x_out)
+// + 2nC (outputs), plus the C-length parameter vectors (cache resident).
+
+#include "vk_capi.h"
+#include "vk_common.cuh"
+
+namespace vk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxC = 8192;
+
+struct LnArgs {
+  int C;
+  int64_t rows;
+  int64_t src_mul, src_add;  // source row = row * src_mul + src_add (last-token LN)
+  const void* x;             // fp16, or bf16 bits when kBf16
+  const _Float16* residual;  // may be null
+  const void* weight;        // fp16, or bf16 bits when kBf16
+  const void* bias;
+  float eps;
+  _Float16* x_out;  // may be null
+  _Float16* y;      // plain mode output
+  // mix mode
+  _Float16* shift;
+  const _Float16* mix[6];
+  _Float16* out[6];
+};
+
+template <bool kBf16>
+__device__ __forceinline__ float ld_in(const void* p, int64_t i) {
+  if constexpr (kBf16) {
+    return bf16f(reinterpret_cast<const uint16_t*>(p)[i]);
+  } else {
+    return (float)reinterpret_cast<const _Float16*>(p)[i];
+  }
+}
+
+// VW: elements per lane access (8 = one 16-byte load, 1 = scalar); NV: accesses
+// per lane (VW * NV * 256 >= C); NMIX: 0 = plain LN output, 1 or 6 = decode
+// fusion with that many token-shift mix vectors.
+template <int VW, int NV, int NMIX, bool kBf16>
+__global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
+  __shared__ float red[kWaves];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int C = p.C;
+  const int64_t src = (row * p.src_mul + p.src_add) * (int64_t)C;
+  const int64_t dst = row * (int64_t)C;
+
+  float v[NV][VW];
+  float sum = 0.0f;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int c0 = (tid + n * kThreads) * VW;
+    if (c0 < C) {
+      if constexpr (VW == 8 && !kBf16) {
+        const h8 xv = ld8(reinterpret_cast<const _Float16*>(p.x) + src + c0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[n][e] = (float)xv.v[e];
+        if (p.residual) {
+          const h8 rv = ld8(p.residual + src + c0);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)rv.v[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          v[n][e] = ld_in<kBf16>(p.x, src + c0 + e);
+          if (p.residual) v[n][e] = v[n][e] + (float)p.residual[src + c0 + e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < VW; ++e) sum += v[n][e];
+    }
+  }
+  const float mean = block_sum<kWaves>(sum, red) / (float)C;
+  float ss = 0.0f;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int c0 = (tid + n * kThreads) * VW;
+    if (c0 < C) {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        const float d = v[n][e] - mean;
+        ss = __builtin_fmaf(d, d, ss);
+      }
+    }
+  }
+  const float rstd = rsqrtf(block_sum<kWaves>(ss, red) / (float)C + p.eps);
+
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int c0 = (tid + n * kThreads) * VW;
+    if (c0 >= C) continue;
+    _Float16 yh[VW], xo[VW];
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float t = (v[n][e] - mean) * rstd;
+      yh[e] = (_Float16)__builtin_fmaf(t, ld_in<kBf16>(p.weight, c0 + e), ld_in<kBf16>(p.bias, c0 + e));
+      xo[e] = (_Float16)v[n][e];
+    }
+    if constexpr (NMIX == 0) {
+      if constexpr (VW == 8) {
+        st8(p.y + dst + c0, *reinterpret_cast<const h8*>(yh));
+        if (p.x_out) st8(p.x_out + dst + c0, *reinterpret_cast<const h8*>(xo));
+      } else {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          p.y[dst + c0 + e] = yh[e];
+          if (p.x_out) p.x_out[dst + c0 + e] = xo[e];
+        }
+      }
+    } else {
+      // Token-shift lerp of the fp16-rounded LN output with the previous token's.
+      _Float16 prev[VW];
+      if constexpr (VW == 8) {
+        *reinterpret_cast<h8*>(prev) = ld8(p.shift + dst + c0);
+        st8(p.x_out + dst + c0, *reinterpret_cast<const h8*>(xo));
+        st8(p.shift + dst + c0, *reinterpret_cast<const h8*>(yh));
+      } else {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          prev[e] = p.shift[dst + c0 + e];
+          p.x_out[dst + c0 + e] = xo[e];
+          p.shift[dst + c0 + e] = yh[e];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NMIX; ++i) {
+        _Float16 o[VW];
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          const float yv = (float)yh[e];
+          o[e] = (_Float16)__builtin_fmaf((float)prev[e] - yv, (float)p.mix[i][c0 + e], yv);
+        }
+        if constexpr (VW == 8) {
+          st8(p.out[i] + dst + c0, *reinterpret_cast<const h8*>(o));
+        } else {
+#pragma unroll
+          for (int e = 0; e < VW; ++e) p.out[i][dst + c0 + e] = o[e];
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const _Float16* x, const _Float16* y, _Float16* out,
+                                                  int64_t n, int vec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (vec) {
+    if (i * 8 >= n) return;
+    const h8 a = ld8(x + i * 8), b = ld8(y + i * 8);
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)((float)a.v[e] + (float)b.v[e]);
+    st8(out + i * 8, o);
+  } else {
+    if (i >= n) return;
+    out[i] = (_Float16)((float)x[i] + (float)y[i]);
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int NMIX, bool kBf16>
+int launch_ln(const char* fn, const LnArgs& p, bool vec_ok, hipStream_t stream) {
+  VK_REQUIRE(p.C > 0 && p.C <= kMaxC, "%s: unsupported C=%d (need 0 < C <= 8192)", fn, p.C);
+  VK_REQUIRE(p.rows >= 0 && p.rows <= 0x7fffffff, "%s: too many rows", fn);
+  if (p.rows == 0) return VKWR_OK;
+  const dim3 grid((unsigned)p.rows), block(kThreads);
+  if (vec_ok && p.C % 8 == 0) {
+    const int per = (p.C / 8 + kThreads - 1) / kThreads;  // 1..4
+    if (per == 1) hipLaunchKernelGGL((layer_norm_kernel<8, 1, NMIX, kBf16>), grid, block, 0, stream, p);
+    else if (per == 2) hipLaunchKernelGGL((layer_norm_kernel<8, 2, NMIX, kBf16>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((layer_norm_kernel<8, 4, NMIX, kBf16>), grid, block, 0, stream, p);
+  } else {
+    const int per = (p.C + kThreads - 1) / kThreads;  // 1..32
+    if (per <= 8) hipLaunchKernelGGL((layer_norm_kernel<1, 8, NMIX, kBf16>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((layer_norm_kernel<1, 32, NMIX, kBf16>), grid, block, 0, stream, p);
+  }
+  return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vkwr_layer_norm_f16(int64_t rows, int C, const uint16_t* x, const uint16_t* residual,
+                                   const uint16_t* weight, const uint16_t* bias, float eps,
+                                   uint16_t* x_out, uint16_t* y, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_layer_norm_f16";
+  VK_REQUIRE(rows == 0 || (x && weight && bias && y), "%s: null pointer", fn);
+  LnArgs p{};
+  p.C = C;
+  p.rows = rows;
+  p.src_mul = 1;
+  p.x = x;
+  p.residual = reinterpret_cast<const _Float16*>(residual);
+  p.weight = weight;
+  p.bias = bias;
+  p.eps = eps;
+  p.x_out = reinterpret_cast<_Float16*>(x_out);
+  p.y = reinterpret_cast<_Float16*>(y);
+  const bool vec = aligned16(x) && aligned16(y) && (!residual || aligned16(residual)) &&
+                   (!x_out || aligned16(x_out));
+  return launch_ln<0, false>(fn, p, vec, (hipStream_t)stream);
+}
+
+extern "C" int vkwr_add_last_layer_norm_f16(int B, int T, int C, const uint16_t* x,
+                                            const uint16_t* residual, const uint16_t* weight,
+                                            const uint16_t* bias, float eps, uint16_t* y,
+                                            void* stream) {
+  clear_error();
+  const char* fn = "vkwr_add_last_layer_norm_f16";
+  VK_REQUIRE(B >= 0 && T > 0, "%s: bad B=%d T=%d", fn, B, T);
+  VK_REQUIRE(B == 0 || (x && residual && weight && bias && y), "%s: null pointer", fn);
+  LnArgs p{};
+  p.C = C;
+  p.rows = B;
+  p.src_mul = T;
+  p.src_add = T - 1;
+  p.x = x;
+  p.residual = reinterpret_cast<const _Float16*>(residual);
+  p.weight = weight;
+  p.bias = bias;
+  p.eps = eps;
+  p.y = reinterpret_cast<_Float16*>(y);
+  const bool vec = aligned16(x) && aligned16(residual) && aligned16(y);
+  return launch_ln<0, false>(fn, p, vec, (hipStream_t)stream);
+}
+
+extern "C" int vkwr_emb_ln0_bf16_to_f16(int64_t V, int C, const uint16_t* emb,
+                                        const uint16_t* weight, const uint16_t* bias, float eps,
+                                        uint16_t* out, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_emb_ln0_bf16_to_f16";
+  VK_REQUIRE(V == 0 || (emb && weight && bias && out), "%s: null pointer", fn);
+  LnArgs p{};
+  p.C = C;
+  p.rows = V;
+  p.src_mul = 1;
+  p.x = emb;
+  p.weight = weight;
+  p.bias = bias;
+  p.eps = eps;
+  p.y = reinterpret_cast<_Float16*>(out);
+  return launch_ln<0, true>(fn, p, false, (hipStream_t)stream);
+}
+
+extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* x,
+                                           const uint16_t* residual, uint16_t* shift_state,
+                                           const uint16_t* weight, const uint16_t* bias, int n_mix,
+                                           const uint16_t* const* mix, float eps, uint16_t* x_out,
+                                           uint16_t* const* out, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_add_layer_norm_mix_f16";
+  VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
+  VK_REQUIRE(mix && out, "%s: null pointer", fn);
+  LnArgs p{};
+  p.C = C;
+  p.rows = rows;
+  p.src_mul = 1;
+  p.x = x;
+  p.residual = reinterpret_cast<const _Float16*>(residual);
+  p.weight = weight;
+  p.bias = bias;
+  p.eps = eps;
+  p.x_out = reinterpret_cast<_Float16*>(x_out);
+  p.shift = reinterpret_cast<_Float16*>(shift_state);
+  bool vec = aligned16(x) && aligned16(residual) && aligned16(shift_state) && aligned16(x_out);
+  for (int i = 0; i < n_mix; ++i) {
+    VK_REQUIRE(rows == 0 || (mix[i] && out[i]), "%s: null pointer", fn);
+    p.mix[i] = reinterpret_cast<const _Float16*>(mix[i]);
+    p.out[i] = reinterpret_cast<_Float16*>(out[i]);
+    vec = vec && aligned16(out[i]);
+  }
+  VK_REQUIRE(rows == 0 || (x && residual && shift_state && weight && bias && x_out),
+             "%s: null pointer", fn);
+  if (n_mix == 1) return launch_ln<1, false>(fn, p, vec, (hipStream_t)stream);
+  return launch_ln<6, false>(fn, p, vec, (hipStream_t)stream);
+}
+
+extern "C" int vkwr_add_f16(int64_t n, const uint16_t* x, const uint16_t* y, uint16_t* out,
+                            void* stream) {
+  clear_error();
+  VK_REQUIRE(n >= 0, "vkwr_add_f16: negative size");
+  if (n == 0) return VKWR_OK;
+  VK_REQUIRE(x && y && out, "vkwr_add_f16: null pointer");
+  const int vec = (n % 8 == 0) && aligned16(x) && aligned16(y) && aligned16(out);
+  const int64_t items = vec ? n / 8 : n;
+  const int64_t blocks = (items + 255) / 256;
+  VK_REQUIRE(blocks <= 0x7fffffff, "vkwr_add_f16: too many elements");
+  hipLaunchKernelGGL(add_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const _Float16*>(x), reinterpret_cast<const _Float16*>(y),
+                     reinterpret_cast<_Float16*>(out), n, vec);
+  return check_launch("vkwr_add_f16");
+}

@@ -80,4 +80,47 @@ __device__ __forceinline__ void dma16(const void* gsrc, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, (VK_LDS void*)lds_base, 16, 0, 0);
 }
 
+// ---------------------------------------------------------------- reductions
+
+// Sum over the 64 lanes of a wave: xor butterfly, then lane 0's total is
+// broadcast so every lane holds bit-identical values (each lane's butterfly
+// associates differently).  Fixed order, so run-to-run deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// Sum over a workgroup of NW waves (NW * 64 threads); `red` is NW floats of LDS.
+// Wave totals are added in wave order.  Contains two barriers: every thread of
+// the workgroup must call it.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------- vectors
+
+// 8 fp16 values (16 bytes), the unit of the vectorised elementwise kernels.
+struct alignas(16) h8 {
+  _Float16 v[8];
+};
+
+__device__ __forceinline__ h8 ld8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
+__device__ __forceinline__ void st8(_Float16* p, const h8& x) { *reinterpret_cast<h8*>(p) = x; }
+
+// bf16 bit pattern -> float (exact).
+__device__ __forceinline__ float bf16f(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
 }  // namespace vk
