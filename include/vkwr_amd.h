@@ -226,6 +226,56 @@ VKWR_EXPORT int vkwr_activation_f16(int act, int64_t n, const uint16_t* x, uint1
 VKWR_EXPORT int vkwr_add_vec_f16(int64_t n, int C, const uint16_t* x, const uint16_t* vec,
                                  uint16_t* out, void* stream);
 
+/* ------------------------------------------------------------------ GEMM */
+
+enum {
+  VKWR_GEMM_B_NK = 0, /* B is [N,K] row-major (nn.Linear weight): y = x . B^T */
+  VKWR_GEMM_B_KN = 1  /* B is [K,N] row-major:                      y = x . B   */
+};
+enum {
+  VKWR_GEMM_ACT_NONE = 0,
+  VKWR_GEMM_ACT_TANH = 1,   /* applied to A elementwise (rounded to fp16) before the product */
+  VKWR_GEMM_ACT_SIGMOID = 2,
+  VKWR_GEMM_ACT_RELU_SQUARE = 3
+};
+enum {
+  VKWR_GEMM_EPI_NONE = 0,
+  VKWR_GEMM_EPI_RELU_SQUARE = 1,    /* y = max(acc, 0)^2 */
+  VKWR_GEMM_EPI_VALUE_RESIDUAL = 2  /* y = v + (v_first - v) * sigmoid(v0[n] + acc) */
+};
+
+/* One GEMM of a batch: c[m,n] = epilogue(sum_k act(a[m,k]) * B(k,n)), fp16
+ * operands and output, fp32 accumulation.  a [m,k], c [m,n] and B are
+ * contiguous row-major; v, v_first [m,n] and v0 [n] are read by the
+ * value-residual epilogue only. */
+typedef struct vkwr_gemm_problem {
+  const uint16_t* a;
+  const uint16_t* b;
+  uint16_t* c;
+  int64_t m, n, k;
+  int b_layout;
+  int a_act;
+  int epilogue;
+  const uint16_t* v;
+  const uint16_t* v_first;
+  const uint16_t* v0;
+} vkwr_gemm_problem;
+
+/* Bytes of device workspace vkwr_gemm_f16 needs for this batch (fp32 K-split
+ * partials; 0 when no problem is split), or -1 on invalid arguments. */
+VKWR_EXPORT int64_t vkwr_gemm_f16_workspace_bytes(int n_problems, const vkwr_gemm_problem* problems);
+
+/* Runs 1..8 independent GEMMs in one launch on the gfx950 matrix cores.
+ * `problems` is a host array; `workspace` is device memory of at least
+ * vkwr_gemm_f16_workspace_bytes(...) bytes (may be NULL when that is 0).
+ * Replaces the device work of every vkwr_v1_linear op -- cublasGemmEx /
+ * cublasLtMatmul (csrc/v1/linear/linear_ops.cu:973-1057, 1237-1392), the
+ * CUDA-core, WMMA and split-K GEMV/GEMM kernels (:46-969, 1059-1833) -- and of
+ * the vkwr_v1_rank adapters (csrc/v1/rank/rank_ops.cu:16-482), reached from
+ * csrc/v1/linear/torch_bindings.cpp:8-225 and csrc/v1/rank/torch_bindings.cpp:8-122. */
+VKWR_EXPORT int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

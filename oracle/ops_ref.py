@@ -143,3 +143,54 @@ def ulp16(x):
     a = np.abs(np.asarray(x, dtype=F64))
     e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
     return np.maximum(2.0 ** (e - 10), 2.0 ** -24)
+
+
+# ---------------------------------------------------------------- GEMMs
+
+def _act(x, act):
+    if act == "tanh":
+        return np.tanh(x)
+    if act == "sigmoid":
+        return sigmoid(x)
+    if act == "relu2":
+        r = np.maximum(x, 0.0)
+        return r * r
+    return x
+
+
+def gemm(a, b, b_layout="nk", a_act=None, epi=None, v=None, v_first=None, v0=None, round_act=True):
+    """fp16 GEMM with fp32-or-better accumulation, restated in float64
+    (reference csrc/v1/linear/linear_ops.cu:1001-1011 cuBLAS fp16 in / fp32
+    compute / fp16 out; rank adapters csrc/v1/rank/rank_ops.cu:16-333).
+    b is [N,K] ("nk", y = a.b^T) or [K,N] ("kn", y = a.b).  a_act in
+    {None, "tanh", "sigmoid", "relu2"} is applied to a elementwise and, with
+    round_act, rounded to fp16 (the reference keeps it in fp32 for the rank
+    adapters and rounds it for the sparse FFN).  epi in {None, "relu2",
+    "vres"}.  Returns (y fp16, abs_sum) where abs_sum = sum_k |a_k b_k| bounds
+    the accumulation error."""
+    a64 = _act(_f(a), a_act)
+    if a_act is not None and round_act:
+        a64 = a64.astype(F16).astype(F64)
+    w = _f(b)
+    wt = w.T if b_layout == "nk" else w
+    y = a64 @ wt
+    abs_sum = np.abs(a64) @ np.abs(wt)
+    if epi == "relu2":
+        r = np.maximum(y, 0.0)
+        y = r * r
+    elif epi == "vres":
+        vv = _f(v)
+        y = vv + (_f(v_first) - vv) * sigmoid(_f(v0) + y)
+    return y.astype(F16), abs_sum
+
+
+def cmix_sparse(x, shift_state, x_k, key_fc, value_fc):
+    """Channel mix (reference csrc/v1/mix/mix_ops.cu:296-863): mixed = lerp(x, prev);
+    act = fp16(relu(mixed . key_fc^T)^2); out = act . value_fc; shift_state := x[:, T-1].
+    The mixed input is rounded to fp16 first (as this build's token-shift op does).
+    x [B,T,C]; shift_state [B,C] (in place); key_fc, value_fc [F,C]."""
+    B, T, C = x.shape
+    mixed = token_shift(x, shift_state, [x_k])[0].reshape(B * T, C)
+    act, _ = gemm(mixed, key_fc, "nk", epi="relu2")
+    out, abs_sum = gemm(act, value_fc, "kn")
+    return out.reshape(B, T, C), act, abs_sum.reshape(B, T, C)

@@ -1,0 +1,252 @@
+"""GPU parity of the fp16 GEMM family (vkwr_v1_linear, vkwr_v1_rank, the
+vkwr_v1_mix channel-mix ops) against the float64 oracle (oracle/ops_ref.py).
+
+Bar (floating point): |gpu - oracle| <= 1 fp16 ulp of the oracle value
++ 1e-5 * sum_k |a_k b_k| (fp32 accumulation over K, with the split-K partial
+sums), + 2^-11 * sum_k |act(a_k) b_k| where the A-operand activation is rounded
+to fp16 on the GPU but not in the reference's rank adapters.  Epilogues are
+checked through their derivatives.  Also restated: the reference's own linear
+tests (tests/ops/test_v1_linear_ops.py) -- shapes, NaN, zero input, torch.matmul
+at atol/rtol 5e-3 -- and its validation errors for the tuning arguments.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops_ref as R
+
+pytestmark = pytest.mark.gpu
+
+rng = np.random.default_rng(7)
+ACC = 1e-5          # fp32 accumulation slack, relative to sum |a b|
+ACT = 2.0 ** -11    # fp16 rounding of an activated A operand (half an ulp, relative)
+
+
+def h(*shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float16)
+
+
+def dev(x, gpu):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+
+
+def check(got, ref, slack, what=""):
+    g = got.detach().cpu().numpy().astype(np.float64) if torch.is_tensor(got) else got.astype(np.float64)
+    r = ref.astype(np.float64)
+    bound = R.ulp16(r) + slack
+    bad = np.abs(g - r) > bound
+    assert not bad.any(), (what, int(bad.sum()), float(np.abs(g - r).max()), float(bound.min()))
+
+
+GEMM_SHAPES = [  # (M, K, N)
+    (1, 64, 64), (1, 4096, 512), (3, 72, 100), (5, 70, 40), (128, 2048, 2048), (128, 2048, 96),
+    (128, 96, 2048), (64, 256, 320), (17, 512, 1024), (300, 1024, 768), (1024, 512, 512),
+]
+
+
+@pytest.mark.parametrize("M,K,N", GEMM_SHAPES)
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_gemm_vs_oracle(gpu, M, K, N, layout):
+    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    a = h(M, K)
+    w = h(N, K, scale=0.05) if layout == "nk" else h(K, N, scale=0.05)
+    y = (L.linear_f16_orig if layout == "nk" else L.linear_f16)(dev(a, gpu), dev(w, gpu))
+    assert y.shape == (M, N) and y.dtype == torch.float16
+    ref, abs_sum = R.gemm(a, w, layout)
+    check(y, ref, ACC * abs_sum, f"{layout} {M}x{K}x{N}")
+
+
+def test_gemm_deterministic_and_split_k(gpu):
+    """Small-M shapes take the K-split path; results are run-to-run identical."""
+    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    a, w = dev(h(128, 8192), gpu), dev(h(2048, 8192, scale=0.02), gpu)
+    y1 = L.linear_f16_orig(a, w)
+    y2 = L.linear_f16_orig(a, w)
+    assert torch.equal(y1, y2)
+    ref, abs_sum = R.gemm(a.cpu().numpy(), w.cpu().numpy(), "nk")
+    check(y1, ref, ACC * abs_sum, "128x8192x2048")
+
+
+def test_all_linear_ops_compute_the_same_function(gpu):
+    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    B, T, K, N = 2, 3, 256, 512
+    x = dev(h(B, T, K), gpu)
+    w_kn = dev(h(K, N, scale=0.05), gpu)
+    w_nk = w_kn.t().contiguous()
+    base = L.linear_f16(x, w_kn)
+    assert base.shape == (B, T, N)
+    same = [
+        L.linear_f16_lt(x, w_kn), L.linear_f16_rows_splitk(x, w_kn, 256),
+        L.linear_f16_orig(x, w_nk), L.linear_orig_rows_f16(x, w_nk, 4, 8),
+        L.linear_orig_rows_cfg_f16(x, w_nk, 64, 4, 4), L.linear_orig_wmma16_f16(x, w_nk),
+        L.linear_f16_orig_lt(x, w_nk), L.linear_f16_orig_lt_cfg(x, w_nk, 4, 0), L.linear_t_f16(x, w_nk),
+    ]
+    for y in same:
+        assert torch.equal(y, base)
+    x1 = dev(h(1, K), gpu)
+    b1 = L.linear_f16(x1, w_kn)
+    for y in (L.linear_f16_m1_splitk(x1, w_kn), L.linear_f16_m1_splitk_cfg(x1, w_kn, 160),
+              L.linear_f16_m1_splitk_tile(x1, w_kn, 128, 128), L.linear_f16_m1_splitk_warpred_tile(x1, w_kn, 64, 64)):
+        assert y.shape == (1, N) and torch.equal(y, b1)
+    x2 = dev(h(2, K), gpu)
+    assert torch.equal(L.linear_orig_rows_exact_f16(x2, w_nk, 128, 2, False), L.linear_f16_orig(x2, w_nk))
+    assert torch.equal(L.linear_orig_rows_exact_f16(x1, w_nk, 128, 2, True), L.linear_f16_orig(x1, w_nk))
+
+
+def test_linear_validation_errors(gpu):
+    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    K, N = 128, 256
+    x = dev(h(2, 4, K), gpu)
+    w = dev(h(K, N), gpu)
+    wo = w.t().contiguous()
+    bad_calls = [
+        lambda: L.linear_f16(dev(h(2, 4, K + 1), gpu), w),          # shape mismatch
+        lambda: L.linear_f16(x.float(), w),                          # dtype
+        lambda: L.linear_f16(dev(h(2, 4, 2 * K), gpu)[..., ::2], w),  # non-contiguous
+        lambda: L.linear_orig_rows_f16(x, wo, 5, 2),
+        lambda: L.linear_orig_rows_cfg_f16(x, wo, 128, 4, 4),
+        lambda: L.linear_orig_rows_exact_f16(x, wo, 128, 2, False),  # 8 rows
+        lambda: L.linear_f16_orig_lt_cfg(x, wo, 2048, 0),
+        lambda: L.linear_f16_orig_lt_cfg(x, wo, 4, 64),
+        lambda: L.linear_f16_m1_splitk(x, w),                         # M != 1
+        lambda: L.linear_f16_m1_splitk_cfg(dev(h(1, K), gpu), w, 100),
+        lambda: L.linear_f16_m1_splitk_tile(dev(h(1, K), gpu), w, 128, 32),
+        lambda: L.linear_f16_m1_splitk_warpred_tile(dev(h(1, K), gpu), w, 384, 64),
+        lambda: L.linear_f16_rows_splitk(x, w, 64),
+        lambda: L.linear_t_act_f16(dev(h(1, 64), gpu), dev(h(1024, 64), gpu), 3),
+        lambda: L.linear_t_act_f16(dev(h(8, 64), gpu), dev(h(1024, 64), gpu), 1),  # M > 4
+        lambda: L.linear_orig_wmma16_f16(dev(h(2, 72), gpu), dev(h(64, 72), gpu)),
+    ]
+    for i, call in enumerate(bad_calls):
+        with pytest.raises(RuntimeError):
+            call()
+            pytest.fail(f"call {i} did not raise")
+    v = dev(h(1, 1024), gpu)
+    with pytest.raises(RuntimeError):  # v0 shape (reference test_linear_t_vres_f16_v0_shape_mismatch)
+        L.linear_t_vres_f16(dev(h(1, 64), gpu), dev(h(1024, 64), gpu), v, v, dev(h(512), gpu))
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_linear_t_act_and_vres(gpu, act):
+    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    M, K, N = 4, 96, 2048
+    x, w = h(M, K), h(N, K, scale=0.1)
+    y = L.linear_t_act_f16(dev(x, gpu), dev(w, gpu), act)
+    ref, abs_sum = R.gemm(x, w, "nk", a_act="tanh" if act == 1 else "sigmoid", round_act=False)
+    check(y, ref, (ACC + ACT) * abs_sum, "t_act")
+    v, vf, v0 = h(M, N), h(M, N), h(N)
+    y = L.linear_t_vres_f16(dev(x, gpu), dev(w, gpu), dev(v, gpu), dev(vf, gpu), dev(v0, gpu))
+    ref, abs_sum = R.gemm(x, w, "nk", epi="vres", v=v, v_first=vf, v0=v0)
+    check(y, ref, 0.25 * np.abs(vf.astype(np.float64) - v) * ACC * abs_sum, "t_vres")
+
+
+def test_linear_reference_unit_tests(gpu):
+    """reference tests/ops/test_v1_linear_ops.py: shapes, NaN, zero input, vs torch.matmul."""
+    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    for B, T, K, N in [(1, 1, 64, 128), (2, 4, 128, 256), (1, 16, 256, 512), (4, 8, 512, 1024)]:
+        x = torch.randn(B, T, K, dtype=torch.float16, device=gpu)
+        w = torch.randn(K, N, dtype=torch.float16, device=gpu)
+        y = L.linear_f16(x, w)
+        assert y.shape == (B, T, N) and not torch.isnan(y).any()
+    x = torch.randn(2, 4, 128, dtype=torch.float16, device=gpu)
+    w = torch.randn(128, 256, dtype=torch.float16, device=gpu)
+    torch.testing.assert_close(L.linear_f16(x, w), torch.matmul(x.float(), w.float()).half(), atol=5e-3, rtol=5e-3)
+    wo = torch.randn(256, 128, dtype=torch.float16, device=gpu)
+    torch.testing.assert_close(L.linear_f16_orig(x, wo), torch.matmul(x.float(), wo.float().t()).half(),
+                               atol=5e-3, rtol=5e-3)
+    torch.testing.assert_close(L.linear_t_f16(x, wo), torch.matmul(x.float(), wo.float().t()).half(),
+                               atol=5e-3, rtol=5e-3)
+    assert (L.linear_f16(torch.zeros_like(x), w) == 0).all()
+    y = L.linear_f16(torch.randn(1, 1, 4096, dtype=torch.float16, device=gpu),
+                     torch.randn(4096, 8192, dtype=torch.float16, device=gpu) * 0.02)
+    assert y.shape == (1, 1, 8192) and not torch.isnan(y).any()
+
+
+# ------------------------------------------------------------------ rank adapters
+
+@pytest.mark.parametrize("M,C,ranks", [(128, 2048, (96, 96, 256, 64)), (3, 256, (32, 16, 64, 8)),
+                                       (1, 4096, (128, 128, 480, 96))])
+def test_rank_in_out(gpu, M, C, ranks):
+    from vkwr_amd._ops.v1 import v1_rank_ops as K
+    Rw, Ra, Rg, Rv = ranks
+    xs = [h(M, C) for _ in range(4)]
+    w1s = [h(r, C, scale=0.02) for r in ranks]
+    outs = K.linear_wagv_rank_in_f16(M, C, Rw, Ra, Rg, Rv, *(dev(a, gpu) for a in xs + w1s))
+    assert [tuple(o.shape) for o in outs] == [(M, r) for r in ranks]
+    for o, x, w in zip(outs, xs, w1s):
+        ref, abs_sum = R.gemm(x, w, "nk")
+        check(o, ref, ACC * abs_sum, "rank_in")
+    outs3 = K.linear_wag_rank_in_f16(M, C, Rw, Ra, Rg, *(dev(a, gpu) for a in xs[:3] + w1s[:3]))
+    assert all(torch.equal(a, b) for a, b in zip(outs3, outs[:3]))
+
+    ins = [o.cpu().numpy() for o in outs]
+    w2s = [h(C, r, scale=0.1) for r in ranks]
+    v, vf, v0 = h(M, C), h(M, C), h(C)
+    res = K.linear_wagv_rank_out_f16(M, C, Rw, Ra, Rg, Rv, *(dev(a, gpu) for a in ins + w2s + [v, vf, v0]))
+    acts = ["tanh", None, "sigmoid", None]
+    for i, (o, x, w, act) in enumerate(zip(res, ins, w2s, acts)):
+        if i < 3:
+            ref, abs_sum = R.gemm(x, w, "nk", a_act=act, round_act=False)
+            check(o, ref, (ACC + (ACT if act else 0)) * abs_sum, f"rank_out {i}")
+        else:
+            ref, abs_sum = R.gemm(x, w, "nk", epi="vres", v=v, v_first=vf, v0=v0)
+            check(o, ref, 0.25 * np.abs(vf.astype(np.float64) - v) * ACC * abs_sum, "rank_out v")
+    res3 = K.linear_wag_rank_out_f16(M, C, Rw, Ra, Rg, *(dev(a, gpu) for a in ins[:3] + w2s[:3]))
+    assert all(torch.equal(a, b) for a, b in zip(res3, res[:3]))
+
+
+def test_rank_validation_errors(gpu):
+    from vkwr_amd._ops.v1 import v1_rank_ops as K
+    M, C = 2, 128
+    x = dev(h(M, C), gpu)
+    w = dev(h(16, C), gpu)
+    with pytest.raises(RuntimeError):
+        K.linear_wag_rank_in_f16(M, C, 16, 16, 8, x, x, x, w, w, w)  # g1_t shape
+    with pytest.raises(RuntimeError):
+        K.linear_wag_rank_out_f16(M, C, 16, 16, 16, x, x, x, w, w, w)  # w1 shape
+
+
+# ------------------------------------------------------------------ channel mix (FFN)
+
+@pytest.mark.parametrize("B,T,C,F", [(1, 1, 256, 256), (2, 8, 256, 512), (128, 1, 2048, 8192), (1, 4, 512, 1024)])
+def test_cmix_sparse(gpu, B, T, C, F):
+    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    x, shift0 = h(B, T, C), h(B, C)
+    x_k = rng.random(C).astype(np.float16)
+    key, value = h(F, C, scale=0.05), h(F, C, scale=0.05)
+    shift = dev(shift0, gpu)
+    if B == 1 and T == 1:
+        y = M.cmix_sparse_one(C, F, dev(x, gpu), shift, dev(x_k, gpu), dev(key, gpu), dev(value, gpu))
+    else:
+        y = M.cmix_sparse_rows(B, T, C, F, dev(x, gpu), shift, dev(x_k, gpu), dev(key, gpu), dev(value, gpu))
+    assert y.shape == (B, T, C)
+    s_ref = shift0.copy()
+    ref, act, abs_sum = R.cmix_sparse(x, s_ref, x_k, key, value)
+    assert np.array_equal(shift.cpu().numpy(), s_ref)
+    # act may differ by 1 fp16 ulp where the up projection straddles a rounding boundary
+    act_slack = ((np.abs(act.astype(np.float64)) * 2.0 ** -9) @ np.abs(value.astype(np.float64))).reshape(B, T, C)
+    check(y, ref, ACC * abs_sum + act_slack, "cmix")
+
+
+def test_cmix_down_ops(gpu):
+    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    B, T, C, F = 2, 3, 512, 1024
+    pre = h(B, T, F)
+    value = h(F, C, scale=0.05)
+    act = R.relu_square(pre)
+    y = M.cmix_sparse_down_rows(B, T, C, F, dev(act, gpu), dev(value, gpu))
+    ref, abs_sum = R.gemm(act.reshape(B * T, F), value, "kn")
+    check(y.reshape(B * T, C), ref, ACC * abs_sum, "down_rows")
+    for fn in (M.cmix_sparse_down_relu_rows, M.cmix_sparse_down_relu_rows_t512):
+        y2 = fn(B, T, C, F, dev(pre, gpu), dev(value, gpu))
+        assert torch.equal(y2, y)
+    y1 = M.cmix_sparse_down_one(C, F, dev(act[0, 0], gpu), dev(value, gpu))
+    assert y1.shape == (1, 1, C) and torch.equal(y1.view(C), y[0, 0])
+    y1r = M.cmix_sparse_down_relu_one(C, F, dev(pre[0, 0], gpu), dev(value, gpu))
+    assert torch.equal(y1r, y1)
+    with pytest.raises(RuntimeError):
+        M.cmix_sparse_down_relu_rows_t512(B, T, 256, F, dev(h(B, T, F), gpu), dev(h(F, 256), gpu))
+    with pytest.raises(RuntimeError):
+        x100 = dev(h(1, 1, 100), gpu)
+        M.cmix_sparse_one(100, 128, x100, dev(h(1, 100), gpu), dev(h(100), gpu), dev(h(128, 100), gpu),
+                          dev(h(128, 100), gpu))

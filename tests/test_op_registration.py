@@ -18,10 +18,10 @@ from vkwr_amd._ops.v1 import v1_wkv_ops
 # Reference interface data for the other namespaces (see tests/golden/README.md).
 _IFACE = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "ref_interface.json")))
 # Namespaces (and their wrapper modules) this build registers.
-BUILT = {"vkwr_v1_norm": "v1_norm_ops", "vkwr_v1_mix": "v1_mix_ops"}
+BUILT = {"vkwr_v1_norm": "v1_norm_ops", "vkwr_v1_mix": "v1_mix_ops", "vkwr_v1_linear": "v1_linear_ops",
+         "vkwr_v1_rank": "v1_rank_ops"}
 # Ops of a built namespace that are not registered yet (skipped, not passed).
-PENDING = {"cmix_sparse_one", "cmix_sparse_rows", "cmix_sparse_down_one", "cmix_sparse_down_rows",
-           "cmix_sparse_down_relu_one", "cmix_sparse_down_relu_rows", "cmix_sparse_down_relu_rows_t512"}
+PENDING = set()
 
 # The reference's schema strings (the interface itself, kept identical on purpose).
 REF_SCHEMAS = {

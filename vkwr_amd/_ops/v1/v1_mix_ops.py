@@ -135,3 +135,67 @@ def _(C, x, vec):
 
 def add_vec(C, x, vec):
     return torch.ops.vkwr_v1_mix.add_vec(C, x, vec)
+
+
+# ===== channel mix (FFN): act = relu(mix(x) . key_fc^T)^2, out = act . value_fc =====
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_one")
+def _(C, F, x, shift_state, x_k, key_fc, value_fc):
+    return torch.empty(1, 1, C, dtype=x.dtype, device=x.device)
+
+
+def cmix_sparse_one(C, F, x, shift_state, x_k, key_fc, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_one(C, F, x, shift_state, x_k, key_fc, value_fc)
+
+
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_rows")
+def _(B, T, C, F, x, shift_state, x_k, key_fc, value_fc):
+    return torch.empty(B, T, C, dtype=x.dtype, device=x.device)
+
+
+def cmix_sparse_rows(B, T, C, F, x, shift_state, x_k, key_fc, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_rows(B, T, C, F, x, shift_state, x_k, key_fc, value_fc)
+
+
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_down_one")
+def _(C, F, act, value_fc):
+    return torch.empty(1, 1, C, dtype=act.dtype, device=act.device)
+
+
+def cmix_sparse_down_one(C, F, act, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_down_one(C, F, act, value_fc)
+
+
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_down_rows")
+def _(B, T, C, F, act, value_fc):
+    return torch.empty(B, T, C, dtype=act.dtype, device=act.device)
+
+
+def cmix_sparse_down_rows(B, T, C, F, act, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_down_rows(B, T, C, F, act, value_fc)
+
+
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_down_relu_one")
+def _(C, F, preact, value_fc):
+    return torch.empty(1, 1, C, dtype=preact.dtype, device=preact.device)
+
+
+def cmix_sparse_down_relu_one(C, F, preact, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_down_relu_one(C, F, preact, value_fc)
+
+
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_down_relu_rows")
+def _(B, T, C, F, preact, value_fc):
+    return torch.empty(B, T, C, dtype=preact.dtype, device=preact.device)
+
+
+def cmix_sparse_down_relu_rows(B, T, C, F, preact, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_down_relu_rows(B, T, C, F, preact, value_fc)
+
+
+@torch.library.register_fake("vkwr_v1_mix::cmix_sparse_down_relu_rows_t512")
+def _(B, T, C, F, preact, value_fc):
+    return torch.empty(B, T, C, dtype=preact.dtype, device=preact.device)
+
+
+def cmix_sparse_down_relu_rows_t512(B, T, C, F, preact, value_fc):
+    return torch.ops.vkwr_v1_mix.cmix_sparse_down_relu_rows_t512(B, T, C, F, preact, value_fc)

@@ -223,7 +223,7 @@ at::Tensor add_vec(int64_t C, at::Tensor x, at::Tensor vec) {
 }  // namespace
 
 // The sparse channel-mix (FFN) ops of this namespace are registered by
-// ffn_bindings.cpp (they run on the GEMM kernels).
+// ffn_bindings.cpp, linked into this same module (they run on the GEMM kernels).
 TORCH_LIBRARY(vkwr_v1_mix, m) {
   m.def("tmix_mix6(int B, int T, int C, Tensor x, Tensor(a!) shift_state, "
       "Tensor x_r, Tensor x_w, Tensor x_k, Tensor x_v, Tensor x_a, Tensor x_g) -> Tensor[]");

@@ -11,6 +11,8 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <vector>
+
 #include "vkwr_amd.h"
 
 namespace vkt {
@@ -64,6 +66,35 @@ inline void check_status(int st, const char* what) {
 template <typename T>
 inline T* ptr(const at::Tensor& x) {
   return reinterpret_cast<T*>(x.data_ptr());
+}
+
+// Runs a batch of GEMMs (include/vkwr_amd.h vkwr_gemm_f16) on the current
+// stream, with the K-split workspace taken from torch's caching allocator.
+inline void run_gemm(std::vector<vkwr_gemm_problem>& probs, const at::Tensor& like, const char* what) {
+  const int64_t ws = vkwr_gemm_f16_workspace_bytes((int)probs.size(), probs.data());
+  check_status(ws < 0 ? VKWR_ERR_INVALID : VKWR_OK, what);
+  at::Tensor w;
+  if (ws > 0) w = at::empty({ws}, like.options().dtype(at::kByte));
+  check_status(vkwr_gemm_f16((int)probs.size(), probs.data(), ws > 0 ? w.data_ptr() : nullptr, ws,
+                             stream()),
+               what);
+}
+
+inline vkwr_gemm_problem gemm_problem(const at::Tensor& a, const at::Tensor& b, at::Tensor& c,
+                                      int64_t m, int64_t n, int64_t k, int b_layout,
+                                      int a_act = VKWR_GEMM_ACT_NONE,
+                                      int epilogue = VKWR_GEMM_EPI_NONE) {
+  vkwr_gemm_problem p{};
+  p.a = reinterpret_cast<const uint16_t*>(a.data_ptr());
+  p.b = reinterpret_cast<const uint16_t*>(b.data_ptr());
+  p.c = reinterpret_cast<uint16_t*>(c.data_ptr());
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.b_layout = b_layout;
+  p.a_act = a_act;
+  p.epilogue = epilogue;
+  return p;
 }
 
 }  // namespace vkt

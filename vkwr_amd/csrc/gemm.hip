@@ -1,0 +1,429 @@
+// fp16 GEMM on the gfx950 matrix cores: y[M,N] = act(x)[M,K] . W, fp32
+// accumulation, fp16 output, with the RWKV-7 epilogues fused.
+//
+// One launch runs a batch of up to 8 independent problems (e.g. the r/k/v
+// projections and the four low-rank adapter inputs of one layer), each cut
+// into BM x BN output tiles and optionally into K splits; the flat workgroup
+// index walks problem -> M tile -> N tile -> K split.
+//
+// Tile loop: 256 lanes (4 waves in a WM x WN grid), K advanced 32 at a time.
+// Each stage moves an A tile (BM x 32) and a B tile (BN x 32, stored k-inner)
+// global -> VGPRs -> LDS, double buffered: the next stage's global loads are
+// issued before the current stage's MFMAs, and one barrier per stage separates
+// the LDS writes from the reads.  A wave computes its (BM/WM) x (BN/WN) sub-tile
+// as 32x32 blocks with v_mfma_f32_32x32x16_f16; lane l feeds A[l%32][8(l/32)..+7]
+// and B[8(l/32)..+7][l%32] (16-byte LDS reads) and receives
+// D[8(r/4) + 4(l/32) + r%4][l%32] in accumulator r.
+//
+// Weights come in either layout of the reference ops: [N,K] (nn.Linear,
+// K contiguous: loaded like A) or [K,N] (N contiguous: 16-byte loads along N,
+// transposed into the k-inner LDS tile).
+//
+// K splits: with too few tiles to fill the 256 CUs, each split writes fp32
+// partial sums to a workspace; a second kernel adds the splits in index order
+// (deterministic) and applies the epilogue.
+//
+// Roofline: HBM-bound at decode (M <= 128 rows: every weight byte is read
+// once, 2 flops per weight element per row); MFMA-bound for large M.
+
+#include <algorithm>
+
+#include "vk_capi.h"
+#include "vk_common.cuh"
+
+namespace vk {
+namespace {
+
+typedef _Float16 hv8 __attribute__((ext_vector_type(8)));
+typedef float fv16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 32;          // K per stage
+constexpr int kLdsK = kBK + 8;   // padded LDS row (halfs): 80-byte rows spread the banks
+constexpr int kMaxProblems = 8;
+
+struct Prob {
+  const _Float16* a;
+  const _Float16* b;
+  _Float16* c;
+  float* ws;  // split partials [splits][m][n] when splits > 1
+  const _Float16 *v, *vf, *v0;  // value-residual epilogue operands
+  int m, n, k;
+  int b_kn;   // 1: B is [K,N]; 0: B is [N,K]
+  int a_act;  // VKWR_GEMM_ACT_*
+  int epi;    // VKWR_GEMM_EPI_*
+  int vec;    // 16-byte accesses allowed (aligned rows, K and N multiples of 8)
+  int tiles_m, tiles_n, splits, k_per_split;
+  int tile_begin;
+};
+
+struct Batch {
+  int n;
+  Prob p[kMaxProblems];
+};
+
+__device__ __forceinline__ float act_in(float x, int act) {
+  if (act == VKWR_GEMM_ACT_TANH) return tanhf(x);
+  if (act == VKWR_GEMM_ACT_SIGMOID) return sigmoidf(x);
+  if (act == VKWR_GEMM_ACT_RELU_SQUARE) {
+    const float r = fmaxf(x, 0.0f);
+    return r * r;
+  }
+  return x;
+}
+
+__device__ __forceinline__ float epilogue(const Prob& P, float acc, int row, int col) {
+  if (P.epi == VKWR_GEMM_EPI_RELU_SQUARE) {
+    const float r = fmaxf(acc, 0.0f);
+    return r * r;
+  }
+  if (P.epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+    const int64_t i = (int64_t)row * P.n + col;
+    const float vv = (float)P.v[i];
+    const float gate = sigmoidf((float)P.v0[col] + acc);
+    return __builtin_fmaf((float)P.vf[i] - vv, gate, vv);
+  }
+  return acc;
+}
+
+// Loads 8 consecutive fp16 values at p[0..7] that lie in a row whose valid
+// range is [0, lim) relative to p; invalid elements read as 0 and `act` (the
+// A-operand activation) is applied to valid elements only.
+__device__ __forceinline__ hv8 load8(const _Float16* p, int lim, bool vec, int act) {
+  hv8 r;
+  if (vec && lim >= 8) {
+    r = *reinterpret_cast<const hv8*>(p);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (!vec && e < lim) ? p[e] : (_Float16)0.0f;
+  }
+  if (act != VKWR_GEMM_ACT_NONE) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < lim) r[e] = (_Float16)act_in((float)r[e], act);
+  }
+  return r;
+}
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(256) void gemm_kernel(Batch bt) {
+  constexpr int TM = BM / WM / 32;  // 32x32 blocks per wave along M
+  constexpr int TN = BN / WN / 32;
+  constexpr int NA = BM * (kBK / 8);  // 16-byte chunks per stage
+  constexpr int NB = BN * (kBK / 8);
+  constexpr int CA = (NA + 255) / 256;  // per lane
+  constexpr int CB = (NB + 255) / 256;
+  static_assert(TM >= 1 && TN >= 1 && CA >= 1 && CB >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * kLdsK];
+
+  // ---- locate problem / tile / split (workgroup-uniform)
+  const int t = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProblems; ++i)
+    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  const Prob& P = bt.p[pi];
+  int lt = t - P.tile_begin;
+  const int split = lt % P.splits;
+  lt /= P.splits;
+  const int m0 = (lt / P.tiles_n) * BM;
+  const int n0 = (lt % P.tiles_n) * BN;
+  const int kb = split * P.k_per_split;
+  const int ke = min(P.k, kb + P.k_per_split);
+  const int nstage = (ke - kb + kBK - 1) / kBK;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const bool vec = P.vec != 0;
+
+  hv8 ra[CA], rb[CB];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int c = tid + i * 256;
+      const int row = c >> 2, kc = (c & 3) * 8;
+      const int gr = m0 + row, gk = k0 + kc;
+      const int lim = (c < NA && gr < P.m) ? ke - gk : 0;
+      ra[i] = load8(P.a + (int64_t)gr * P.k + gk, lim, vec, P.a_act);
+    }
+    if (!P.b_kn) {
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        const int c = tid + i * 256;
+        const int row = c >> 2, kc = (c & 3) * 8;
+        const int gn = n0 + row, gk = k0 + kc;
+        const int lim = (c < NB && gn < P.n) ? ke - gk : 0;
+        rb[i] = load8(P.b + (int64_t)gn * P.k + gk, lim, vec, VKWR_GEMM_ACT_NONE);
+      }
+    } else {
+      constexpr int NC = BN / 8;  // 8-wide n chunks per k row
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        const int c = tid + i * 256;
+        const int kr = c / NC, nc = (c % NC) * 8;
+        const int gk = k0 + kr, gn = n0 + nc;
+        const int lim = (c < NB && gk < ke) ? P.n - gn : 0;
+        rb[i] = load8(P.b + (int64_t)gk * P.n + gn, lim, vec, VKWR_GEMM_ACT_NONE);
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int c = tid + i * 256;
+      if (c < NA) *reinterpret_cast<hv8*>(&As[buf][(c >> 2) * kLdsK + (c & 3) * 8]) = ra[i];
+    }
+    if (!P.b_kn) {
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        const int c = tid + i * 256;
+        if (c < NB) *reinterpret_cast<hv8*>(&Bs[buf][(c >> 2) * kLdsK + (c & 3) * 8]) = rb[i];
+      }
+    } else {
+      constexpr int NC = BN / 8;
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        const int c = tid + i * 256;
+        if (c >= NB) continue;
+        const int kr = c / NC, nc = (c % NC) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Bs[buf][(nc + e) * kLdsK + kr] = rb[i][e];
+      }
+    }
+  };
+
+  fv16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int arow = wm * (BM / WM) + (lane & 31);
+  const int bcol = wn * (BN / WN) + (lane & 31);
+  const int koff = (lane >> 5) * 8;
+
+  if (nstage > 0) {
+    gload(kb);
+    lstore(0);
+    __syncthreads();
+  }
+  for (int s = 0; s < nstage; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nstage) gload(kb + (s + 1) * kBK);
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += 16) {
+      hv8 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[i] = *reinterpret_cast<const hv8*>(&As[buf][(arow + i * 32) * kLdsK + kk + koff]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[j] = *reinterpret_cast<const hv8*>(&Bs[buf][(bcol + j * 32) * kLdsK + kk + koff]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (s + 1 < nstage) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + bcol + j * 32;
+      if (col >= P.n) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= P.m) continue;
+        if (P.splits > 1) {
+          P.ws[((int64_t)split * P.m + row) * P.n + col] = acc[i][j][r];
+        } else {
+          P.c[(int64_t)row * P.n + col] = (_Float16)epilogue(P, acc[i][j][r], row, col);
+        }
+      }
+    }
+  }
+}
+
+// Adds the K-split partials of every split problem in split order and applies
+// the epilogue.  blockIdx.y = problem index.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(Batch bt) {
+  const Prob& P = bt.p[blockIdx.y];
+  if (P.splits <= 1) return;
+  const int64_t mn = (int64_t)P.m * P.n;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
+    float s = P.ws[i];
+    for (int z = 1; z < P.splits; ++z) s += P.ws[z * mn + i];
+    const int row = (int)(i / P.n), col = (int)(i % P.n);
+    P.c[i] = (_Float16)epilogue(P, s, row, col);
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+struct Config {
+  int bm, bn;
+};
+
+// Tile shape from the largest M of the batch (all problems of one launch share it).
+Config pick_config(int max_m, int min_n) {
+  if (max_m <= 32) return {32, 128};
+  if (max_m <= 64) return {64, 128};
+  if (min_n >= 128 && max_m > 256) return {128, 128};
+  return {128, 64};
+}
+
+// Fills tiling fields and returns the workspace bytes the batch needs.
+int64_t plan(Batch& bt, Config cfg, int target_wgs) {
+  int tiles = 0;
+  for (int i = 0; i < bt.n; ++i) {
+    Prob& P = bt.p[i];
+    P.tiles_m = (P.m + cfg.bm - 1) / cfg.bm;
+    P.tiles_n = (P.n + cfg.bn - 1) / cfg.bn;
+    tiles += P.tiles_m * P.tiles_n;
+  }
+  int64_t ws = 0;
+  for (int i = 0; i < bt.n; ++i) {
+    Prob& P = bt.p[i];
+    const int base = P.tiles_m * P.tiles_n;
+    // Split K only when the whole batch leaves CUs idle; keep >= 8 stages per split.
+    int s = 1;
+    if (tiles < target_wgs && P.m <= 256) {
+      s = (target_wgs + tiles - 1) / tiles;
+      s = std::min(s, std::max(1, P.k / (8 * kBK)));
+      s = std::min(s, 16);
+    }
+    int kps = (P.k + s - 1) / s;
+    kps = (kps + kBK - 1) / kBK * kBK;
+    s = (P.k + kps - 1) / kps;
+    P.splits = std::max(1, s);
+    P.k_per_split = std::max(kps, kBK);
+    if (P.splits > 1) ws += (int64_t)P.splits * P.m * P.n * 4;
+    (void)base;
+  }
+  int begin = 0;
+  for (int i = 0; i < bt.n; ++i) {
+    bt.p[i].tile_begin = begin;
+    begin += bt.p[i].tiles_m * bt.p[i].tiles_n * bt.p[i].splits;
+  }
+  return ws;
+}
+
+int total_wgs(const Batch& bt) {
+  int t = 0;
+  for (int i = 0; i < bt.n; ++i) t += bt.p[i].tiles_m * bt.p[i].tiles_n * bt.p[i].splits;
+  return t;
+}
+
+int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, Config& cfg) {
+  VK_REQUIRE(n >= 1 && n <= kMaxProblems, "%s: 1..%d problems per launch (got %d)", fn, kMaxProblems, n);
+  VK_REQUIRE(pr != nullptr, "%s: null problem list", fn);
+  bt.n = n;
+  int max_m = 0, min_n = 1 << 30;
+  for (int i = 0; i < n; ++i) {
+    const vkwr_gemm_problem& q = pr[i];
+    VK_REQUIRE(q.m >= 0 && q.n >= 0 && q.k >= 0, "%s: negative size in problem %d", fn, i);
+    VK_REQUIRE(q.m <= 0x7fffffff && q.n <= 0x7fffffff && q.k <= 0x7fffffff &&
+                   q.m * q.n <= ((int64_t)1 << 40),
+               "%s: problem %d too large", fn, i);
+    VK_REQUIRE(q.b_layout == VKWR_GEMM_B_NK || q.b_layout == VKWR_GEMM_B_KN, "%s: bad b_layout", fn);
+    VK_REQUIRE(q.a_act >= VKWR_GEMM_ACT_NONE && q.a_act <= VKWR_GEMM_ACT_RELU_SQUARE, "%s: bad a_act", fn);
+    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_GEMM_EPI_VALUE_RESIDUAL,
+               "%s: bad epilogue", fn);
+    const bool empty = q.m == 0 || q.n == 0;
+    VK_REQUIRE(empty || (q.a && q.b && q.c), "%s: null pointer in problem %d", fn, i);
+    VK_REQUIRE(empty || q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL || (q.v && q.v_first && q.v0),
+               "%s: value-residual epilogue needs v, v_first, v0", fn);
+    Prob& P = bt.p[i];
+    P = Prob{};
+    P.a = reinterpret_cast<const _Float16*>(q.a);
+    P.b = reinterpret_cast<const _Float16*>(q.b);
+    P.c = reinterpret_cast<_Float16*>(q.c);
+    P.v = reinterpret_cast<const _Float16*>(q.v);
+    P.vf = reinterpret_cast<const _Float16*>(q.v_first);
+    P.v0 = reinterpret_cast<const _Float16*>(q.v0);
+    P.m = (int)q.m;
+    P.n = (int)q.n;
+    P.k = (int)q.k;
+    P.b_kn = q.b_layout == VKWR_GEMM_B_KN;
+    P.a_act = q.a_act;
+    P.epi = q.epilogue;
+    P.vec = aligned16(q.a) && aligned16(q.b) && q.k % 8 == 0 && (!P.b_kn || q.n % 8 == 0);
+    if (!empty) {
+      max_m = std::max(max_m, P.m);
+      min_n = std::min(min_n, P.n);
+    }
+  }
+  cfg = pick_config(max_m, min_n);
+  return VKWR_OK;
+}
+
+constexpr int kTargetWgs = 512;  // two workgroups per CU on 256 CUs
+
+}  // namespace
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int64_t vkwr_gemm_f16_workspace_bytes(int n_problems, const vkwr_gemm_problem* problems) {
+  clear_error();
+  Batch bt;
+  Config cfg;
+  if (build_batch("vkwr_gemm_f16_workspace_bytes", n_problems, problems, bt, cfg)) return -1;
+  return plan(bt, cfg, kTargetWgs);
+}
+
+extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_gemm_f16";
+  Batch bt;
+  Config cfg;
+  if (int e = build_batch(fn, n_problems, problems, bt, cfg)) return e;
+  const int64_t need = plan(bt, cfg, kTargetWgs);
+  VK_REQUIRE(need <= workspace_bytes && (need == 0 || workspace != nullptr),
+             "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need,
+             (long long)workspace_bytes);
+  // Zero-sized problems and K == 0: nothing to tile; K == 0 writes epilogue(0).
+  float* ws = reinterpret_cast<float*>(workspace);
+  for (int i = 0; i < bt.n; ++i) {
+    Prob& P = bt.p[i];
+    if (P.m == 0 || P.n == 0) {
+      P.tiles_m = P.tiles_n = 0;
+    }
+    if (P.splits > 1) {
+      P.ws = ws;
+      ws += (int64_t)P.splits * P.m * P.n;
+    }
+  }
+  int begin = 0;
+  bool any_split = false;
+  for (int i = 0; i < bt.n; ++i) {
+    bt.p[i].tile_begin = begin;
+    begin += bt.p[i].tiles_m * bt.p[i].tiles_n * bt.p[i].splits;
+    any_split = any_split || bt.p[i].splits > 1;
+  }
+  const int wgs = total_wgs(bt);
+  if (wgs == 0) return VKWR_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (cfg.bm == 32) hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 4>), dim3(wgs), dim3(256), 0, s, bt);
+  else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2>), dim3(wgs), dim3(256), 0, s, bt);
+  else if (cfg.bn == 128) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2>), dim3(wgs), dim3(256), 0, s, bt);
+  else hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2>), dim3(wgs), dim3(256), 0, s, bt);
+  if (int e = check_launch(fn)) return e;
+  if (any_split) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(256, bt.n), dim3(256), 0, s, bt);
+    if (int e = check_launch(fn)) return e;
+  }
+  return VKWR_OK;
+}
