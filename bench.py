@@ -42,6 +42,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target length of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model-steps", type=int, default=20,
+                    help="timed decode steps of the 1.5B-shape model at bs=128 (0: skip)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph (for counter runs); "
                          "skips the cache variants")
@@ -100,6 +102,56 @@ def capture(step_fn, n_steps, stream):
                 step_fn(i)
     torch.cuda.synchronize()
     return g
+
+
+def model_decode(dev, steps, warmup=3):
+    """the RWKV-7 1.5B-shape decode step (L=24, C=2048, random fp16
+    weights) for 128 sequences at T=1 from a 160-slot state pool.  One step is captured
+    into a HIP graph and replayed `steps` times (the recurrent state advances every
+    replay); HIP events on the replay stream time it."""
+    from vkwr_amd.model_executor import DecodeEngine, RWKV7Config, RWKV7Model, RWKV7State
+    from vkwr_amd.model_executor.rwkv7 import flops_per_step, gbytes_per_step
+
+    cfg = RWKV7Config.preset("1.5b")
+    B = 128
+    model = RWKV7Model(cfg, dev, seed=0)
+    state = RWKV7State(cfg, 160, dev, std=0.1, seed=1)
+    eng = DecodeEngine(model, B)
+    g = torch.Generator().manual_seed(3)
+    slots = torch.randperm(160, generator=g)[:B].to(torch.int32).to(dev)
+    tokens = torch.randint(0, cfg.vocab, (B,), generator=g, dtype=torch.int32).to(dev)
+    for _ in range(warmup):
+        eng.step(state, tokens, slots)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = capture(lambda i: eng.step(state, tokens, slots), 1, stream)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    nbytes = gbytes_per_step(cfg, B)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del graph
+    return {
+        "workload": "RWKV-7 1.5B-shape decode step (BASELINE config 3): L=24, C=2048, H=32, F=8192, "
+                    "ranks w/a/v/g 96/96/64/256, V=65536, bs=128, T=1, random-init fp16 weights, "
+                    "fp32 WKV state in a 160-slot pool",
+        "tokens_per_s": round(B / (ms * 1e-3), 1),
+        "ms_per_step": round(ms, 4),
+        "steps": steps,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": nbytes,
+                     "tokens_per_s_at_peak": round(B / (nbytes / (HBM_PEAK_GBS * 1e9)), 1)},
+        "gemm_tflops": round(flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
+        "timing": "one decode step captured as a HIP graph, replayed; HIP events on the replay stream",
+    }
 
 
 def cpu_baseline(target_s):
@@ -254,6 +306,10 @@ def main():
         "variants": variants,
         "cpu_baseline": None,
     }
+    if args.model_steps > 0 and not args.eager:
+        del inputs
+        torch.cuda.empty_cache()
+        result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -134,10 +134,15 @@ VKWR_EXPORT int vkwr_emb_ln0_bf16_to_f16(int64_t V, int C, const uint16_t* emb,
                                          float eps, uint16_t* out, void* stream);
 
 /* Decode-step fused residual add + LayerNorm + token-shift lerp (T = 1).
- *   x, residual [rows, C]; shift_state [rows, C] (in place); n_mix = 1 or 6
- *   mix vectors mix[i] [C]; outputs x_out [rows, C] = fp16(x + residual) and
- *   out[i] [rows, C] = fp16(y + (prev - y) * mix[i]), where y = fp16(LN(x + residual))
- *   and prev = shift_state at entry; then shift_state = y.
+ *   x, residual [rows, C] (residual may be NULL: zero); shift_state [*, C]
+ *   (in place); n_mix = 1 or 6 mix vectors mix[i] [C]; outputs
+ *   x_out [rows, C] = fp16(x + residual) and out[i] [rows, C] =
+ *   fp16(y + (prev - y) * mix[i]), where y = fp16(LN(x + residual)) and prev is
+ *   the shift_state row at entry; then that shift_state row = y.
+ *   x_rows (may be NULL) gathers x: row r reads x[x_rows[r]] (an embedding
+ *   lookup); shift_slots (may be NULL) maps row r to shift_state[shift_slots[r]]
+ *   (a per-sequence slot pool).  The caller guarantees both are in range and
+ *   shift_slots distinct.
  * Replaces add_layer_norm_cmix_mix_f16{,_cfg,_scalar_stats}_cuda and
  * add_layer_norm_tmix_mix6_f16{,_cfg,_scalar_stats}_cuda
  * (csrc/v1/norm/norm_ops.cu:1045-1340), reached from the vkwr_v1_norm ops of the
@@ -146,7 +151,9 @@ VKWR_EXPORT int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t*
                                             const uint16_t* residual, uint16_t* shift_state,
                                             const uint16_t* weight, const uint16_t* bias,
                                             int n_mix, const uint16_t* const* mix, float eps,
-                                            uint16_t* x_out, uint16_t* const* out, void* stream);
+                                            uint16_t* x_out, uint16_t* const* out,
+                                            const int32_t* x_rows, const int32_t* shift_slots,
+                                            void* stream);
 
 /* out = x + y elementwise (fp32 add, fp16 round), n elements.
  * Replaces add_f16_cuda (csrc/v1/norm/norm_ops.cu:866-876), reached from
@@ -241,13 +248,14 @@ enum {
 enum {
   VKWR_GEMM_EPI_NONE = 0,
   VKWR_GEMM_EPI_RELU_SQUARE = 1,    /* y = max(acc, 0)^2 */
-  VKWR_GEMM_EPI_VALUE_RESIDUAL = 2  /* y = v + (v_first - v) * sigmoid(v0[n] + acc) */
+  VKWR_GEMM_EPI_VALUE_RESIDUAL = 2, /* y = v + (v_first - v) * sigmoid(v0[n] + acc) */
+  VKWR_GEMM_EPI_BIAS = 3            /* y = acc + v0[n] */
 };
 
 /* One GEMM of a batch: c[m,n] = epilogue(sum_k act(a[m,k]) * B(k,n)), fp16
  * operands and output, fp32 accumulation.  a [m,k], c [m,n] and B are
  * contiguous row-major; v, v_first [m,n] and v0 [n] are read by the
- * value-residual epilogue only. */
+ * value-residual epilogue, v0 [n] by the bias epilogue. */
 typedef struct vkwr_gemm_problem {
   const uint16_t* a;
   const uint16_t* b;

@@ -1,0 +1,102 @@
+"""End-to-end RWKV-7 decode step (vkwr_amd.model_executor) against the
+float32 composition oracle (oracle/model_ref.py).
+
+Bar (north_star): end-to-end logits within max-abs 5e-2 of the float32 model;
+slots outside the batch bitwise unchanged.  The WKV op itself is bit-exact on
+identical inputs (tests/test_wkv_gpu.py); end to end its inputs differ from the
+oracle's by fp16 rounding flips of the intermediates (GEMM accumulation order),
+so the updated states are checked to the drift this produces: 1e-3 for the
+2-layer model, 2.5e-2 after 24 layers of the 1.5B shape (measured on MI355X:
+1.8e-3 at layer 0 rising to 1.0e-2 at layer 24, logits max-abs 2.4e-2 on
+logits of magnitude up to 5).
+"""
+import pytest
+import torch
+
+from oracle import model_ref
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 5e-2
+STATE_TOL = 1e-3
+
+
+def _setup(gpu, preset, B, P, seed=0):
+    from vkwr_amd.model_executor import RWKV7Config, RWKV7Model, RWKV7State, DecodeEngine
+    cfg = RWKV7Config.preset(preset)
+    model = RWKV7Model(cfg, gpu, seed=seed)
+    state = RWKV7State(cfg, P, gpu, std=0.1, seed=seed + 1)
+    eng = DecodeEngine(model, B)
+    g = torch.Generator().manual_seed(seed)
+    slots = torch.randperm(P, generator=g)[:B].to(torch.int32).to(gpu)
+    return cfg, model, state, eng, slots, g
+
+
+def test_tiny_model_matches_cpu_oracle_over_steps(gpu):
+    cfg, model, state, eng, slots, g = _setup(gpu, "tiny", B=4, P=9)
+    wkv = state.wkv.cpu().clone()
+    att, ffn = state.att_shift.cpu().clone(), state.ffn_shift.cpu().clone()
+    wkv_r, att_r, ffn_r = wkv.clone(), att.clone(), ffn.clone()
+    for step in range(3):
+        tokens = torch.randint(0, cfg.vocab, (4,), generator=g, dtype=torch.int32)
+        logits = eng.step(state, tokens.to(gpu), slots).float().cpu()
+        ref = model_ref.decode_step(model, wkv, att, ffn, tokens, slots.cpu(), round_fp16=True)
+        ref32 = model_ref.decode_step(model, wkv_r, att_r, ffn_r, tokens, slots.cpu(), round_fp16=False)
+        assert (logits - ref).abs().max() <= 1e-2, (step, float((logits - ref).abs().max()))
+        assert (logits - ref32).abs().max() <= LOGIT_TOL, (step, float((logits - ref32).abs().max()))
+        assert (state.wkv.cpu() - wkv).abs().max() <= STATE_TOL
+    others = [s for s in range(9) if s not in slots.cpu().tolist()]
+    assert torch.equal(state.wkv.cpu()[:, others], RWKV7StateInit(cfg, gpu)[:, others])
+
+
+def RWKV7StateInit(cfg, gpu):
+    """The untouched initial pool (same seed as _setup)."""
+    from vkwr_amd.model_executor import RWKV7State
+    return RWKV7State(cfg, 9, gpu, std=0.1, seed=1).wkv.cpu()
+
+
+def test_1p5b_decode_step_bs128_logits(gpu):
+    """BASELINE config 3 at full shape: L=24, C=2048, bs=128, one decode step, logits
+    and states against the float32 composition evaluated with torch on the GPU."""
+    cfg, model, state, eng, slots, g = _setup(gpu, "1.5b", B=128, P=160)
+    tokens = torch.randint(0, cfg.vocab, (128,), generator=g, dtype=torch.int32).to(gpu)
+    wkv = state.wkv.clone()
+    att, ffn = state.att_shift.clone(), state.ffn_shift.clone()
+    logits = eng.step(state, tokens, slots).float()
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        ref = model_ref.decode_step(model, wkv, att, ffn, tokens, slots, round_fp16=False)
+    err = (logits - ref).abs().max().item()
+    assert err <= LOGIT_TOL, err
+    sl = slots.long()
+    assert (state.wkv[:, sl] - wkv[:, sl]).abs().max().item() <= 2.5e-2
+    others = torch.ones(160, dtype=torch.bool, device=gpu)
+    others[sl] = False
+    assert torch.equal(state.wkv[:, others], wkv[:, others])  # untouched by both
+
+
+def test_decode_step_is_deterministic_and_graph_capturable(gpu):
+    cfg, model, state, eng, slots, g = _setup(gpu, "tiny", B=8, P=8)
+    tokens = torch.randint(0, cfg.vocab, (8,), generator=g, dtype=torch.int32).to(gpu)
+    s0 = [state.wkv.clone(), state.att_shift.clone(), state.ffn_shift.clone()]
+    eager = eng.step(state, tokens, slots).clone()
+    s1 = [state.wkv.clone(), state.att_shift.clone(), state.ffn_shift.clone()]
+    # reset and replay through a captured graph, several times, eager work in between
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    for t, v in zip((state.wkv, state.att_shift, state.ffn_shift), s0):
+        t.copy_(v)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            out = eng.step(state, tokens, slots)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for t, v in zip((state.wkv, state.att_shift, state.ffn_shift), s0):
+            t.copy_(v)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        for t, v in zip((state.wkv, state.att_shift, state.ffn_shift), s1):
+            assert torch.equal(t, v)

@@ -82,6 +82,7 @@ __device__ __forceinline__ float epilogue(const Prob& P, float acc, int row, int
     const float gate = sigmoidf((float)P.v0[col] + acc);
     return __builtin_fmaf((float)P.vf[i] - vv, gate, vv);
   }
+  if (P.epi == VKWR_GEMM_EPI_BIAS) return acc + (float)P.v0[col];
   return acc;
 }
 
@@ -338,12 +339,13 @@ int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, C
                "%s: problem %d too large", fn, i);
     VK_REQUIRE(q.b_layout == VKWR_GEMM_B_NK || q.b_layout == VKWR_GEMM_B_KN, "%s: bad b_layout", fn);
     VK_REQUIRE(q.a_act >= VKWR_GEMM_ACT_NONE && q.a_act <= VKWR_GEMM_ACT_RELU_SQUARE, "%s: bad a_act", fn);
-    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_GEMM_EPI_VALUE_RESIDUAL,
+    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_GEMM_EPI_BIAS,
                "%s: bad epilogue", fn);
     const bool empty = q.m == 0 || q.n == 0;
     VK_REQUIRE(empty || (q.a && q.b && q.c), "%s: null pointer in problem %d", fn, i);
     VK_REQUIRE(empty || q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL || (q.v && q.v_first && q.v0),
                "%s: value-residual epilogue needs v, v_first, v0", fn);
+    VK_REQUIRE(empty || q.epilogue != VKWR_GEMM_EPI_BIAS || q.v0, "%s: bias epilogue needs v0", fn);
     Prob& P = bt.p[i];
     P = Prob{};
     P.a = reinterpret_cast<const _Float16*>(q.a);

@@ -36,6 +36,8 @@ struct LnArgs {
   float eps;
   _Float16* x_out;  // may be null
   _Float16* y;      // plain mode output
+  const int32_t* x_rows;       // may be null: x row = row
+  const int32_t* shift_slots;  // may be null: shift row = row
   // mix mode
   _Float16* shift;
   const _Float16* mix[6];
@@ -60,8 +62,12 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int C = p.C;
-  const int64_t src = (row * p.src_mul + p.src_add) * (int64_t)C;
+  const int64_t xrow = p.x_rows ? (int64_t)p.x_rows[row] : row * p.src_mul + p.src_add;
+  const int64_t src = xrow * (int64_t)C;
+  const int64_t rrow = row * p.src_mul + p.src_add;  // residual row
+  const int64_t rsrc = rrow * (int64_t)C;
   const int64_t dst = row * (int64_t)C;
+  const int64_t sdst = (p.shift_slots ? (int64_t)p.shift_slots[row] : row) * (int64_t)C;
 
   float v[NV][VW];
   float sum = 0.0f;
@@ -74,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[n][e] = (float)xv.v[e];
         if (p.residual) {
-          const h8 rv = ld8(p.residual + src + c0);
+          const h8 rv = ld8(p.residual + rsrc + c0);
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)rv.v[e];
         }
@@ -82,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           v[n][e] = ld_in<kBf16>(p.x, src + c0 + e);
-          if (p.residual) v[n][e] = v[n][e] + (float)p.residual[src + c0 + e];
+          if (p.residual) v[n][e] = v[n][e] + (float)p.residual[rsrc + c0 + e];
         }
       }
 #pragma unroll
@@ -130,15 +136,15 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       // Token-shift lerp of the fp16-rounded LN output with the previous token's.
       _Float16 prev[VW];
       if constexpr (VW == 8) {
-        *reinterpret_cast<h8*>(prev) = ld8(p.shift + dst + c0);
+        *reinterpret_cast<h8*>(prev) = ld8(p.shift + sdst + c0);
         st8(p.x_out + dst + c0, *reinterpret_cast<const h8*>(xo));
-        st8(p.shift + dst + c0, *reinterpret_cast<const h8*>(yh));
+        st8(p.shift + sdst + c0, *reinterpret_cast<const h8*>(yh));
       } else {
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-          prev[e] = p.shift[dst + c0 + e];
+          prev[e] = p.shift[sdst + c0 + e];
           p.x_out[dst + c0 + e] = xo[e];
-          p.shift[dst + c0 + e] = yh[e];
+          p.shift[sdst + c0 + e] = yh[e];
         }
       }
 #pragma unroll
@@ -269,7 +275,8 @@ extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* 
                                            const uint16_t* residual, uint16_t* shift_state,
                                            const uint16_t* weight, const uint16_t* bias, int n_mix,
                                            const uint16_t* const* mix, float eps, uint16_t* x_out,
-                                           uint16_t* const* out, void* stream) {
+                                           uint16_t* const* out, const int32_t* x_rows,
+                                           const int32_t* shift_slots, void* stream) {
   clear_error();
   const char* fn = "vkwr_add_layer_norm_mix_f16";
   VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
@@ -285,15 +292,17 @@ extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* 
   p.eps = eps;
   p.x_out = reinterpret_cast<_Float16*>(x_out);
   p.shift = reinterpret_cast<_Float16*>(shift_state);
-  bool vec = aligned16(x) && aligned16(residual) && aligned16(shift_state) && aligned16(x_out);
+  p.x_rows = x_rows;
+  p.shift_slots = shift_slots;
+  bool vec = aligned16(x) && (!residual || aligned16(residual)) && aligned16(shift_state) &&
+             aligned16(x_out);
   for (int i = 0; i < n_mix; ++i) {
     VK_REQUIRE(rows == 0 || (mix[i] && out[i]), "%s: null pointer", fn);
     p.mix[i] = reinterpret_cast<const _Float16*>(mix[i]);
     p.out[i] = reinterpret_cast<_Float16*>(out[i]);
     vec = vec && aligned16(out[i]);
   }
-  VK_REQUIRE(rows == 0 || (x && residual && shift_state && weight && bias && x_out),
-             "%s: null pointer", fn);
+  VK_REQUIRE(rows == 0 || (x && shift_state && weight && bias && x_out), "%s: null pointer", fn);
   if (n_mix == 1) return launch_ln<1, false>(fn, p, vec, (hipStream_t)stream);
   return launch_ln<6, false>(fn, p, vec, (hipStream_t)stream);
 }
