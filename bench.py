@@ -44,6 +44,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--model-steps", type=int, default=20,
                     help="timed decode steps of the 1.5B-shape model at bs=128 (0: skip)")
+    ap.add_argument("--rowmajor-gemm", action="store_true",
+                    help="run the model decode step on the row-major GEMM instead of the frag GEMM")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph (for counter runs); "
                          "skips the cache variants")
@@ -104,7 +106,7 @@ def capture(step_fn, n_steps, stream):
     return g
 
 
-def model_decode(dev, steps, warmup=3):
+def model_decode(dev, steps, warmup=3, frag=True):
     """the RWKV-7 1.5B-shape decode step (L=24, C=2048, random fp16
     weights) for 128 sequences at T=1 from a 160-slot state pool.  One step is captured
     into a HIP graph and replayed `steps` times (the recurrent state advances every
@@ -116,7 +118,7 @@ def model_decode(dev, steps, warmup=3):
     B = 128
     model = RWKV7Model(cfg, dev, seed=0)
     state = RWKV7State(cfg, 160, dev, std=0.1, seed=1)
-    eng = DecodeEngine(model, B)
+    eng = DecodeEngine(model, B, frag=frag)
     g = torch.Generator().manual_seed(3)
     slots = torch.randperm(160, generator=g)[:B].to(torch.int32).to(dev)
     tokens = torch.randint(0, cfg.vocab, (B,), generator=g, dtype=torch.int32).to(dev)
@@ -150,6 +152,7 @@ def model_decode(dev, steps, warmup=3):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": nbytes,
                      "tokens_per_s_at_peak": round(B / (nbytes / (HBM_PEAK_GBS * 1e9)), 1)},
         "gemm_tflops": round(flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
+        "gemm_path": "frag (vkwr_frag_gemm_f16, weights packed at load)" if frag else "row-major (vkwr_gemm_f16)",
         "timing": "one decode step captured as a HIP graph, replayed; HIP events on the replay stream",
     }
 
@@ -309,7 +312,7 @@ def main():
     if args.model_steps > 0 and not args.eager:
         del inputs
         torch.cuda.empty_cache()
-        result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps)
+        result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

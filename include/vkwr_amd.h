@@ -284,6 +284,89 @@ VKWR_EXPORT int64_t vkwr_gemm_f16_workspace_bytes(int n_problems, const vkwr_gem
 VKWR_EXPORT int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, void* workspace,
                               int64_t workspace_bytes, void* stream);
 
+/* Frag-output variants of three producers: identical arithmetic to
+ * vkwr_add_layer_norm_mix_f16, vkwr_add_last_layer_norm_f16 and
+ * vkwr_tmix_groupnorm_bonus_gate_f16, but out[] / y / out are written as frag
+ * matrices [rows, C] (the layout defined below; C % 128 == 0, x_out and the
+ * shift state stay row-major), ready to be the activation of
+ * vkwr_frag_gemm_f16.  Rows pad and columns need no pad (C % 128 == 0); rows
+ * beyond `rows` are not written.  No counterpart in the reference: they let
+ * the decode executor feed its projections without a layout pass. */
+VKWR_EXPORT int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint16_t* x,
+                                                 const uint16_t* residual, uint16_t* shift_state,
+                                                 const uint16_t* weight, const uint16_t* bias,
+                                                 int n_mix, const uint16_t* const* mix, float eps,
+                                                 uint16_t* x_out, uint16_t* const* out,
+                                                 const int32_t* x_rows, const int32_t* shift_slots,
+                                                 void* stream);
+VKWR_EXPORT int vkwr_add_last_layer_norm_frag_f16(int B, int T, int C, const uint16_t* x,
+                                                  const uint16_t* residual, const uint16_t* weight,
+                                                  const uint16_t* bias, float eps, uint16_t* y,
+                                                  void* stream);
+VKWR_EXPORT int vkwr_tmix_groupnorm_bonus_gate_frag_f16(int B, int T, int C, int H, const uint16_t* x,
+                                                        const uint16_t* r, const uint16_t* k,
+                                                        const uint16_t* v, const uint16_t* r_k,
+                                                        const uint16_t* weight, const uint16_t* bias,
+                                                        const uint16_t* g, uint16_t* out, void* stream);
+
+/* ------------------------------------------------- fragment-layout GEMM
+ *
+ * Decode-step GEMMs (m <= a few hundred rows) are bound by streaming the
+ * weights once from HBM.  The fragment ("frag") layout stores a matrix X[R,K]
+ * (R = rows of the activation or output columns of the weight, K = the
+ * reduction dimension) in the operand order of v_mfma_f32_32x32x16_f16, so
+ * every wave-wide 16-byte-per-lane load is one contiguous kilobyte:
+ *   R_pad = roundup(R, 128), K_pad = roundup(K, 128), zero padded;
+ *   element (r, k) at half index
+ *     (((r / 32) * (K_pad / 16) + k / 16) * 64 + ((k / 8) % 2) * 32 + r % 32) * 8 + k % 8.
+ * No counterpart in the reference (it streams row-major weights through
+ * cuBLAS / its split-K kernels, csrc/v1/linear/linear_ops.cu:46-1833); the
+ * model executor packs its weights once at load and its producers write the
+ * activations feeding each projection directly in this layout. */
+
+#define VKWR_FRAG_PAD 128
+
+enum {
+  VKWR_FRAG_EPI_TANH = 4,   /* y = tanh(acc) (frag GEMM only) */
+  VKWR_FRAG_EPI_SIGMOID = 5 /* y = sigmoid(acc) (frag GEMM only) */
+};
+
+/* Packs src into frag layout: src is [rows, k] row-major (src_layout
+ * VKWR_GEMM_B_NK) or [k, rows] row-major (VKWR_GEMM_B_KN); dst holds
+ * roundup(rows,128) * roundup(k,128) halfs, pads written as zero. */
+VKWR_EXPORT int vkwr_frag_pack_f16(int64_t rows, int64_t k, const uint16_t* src, int src_layout,
+                                   uint16_t* dst, void* stream);
+
+/* Inverse of vkwr_frag_pack_f16 for the [rows, k] row-major case. */
+VKWR_EXPORT int vkwr_frag_unpack_f16(int64_t rows, int64_t k, const uint16_t* src, uint16_t* dst,
+                                     void* stream);
+
+/* One problem of a frag GEMM batch: c = epilogue(a . b^T) with a the frag
+ * activation [m, k], b the frag weight [n, k], fp32 accumulation.  c is
+ * row-major [m, n] (c_frag = 0) or a frag matrix [m, n] (c_frag = 1, ready to
+ * feed the next frag GEMM as its activation; the pad columns n..n_pad-1 are
+ * written too, as epilogue(0), and rows >= m are not written).  Epilogues:
+ * VKWR_GEMM_EPI_* (value residual and bias need c_frag = 0) or
+ * VKWR_FRAG_EPI_TANH / _SIGMOID. */
+typedef struct vkwr_frag_gemm_problem {
+  const uint16_t* a;
+  const uint16_t* b;
+  uint16_t* c;
+  int64_t m, n, k;
+  int epilogue;
+  int c_frag;
+  const uint16_t* v;
+  const uint16_t* v_first;
+  const uint16_t* v0;
+} vkwr_frag_gemm_problem;
+
+/* Runs 1..8 frag GEMMs in one launch (no workspace: the K split is inside
+ * each workgroup, reduced through LDS in a fixed order, so results are
+ * deterministic).  All pointers 16-byte aligned; n a multiple of 8 for
+ * row-major c.  No counterpart in the reference (see above). */
+VKWR_EXPORT int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* problems,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

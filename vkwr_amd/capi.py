@@ -26,12 +26,32 @@ _f = ctypes.c_float
 GEMM_B_NK, GEMM_B_KN = 0, 1
 ACT_NONE, ACT_TANH, ACT_SIGMOID, ACT_RELU_SQUARE = 0, 1, 2, 3
 EPI_NONE, EPI_RELU_SQUARE, EPI_VALUE_RESIDUAL, EPI_BIAS = 0, 1, 2, 3
+EPI_TANH, EPI_SIGMOID = 4, 5  # frag GEMM only
 MAX_GEMM_PROBLEMS = 8
+FRAG_PAD = 128
+
+
+def frag_pad(x):
+    """Padded extent of a frag-matrix dimension (rows and K: multiples of 128)."""
+    return (x + FRAG_PAD - 1) // FRAG_PAD * FRAG_PAD
+
+
+def frag_empty(rows, k, device, zero=True):
+    """A frag matrix [rows, k] (flat fp16 storage of frag_pad(rows) * frag_pad(k)
+    halfs).  Zero-filled by default: producers never write the K pad, and the
+    frag GEMM needs it finite."""
+    n = frag_pad(rows) * frag_pad(k)
+    return (torch.zeros if zero else torch.empty)(n, dtype=torch.float16, device=device)
 
 
 class GemmProblem(ctypes.Structure):
     _fields_ = [("a", _p), ("b", _p), ("c", _p), ("m", _i64), ("n", _i64), ("k", _i64),
                 ("b_layout", _i), ("a_act", _i), ("epilogue", _i), ("v", _p), ("v_first", _p), ("v0", _p)]
+
+
+class FragProblem(ctypes.Structure):
+    _fields_ = [("a", _p), ("b", _p), ("c", _p), ("m", _i64), ("n", _i64), ("k", _i64),
+                ("epilogue", _i), ("c_frag", _i), ("v", _p), ("v_first", _p), ("v0", _p)]
 
 
 def _sig(name, args, res=_i):
@@ -52,6 +72,13 @@ _gate = _sig("vkwr_tmix_kk_a_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p,
 _gn = _sig("vkwr_tmix_groupnorm_bonus_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _wkv_slots = _sig("vkwr_wkv7_fp32_forward_slots",
                   [_i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p])
+_frag_gemm = _sig("vkwr_frag_gemm_f16", [_i, ctypes.POINTER(FragProblem), _p])
+_frag_pack = _sig("vkwr_frag_pack_f16", [_i64, _i64, _p, _i, _p, _p])
+_frag_unpack = _sig("vkwr_frag_unpack_f16", [_i64, _i64, _p, _p, _p])
+_ln_mix_frag = _sig("vkwr_add_layer_norm_mix_frag_f16",
+                    [_i64, _i, _p, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p, _p, _p])
+_ln_last_frag = _sig("vkwr_add_last_layer_norm_frag_f16", [_i, _i, _i, _p, _p, _p, _p, _f, _p, _p])
+_gn_frag = _sig("vkwr_tmix_groupnorm_bonus_gate_frag_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _shift = _sig("vkwr_token_shift_mix_f16", [_i, _i, _i, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 
 
@@ -100,14 +127,16 @@ def gemm(problems, workspace):
 
 
 def add_layer_norm_mix(x, residual, shift_state, weight, bias, mixes, x_out, outs, eps=1e-5,
-                       x_rows=None, shift_slots=None):
+                       x_rows=None, shift_slots=None, frag=False):
+    """frag=True: outs are frag matrices [rows, C] (see frag_empty)."""
     rows = x_out.shape[0]
     C = x_out.shape[-1]
     mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
-    _check(_ln_mix(rows, C, _ptr(x), _ptr(residual), _ptr(shift_state), _ptr(weight), _ptr(bias), len(mixes),
-                   mp, eps, _ptr(x_out), op, _ptr(x_rows), _ptr(shift_slots), _stream()),
-           "vkwr_add_layer_norm_mix_f16")
+    fn = _ln_mix_frag if frag else _ln_mix
+    _check(fn(rows, C, _ptr(x), _ptr(residual), _ptr(shift_state), _ptr(weight), _ptr(bias), len(mixes),
+              mp, eps, _ptr(x_out), op, _ptr(x_rows), _ptr(shift_slots), _stream()),
+           "vkwr_add_layer_norm_mix%s_f16" % ("_frag" if frag else ""))
 
 
 def layer_norm(x, weight, bias, y, eps=1e-5, residual=None, x_out=None):
@@ -116,9 +145,10 @@ def layer_norm(x, weight, bias, y, eps=1e-5, residual=None, x_out=None):
                _stream()), "vkwr_layer_norm_f16")
 
 
-def add_last_layer_norm(B, T, C, x, residual, weight, bias, y, eps=1e-5):
-    _check(_ln_last(B, T, C, _ptr(x), _ptr(residual), _ptr(weight), _ptr(bias), eps, _ptr(y), _stream()),
-           "vkwr_add_last_layer_norm_f16")
+def add_last_layer_norm(B, T, C, x, residual, weight, bias, y, eps=1e-5, frag=False):
+    fn = _ln_last_frag if frag else _ln_last
+    _check(fn(B, T, C, _ptr(x), _ptr(residual), _ptr(weight), _ptr(bias), eps, _ptr(y), _stream()),
+           "vkwr_add_last_layer_norm%s_f16" % ("_frag" if frag else ""))
 
 
 def kk_a_gate(B, T, C, H, k, k_k, a0, a12, k_a, new_k, neg_kk, kka, x=None, shift_state=None):
@@ -126,9 +156,42 @@ def kk_a_gate(B, T, C, H, k, k_k, a0, a12, k_a, new_k, neg_kk, kka, x=None, shif
                  _ptr(new_k), _ptr(neg_kk), _ptr(kka), _stream()), "vkwr_tmix_kk_a_gate_f16")
 
 
-def groupnorm_bonus_gate(B, T, C, H, x, r, k, v, r_k, weight, bias, g, out):
-    _check(_gn(B, T, C, H, _ptr(x), _ptr(r), _ptr(k), _ptr(v), _ptr(r_k), _ptr(weight), _ptr(bias), _ptr(g),
-               _ptr(out), _stream()), "vkwr_tmix_groupnorm_bonus_gate_f16")
+def groupnorm_bonus_gate(B, T, C, H, x, r, k, v, r_k, weight, bias, g, out, frag=False):
+    fn = _gn_frag if frag else _gn
+    _check(fn(B, T, C, H, _ptr(x), _ptr(r), _ptr(k), _ptr(v), _ptr(r_k), _ptr(weight), _ptr(bias), _ptr(g),
+              _ptr(out), _stream()), "vkwr_tmix_groupnorm_bonus_gate%s_f16" % ("_frag" if frag else ""))
+
+
+def frag_pack(src, rows, k, dst, src_layout=GEMM_B_NK):
+    """Pack src ([rows,k] row-major, or [k,rows] with GEMM_B_KN) into the frag matrix dst."""
+    assert src.dtype == torch.float16 and src.is_contiguous() and src.numel() == rows * k
+    assert dst.numel() >= frag_pad(rows) * frag_pad(k)
+    _check(_frag_pack(rows, k, _ptr(src), src_layout, _ptr(dst), _stream()), "vkwr_frag_pack_f16")
+
+
+def frag_unpack(src, rows, k, dst):
+    assert dst.numel() == rows * k and dst.is_contiguous()
+    _check(_frag_unpack(rows, k, _ptr(src), _ptr(dst), _stream()), "vkwr_frag_unpack_f16")
+
+
+def frag_problem(a, b, c, m, n, k, epilogue=EPI_NONE, c_frag=False, v=None, v_first=None, v0=None):
+    """One frag GEMM: c = epilogue(a . b^T); a frag [m,k], b frag [n,k]; c row-major [m,n] or frag."""
+    assert a.numel() >= frag_pad(m) * frag_pad(k), (a.numel(), m, k)
+    assert b.numel() >= frag_pad(n) * frag_pad(k), (b.numel(), n, k)
+    assert c.numel() >= (frag_pad(m) * frag_pad(n) if c_frag else m * n)
+    return FragProblem(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, epilogue, 1 if c_frag else 0,
+                       _ptr(v), _ptr(v_first), _ptr(v0))
+
+
+def frag_gemm(problems):
+    """Runs 1..8 frag GEMMs in one launch."""
+    arr = _arr_frag(problems)
+    _check(_frag_gemm(len(problems), arr, _stream()), "vkwr_frag_gemm_f16")
+
+
+def _arr_frag(problems):
+    assert 1 <= len(problems) <= MAX_GEMM_PROBLEMS
+    return (FragProblem * len(problems))(*problems)
 
 
 def wkv_slots(B, T, C, H, pool, slots, r, w, k, v, a, b, y):

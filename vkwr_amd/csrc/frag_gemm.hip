@@ -1,0 +1,400 @@
+// Decode-step GEMM on fragment-layout operands: c = epilogue(a . b^T).
+//
+// At decode the activation a has few rows (one per sequence, m <= a few
+// hundred) and every weight byte is used m times, so the GEMM is bound by
+// streaming the weights once from HBM.  Two things decide how close to that
+// bound a gfx950 kernel gets:
+//
+//  * Load efficiency.  The A and B operands of v_mfma_f32_32x32x16_f16 give
+//    lane l the 8 halfs (row l % 32, k 8*(l / 32)..+7) of a 32 x 16 tile; read
+//    from a row-major matrix each wave load touches 32 rows x 32 bytes.  In the
+//    frag layout (vk_common.cuh frag_index) that tile is one contiguous
+//    kilobyte, so every load is fully coalesced and needs no LDS staging.
+//    Weights are packed once at model load; the producers of each projection
+//    input write it directly in frag layout.
+//
+//  * Parallelism without a K-split workspace.  A workgroup owns one
+//    (32 TM) x (32 TN) output tile over the whole of K; its NW waves take the
+//    16 KS-wide k blocks w, w + NW, ... with a two-deep register pipeline
+//    (loads are issued unconditionally -- the last block's index is clamped --
+//    so the compiler's wait counts stay exact), and the NW partial tiles are
+//    added through LDS in wave order after one barrier.  Deterministic, no
+//    second kernel, no fp32 partials in HBM.
+//
+// When a problem has several row tiles, the row tiles of one column tile are
+// given workgroup ids that differ by multiples of 8: gfx950 dispatches
+// workgroups round-robin over its 8 XCDs, so they share an L2 and the second
+// read of the weight tile hits it.
+//
+// Roofline: HBM-bound; algorithmic bytes = n*k*2 (weights) + m*k*2 + m*n*2.
+
+#include <algorithm>
+
+#include "vk_capi.h"
+#include "vk_common.cuh"
+
+namespace vk {
+namespace {
+
+typedef _Float16 hv8 __attribute__((ext_vector_type(8)));
+typedef float fv16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMaxFragProblems = 8;
+
+struct FProb {
+  const _Float16* a;
+  const _Float16* b;
+  _Float16* c;
+  const _Float16 *v, *vf, *v0;
+  int m, n, npad, kpad;
+  int epi, c_frag;
+  int ncol, nmb;            // column tiles, row tiles
+  int wg_begin;             // first workgroup id (multiple of 8)
+  int xcd_map;              // row tiles of a column tile share an XCD
+};
+
+struct FBatch {
+  int n;
+  FProb p[kMaxFragProblems];
+};
+
+__device__ __forceinline__ float apply_act(int epi, float x) {
+  if (epi == VKWR_GEMM_EPI_RELU_SQUARE) {
+    const float r = fmaxf(x, 0.0f);
+    return r * r;
+  }
+  if (epi == VKWR_FRAG_EPI_TANH) return tanhf(x);
+  if (epi == VKWR_FRAG_EPI_SIGMOID) return sigmoidf(x);
+  return x;
+}
+
+template <int TM, int TN, int NW, int KS>
+__global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
+  constexpr int kTiles = TM * TN;
+  __shared__ float red[NW * kTiles * 1024];
+
+  // ---- problem and tile of this workgroup (uniform)
+  const int wg = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxFragProblems; ++i)
+    if (i < bt.n && wg >= bt.p[i].wg_begin) pi = i;
+  const FProb& P = bt.p[pi];
+  const int lt = wg - P.wg_begin;
+  if (lt >= P.ncol * P.nmb) return;  // round-up workgroup
+  int cb, mb;
+  if (P.xcd_map) {
+    const int x = lt & 7, t = lt >> 3;
+    cb = (t / P.nmb) * 8 + x;
+    mb = t % P.nmb;
+  } else {
+    cb = lt / P.nmb;
+    mb = lt % P.nmb;
+  }
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t kstep = P.kpad >> 4;  // 16-k steps per 32-row block
+  const _Float16* ap[TM];
+  const _Float16* bp[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) ap[i] = P.a + ((int64_t)(mb * TM + i) * kstep * 64 + lane) * 8;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bp[j] = P.b + ((int64_t)(cb * TN + j) * kstep * 64 + lane) * 8;
+
+  fv16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nper = P.kpad / (16 * KS * NW);  // k blocks per wave (host guarantees >= 1, exact)
+  hv8 fa[2][KS][TM], fb[2][KS][TN];
+  auto load = [&](int buf, int j) {
+    j = j < nper ? j : nper - 1;
+    const int64_t o = (int64_t)(wave + NW * j) * KS * 512;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj) fb[buf][s][jj] = *reinterpret_cast<const hv8*>(bp[jj] + o + s * 512);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[buf][s][i] = *reinterpret_cast<const hv8*>(ap[i] + o + s * 512);
+    }
+  };
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][s][i], fb[buf][s][j], acc[i][j], 0, 0, 0);
+  };
+  // The scheduling barriers keep each prefetch ahead of the MFMAs that do not
+  // need it (left alone, the scheduler sinks the loads below them).
+  load(0, 0);
+  for (int j = 0; j + 1 < nper; j += 2) {
+    load(1, j + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(0, j + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (nper & 1) compute(0);
+
+  // ---- reduce the NW partial tiles in wave order, then 8 columns per thread
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[((wave * kTiles + t) * 16 + r) * 64 + lane] = acc[t / TN][t % TN][r];
+  __syncthreads();
+  constexpr int kGroups = kTiles * 16 * 8;
+  for (int g = threadIdx.x; g < kGroups; g += NW * 64) {
+    const int t = g >> 7, r = (g >> 3) & 15, l0 = (g & 7) * 8;
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = red[(t * 16 + r) * 64 + l0 + e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] += red[((w * kTiles + t) * 16 + r) * 64 + l0 + e];
+    const int i = t / TN, j = t % TN;
+    const int row = (mb * TM + i) * 32 + 8 * (r >> 2) + 4 * (l0 >> 5) + (r & 3);
+    const int col = (cb * TN + j) * 32 + (l0 & 31);
+    if (row >= P.m) continue;
+    h8 o;
+    if (P.c_frag) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(P.epi, s[e]);
+      st8(P.c + frag_index(row, col, P.npad), o);
+      continue;
+    }
+    if (col >= P.n) continue;
+    const int64_t idx = (int64_t)row * P.n + col;
+    if (P.epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+      const h8 vv = ld8(P.v + idx), vf = ld8(P.vf + idx), v0 = ld8(P.v0 + col);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (float)vv.v[e];
+        const float gate = sigmoidf((float)v0.v[e] + s[e]);
+        o.v[e] = (_Float16)__builtin_fmaf((float)vf.v[e] - x, gate, x);
+      }
+    } else if (P.epi == VKWR_GEMM_EPI_BIAS) {
+      const h8 v0 = ld8(P.v0 + col);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)(s[e] + (float)v0.v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(P.epi, s[e]);
+    }
+    st8(P.c + idx, o);
+  }
+}
+
+// ---------------------------------------------------------------- packing
+
+__global__ __launch_bounds__(256) void frag_pack_kernel(int64_t rows, int64_t k, const _Float16* src, int kn,
+                                                        int64_t kpad, int64_t nchunks, int vec,
+                                                        _Float16* dst) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t ci = (int64_t)blockIdx.x * 256 + threadIdx.x; ci < nchunks; ci += stride) {
+    const int lane = (int)(ci & 63);
+    const int64_t fs = ci >> 6;
+    const int64_t rb = fs / (kpad >> 4), ks = fs % (kpad >> 4);
+    const int64_t r = rb * 32 + (lane & 31);
+    const int64_t k0 = ks * 16 + (lane >> 5) * 8;
+    h8 o;
+    if (!kn && vec && r < rows && k0 + 8 <= k) {
+      o = ld8(src + r * k + k0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t kk = k0 + e;
+        o.v[e] = (r < rows && kk < k) ? (kn ? src[kk * rows + r] : src[r * k + kk]) : (_Float16)0.0f;
+      }
+    }
+    st8(dst + ci * 8, o);
+  }
+}
+
+__global__ __launch_bounds__(256) void frag_unpack_kernel(int64_t rows, int64_t k, const _Float16* src,
+                                                          int64_t kpad, _Float16* dst) {
+  const int64_t n = rows * k;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / k, kk = i % k;
+    dst[i] = src[frag_index(r, kk, kpad)];
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+unsigned grid_blocks(int64_t work) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((work + 255) / 256, 8192));
+}
+
+// ---------------------------------------------------------------- dispatch
+
+struct FragConfig {
+  int tm, tn, nw, ks;
+};
+
+int tiles_for(const FBatch& bt, int bm, int bn) {
+  int t = 0;
+  for (int i = 0; i < bt.n; ++i) t += (bt.p[i].m + bm - 1) / bm * (bt.p[i].npad / bn);
+  return t;
+}
+
+// One configuration per launch.  Large batches of tiles take 128 x 64 tiles;
+// medium ones 64 x 64; small ones (fewer than 128 such tiles: too few
+// workgroups for 256 CUs) 32 x 32 with more K per block.
+FragConfig pick_frag_config(const FBatch& bt) {
+  int max_m = 0;
+  int64_t kdiv = 0;  // gcd of the padded K
+  for (int i = 0; i < bt.n; ++i) {
+    max_m = std::max(max_m, bt.p[i].m);
+    int64_t a = kdiv, b = bt.p[i].kpad;
+    while (b) { const int64_t t = a % b; a = b; b = t; }
+    kdiv = a;
+  }
+  auto ks_for = [&](int nw, int ks_max) {
+    int ks = ks_max;
+    while (ks > 1 && kdiv % (16 * ks * nw) != 0) ks /= 2;
+    return ks;
+  };
+  if (max_m <= 32) {
+    if (tiles_for(bt, 32, 64) >= 128) return {1, 2, 8, ks_for(8, 2)};
+    return {1, 1, 8, ks_for(8, 4)};
+  }
+  const int t64 = tiles_for(bt, 64, 64);
+  if (t64 >= 1024) return {4, 2, 4, 2};
+  if (t64 >= 128) return {2, 2, 8, ks_for(8, 2)};
+  return {1, 1, 8, ks_for(8, 4)};
+}
+
+template <int TM, int TN, int NW, int KS>
+void launch_cfg(const FBatch& bt, int wgs, hipStream_t s) {
+  hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS>), dim3(wgs), dim3(NW * 64), 0, s, bt);
+}
+
+int launch_frag(const FBatch& bt, FragConfig c, int wgs, hipStream_t s) {
+#define VK_FRAG_CASE(a, b_, c_, d)                                        \
+  if (c.tm == a && c.tn == b_ && c.nw == c_ && c.ks == d) {               \
+    launch_cfg<a, b_, c_, d>(bt, wgs, s);                                 \
+    return VKWR_OK;                                                       \
+  }
+  VK_FRAG_CASE(4, 2, 4, 2)
+  VK_FRAG_CASE(2, 2, 8, 2)
+  VK_FRAG_CASE(2, 2, 8, 1)
+  VK_FRAG_CASE(1, 1, 8, 4)
+  VK_FRAG_CASE(1, 1, 8, 2)
+  VK_FRAG_CASE(1, 1, 8, 1)
+  VK_FRAG_CASE(1, 2, 8, 2)
+  VK_FRAG_CASE(1, 2, 8, 1)
+#undef VK_FRAG_CASE
+  set_error("vkwr_frag_gemm_f16: no kernel for tile config %dx%dx%dx%d", c.tm, c.tn, c.nw, c.ks);
+  return VKWR_ERR_INVALID;
+}
+
+}  // namespace
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" int vkwr_frag_pack_f16(int64_t rows, int64_t k, const uint16_t* src, int src_layout,
+                                  uint16_t* dst, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_frag_pack_f16";
+  VK_REQUIRE(rows >= 0 && k >= 0, "%s: negative size", fn);
+  VK_REQUIRE(src_layout == VKWR_GEMM_B_NK || src_layout == VKWR_GEMM_B_KN, "%s: bad src_layout", fn);
+  if (rows == 0 || k == 0) return VKWR_OK;
+  VK_REQUIRE(src && dst, "%s: null pointer", fn);
+  VK_REQUIRE(aligned16(dst), "%s: dst must be 16-byte aligned", fn);
+  const int64_t kpad = frag_pad(k), rpad = frag_pad(rows);
+  const int64_t nchunks = rpad * kpad / 8;
+  const int vec = src_layout == VKWR_GEMM_B_NK && k % 8 == 0 && aligned16(src);
+  hipLaunchKernelGGL(frag_pack_kernel, dim3(grid_blocks(nchunks)), dim3(256), 0, (hipStream_t)stream, rows, k,
+                     reinterpret_cast<const _Float16*>(src), src_layout == VKWR_GEMM_B_KN, kpad, nchunks, vec,
+                     reinterpret_cast<_Float16*>(dst));
+  return check_launch(fn);
+}
+
+extern "C" int vkwr_frag_unpack_f16(int64_t rows, int64_t k, const uint16_t* src, uint16_t* dst,
+                                    void* stream) {
+  clear_error();
+  const char* fn = "vkwr_frag_unpack_f16";
+  VK_REQUIRE(rows >= 0 && k >= 0, "%s: negative size", fn);
+  if (rows == 0 || k == 0) return VKWR_OK;
+  VK_REQUIRE(src && dst, "%s: null pointer", fn);
+  hipLaunchKernelGGL(frag_unpack_kernel, dim3(grid_blocks(rows * k)), dim3(256), 0, (hipStream_t)stream, rows, k,
+                     reinterpret_cast<const _Float16*>(src), frag_pad(k), reinterpret_cast<_Float16*>(dst));
+  return check_launch(fn);
+}
+
+extern "C" int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* problems, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_frag_gemm_f16";
+  VK_REQUIRE(n_problems >= 1 && n_problems <= kMaxFragProblems, "%s: 1..%d problems per launch (got %d)", fn,
+             kMaxFragProblems, n_problems);
+  VK_REQUIRE(problems != nullptr, "%s: null problem list", fn);
+  FBatch bt;
+  bt.n = 0;
+  for (int i = 0; i < n_problems; ++i) {
+    const vkwr_frag_gemm_problem& q = problems[i];
+    VK_REQUIRE(q.m >= 0 && q.n >= 0 && q.k >= 0, "%s: negative size in problem %d", fn, i);
+    VK_REQUIRE(q.m <= (1 << 20) && q.n <= (1 << 24) && q.k <= (1 << 20), "%s: problem %d too large", fn, i);
+    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_FRAG_EPI_SIGMOID, "%s: bad epilogue", fn);
+    VK_REQUIRE(q.c_frag == 0 || q.c_frag == 1, "%s: bad c_frag", fn);
+    if (q.m == 0 || q.n == 0) continue;
+    VK_REQUIRE(q.k > 0, "%s: k == 0 in problem %d", fn, i);
+    VK_REQUIRE(q.a && q.b && q.c, "%s: null pointer in problem %d", fn, i);
+    VK_REQUIRE(aligned16(q.a) && aligned16(q.b) && aligned16(q.c), "%s: operands must be 16-byte aligned", fn);
+    if (q.c_frag) {
+      VK_REQUIRE(q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL && q.epilogue != VKWR_GEMM_EPI_BIAS,
+                 "%s: value-residual / bias epilogues need a row-major output", fn);
+    } else {
+      VK_REQUIRE(q.n % 8 == 0, "%s: row-major output needs n %% 8 == 0 (problem %d)", fn, i);
+    }
+    if (q.epilogue == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+      VK_REQUIRE(q.v && q.v_first && q.v0, "%s: value-residual epilogue needs v, v_first, v0", fn);
+      VK_REQUIRE(aligned16(q.v) && aligned16(q.v_first) && aligned16(q.v0), "%s: epilogue operands alignment", fn);
+    }
+    if (q.epilogue == VKWR_GEMM_EPI_BIAS) {
+      VK_REQUIRE(q.v0 && aligned16(q.v0), "%s: bias epilogue needs an aligned v0", fn);
+    }
+    FProb& P = bt.p[bt.n++];
+    P = FProb{};
+    P.a = reinterpret_cast<const _Float16*>(q.a);
+    P.b = reinterpret_cast<const _Float16*>(q.b);
+    P.c = reinterpret_cast<_Float16*>(q.c);
+    P.v = reinterpret_cast<const _Float16*>(q.v);
+    P.vf = reinterpret_cast<const _Float16*>(q.v_first);
+    P.v0 = reinterpret_cast<const _Float16*>(q.v0);
+    P.m = (int)q.m;
+    P.n = (int)q.n;
+    P.npad = (int)frag_pad(q.n);
+    P.kpad = (int)frag_pad(q.k);
+    P.epi = q.epilogue;
+    P.c_frag = q.c_frag;
+  }
+  if (bt.n == 0) return VKWR_OK;
+  const FragConfig cfg = pick_frag_config(bt);
+  const int bm = 32 * cfg.tm, bn = 32 * cfg.tn;
+  int begin = 0;
+  for (int i = 0; i < bt.n; ++i) {
+    FProb& P = bt.p[i];
+    VK_REQUIRE(P.kpad % (16 * cfg.ks * cfg.nw) == 0, "%s: internal: K split", fn);
+    P.ncol = P.npad / bn;
+    P.nmb = (P.m + bm - 1) / bm;
+    P.wg_begin = begin;
+    P.xcd_map = P.nmb > 1 && P.ncol % 8 == 0;
+    const int wgs = P.ncol * P.nmb;
+    begin += (wgs + 7) / 8 * 8;
+  }
+  if (int e = launch_frag(bt, cfg, begin, (hipStream_t)stream)) return e;
+  return check_launch(fn);
+}

@@ -137,6 +137,7 @@ struct GnArgs {
   int64_t heads;
   const _Float16 *x, *r, *k, *v, *r_k, *w, *b, *g;
   _Float16* out;
+  int out_frag;  // out in frag layout (row = token, K = C)
 };
 
 __global__ __launch_bounds__(256) void groupnorm_bonus_gate_kernel(GnArgs p) {
@@ -154,7 +155,8 @@ __global__ __launch_bounds__(256) void groupnorm_bonus_gate_kernel(GnArgs p) {
   const float rkv = wave_sum((float)p.r[idx] * (float)p.k[idx] * (float)p.r_k[c]);
   float y = __builtin_fmaf(d * rstd, (float)p.w[c], (float)p.b[c]);
   y = __builtin_fmaf(rkv, (float)p.v[idx], y);
-  p.out[idx] = (_Float16)(y * (float)p.g[idx]);
+  const int64_t o = p.out_frag ? frag_index(head / p.H, c, (int64_t)p.H * kHead) : idx;
+  p.out[o] = (_Float16)(y * (float)p.g[idx]);
 }
 
 __global__ __launch_bounds__(256) void vres_gate_kernel(int64_t n, int C, const _Float16* v,
@@ -291,13 +293,10 @@ extern "C" int vkwr_tmix_kk_a_gate_f16(int B, int T, int C, int H, const uint16_
   return check_launch(fn);
 }
 
-extern "C" int vkwr_tmix_groupnorm_bonus_gate_f16(int B, int T, int C, int H, const uint16_t* x,
-                                                  const uint16_t* r, const uint16_t* k,
-                                                  const uint16_t* v, const uint16_t* r_k,
-                                                  const uint16_t* weight, const uint16_t* bias,
-                                                  const uint16_t* g, uint16_t* out, void* stream) {
-  clear_error();
-  const char* fn = "vkwr_tmix_groupnorm_bonus_gate_f16";
+namespace {
+int groupnorm_bonus_gate(const char* fn, int B, int T, int C, int H, const uint16_t* x, const uint16_t* r,
+                         const uint16_t* k, const uint16_t* v, const uint16_t* r_k, const uint16_t* weight,
+                         const uint16_t* bias, const uint16_t* g, uint16_t* out, int frag, void* stream) {
   VK_REQUIRE(B >= 0 && T >= 0 && H >= 0, "%s: negative size", fn);
   VK_REQUIRE(C == H * kHead, "%s: only head size 64 is supported (C=%d H=%d)", fn, C, H);
   const int64_t heads = (int64_t)B * T * H;
@@ -308,12 +307,34 @@ extern "C" int vkwr_tmix_groupnorm_bonus_gate_f16(int B, int T, int C, int H, co
            reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
            reinterpret_cast<const _Float16*>(r_k), reinterpret_cast<const _Float16*>(weight),
            reinterpret_cast<const _Float16*>(bias), reinterpret_cast<const _Float16*>(g),
-           reinterpret_cast<_Float16*>(out)};
+           reinterpret_cast<_Float16*>(out), frag};
+  VK_REQUIRE(!frag || C % kFragPad == 0, "%s: frag output needs C %% %d == 0", fn, kFragPad);
   const int64_t blocks = (heads + 3) / 4;
   VK_REQUIRE(blocks <= 0x7fffffff, "%s: too many heads", fn);
   hipLaunchKernelGGL(groupnorm_bonus_gate_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      (hipStream_t)stream, p);
   return check_launch(fn);
+}
+}  // namespace
+
+extern "C" int vkwr_tmix_groupnorm_bonus_gate_f16(int B, int T, int C, int H, const uint16_t* x,
+                                                  const uint16_t* r, const uint16_t* k,
+                                                  const uint16_t* v, const uint16_t* r_k,
+                                                  const uint16_t* weight, const uint16_t* bias,
+                                                  const uint16_t* g, uint16_t* out, void* stream) {
+  clear_error();
+  return groupnorm_bonus_gate("vkwr_tmix_groupnorm_bonus_gate_f16", B, T, C, H, x, r, k, v, r_k, weight, bias,
+                              g, out, 0, stream);
+}
+
+extern "C" int vkwr_tmix_groupnorm_bonus_gate_frag_f16(int B, int T, int C, int H, const uint16_t* x,
+                                                       const uint16_t* r, const uint16_t* k,
+                                                       const uint16_t* v, const uint16_t* r_k,
+                                                       const uint16_t* weight, const uint16_t* bias,
+                                                       const uint16_t* g, uint16_t* out, void* stream) {
+  clear_error();
+  return groupnorm_bonus_gate("vkwr_tmix_groupnorm_bonus_gate_frag_f16", B, T, C, H, x, r, k, v, r_k, weight,
+                              bias, g, out, 1, stream);
 }
 
 extern "C" int vkwr_tmix_vres_gate_f16(int64_t rows, int C, const uint16_t* v,

@@ -42,6 +42,7 @@ struct LnArgs {
   _Float16* shift;
   const _Float16* mix[6];
   _Float16* out[6];
+  int out_frag;  // y / out[] in frag layout (row blocks of 32, K = C; needs VW == 8)
 };
 
 template <bool kBf16>
@@ -121,9 +122,10 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       yh[e] = (_Float16)__builtin_fmaf(t, ld_in<kBf16>(p.weight, c0 + e), ld_in<kBf16>(p.bias, c0 + e));
       xo[e] = (_Float16)v[n][e];
     }
+    const int64_t odst = p.out_frag ? frag_index(row, c0, C) : dst + c0;  // y / out[] element offset
     if constexpr (NMIX == 0) {
       if constexpr (VW == 8) {
-        st8(p.y + dst + c0, *reinterpret_cast<const h8*>(yh));
+        st8(p.y + odst, *reinterpret_cast<const h8*>(yh));
         if (p.x_out) st8(p.x_out + dst + c0, *reinterpret_cast<const h8*>(xo));
       } else {
 #pragma unroll
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
           o[e] = (_Float16)__builtin_fmaf((float)prev[e] - yv, (float)p.mix[i][c0 + e], yv);
         }
         if constexpr (VW == 8) {
-          st8(p.out[i] + dst + c0, *reinterpret_cast<const h8*>(o));
+          st8(p.out[i] + odst, *reinterpret_cast<const h8*>(o));
         } else {
 #pragma unroll
           for (int e = 0; e < VW; ++e) p.out[i][dst + c0 + e] = o[e];
@@ -189,6 +191,8 @@ int launch_ln(const char* fn, const LnArgs& p, bool vec_ok, hipStream_t stream) 
   VK_REQUIRE(p.C > 0 && p.C <= kMaxC, "%s: unsupported C=%d (need 0 < C <= 8192)", fn, p.C);
   VK_REQUIRE(p.rows >= 0 && p.rows <= 0x7fffffff, "%s: too many rows", fn);
   if (p.rows == 0) return VKWR_OK;
+  VK_REQUIRE(!p.out_frag || (vec_ok && p.C % kFragPad == 0),
+             "%s: frag output needs C %% %d == 0 and 16-byte aligned rows", fn, kFragPad);
   const dim3 grid((unsigned)p.rows), block(kThreads);
   if (vec_ok && p.C % 8 == 0) {
     const int per = (p.C / 8 + kThreads - 1) / kThreads;  // 1..4
@@ -230,12 +234,10 @@ extern "C" int vkwr_layer_norm_f16(int64_t rows, int C, const uint16_t* x, const
   return launch_ln<0, false>(fn, p, vec, (hipStream_t)stream);
 }
 
-extern "C" int vkwr_add_last_layer_norm_f16(int B, int T, int C, const uint16_t* x,
-                                            const uint16_t* residual, const uint16_t* weight,
-                                            const uint16_t* bias, float eps, uint16_t* y,
-                                            void* stream) {
-  clear_error();
-  const char* fn = "vkwr_add_last_layer_norm_f16";
+namespace {
+int add_last_ln(const char* fn, int B, int T, int C, const uint16_t* x, const uint16_t* residual,
+                const uint16_t* weight, const uint16_t* bias, float eps, uint16_t* y, int frag,
+                void* stream) {
   VK_REQUIRE(B >= 0 && T > 0, "%s: bad B=%d T=%d", fn, B, T);
   VK_REQUIRE(B == 0 || (x && residual && weight && bias && y), "%s: null pointer", fn);
   LnArgs p{};
@@ -249,8 +251,27 @@ extern "C" int vkwr_add_last_layer_norm_f16(int B, int T, int C, const uint16_t*
   p.bias = bias;
   p.eps = eps;
   p.y = reinterpret_cast<_Float16*>(y);
+  p.out_frag = frag;
   const bool vec = aligned16(x) && aligned16(residual) && aligned16(y);
   return launch_ln<0, false>(fn, p, vec, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int vkwr_add_last_layer_norm_f16(int B, int T, int C, const uint16_t* x,
+                                            const uint16_t* residual, const uint16_t* weight,
+                                            const uint16_t* bias, float eps, uint16_t* y,
+                                            void* stream) {
+  clear_error();
+  return add_last_ln("vkwr_add_last_layer_norm_f16", B, T, C, x, residual, weight, bias, eps, y, 0, stream);
+}
+
+extern "C" int vkwr_add_last_layer_norm_frag_f16(int B, int T, int C, const uint16_t* x,
+                                                 const uint16_t* residual, const uint16_t* weight,
+                                                 const uint16_t* bias, float eps, uint16_t* y,
+                                                 void* stream) {
+  clear_error();
+  return add_last_ln("vkwr_add_last_layer_norm_frag_f16", B, T, C, x, residual, weight, bias, eps, y, 1,
+                     stream);
 }
 
 extern "C" int vkwr_emb_ln0_bf16_to_f16(int64_t V, int C, const uint16_t* emb,
@@ -271,14 +292,11 @@ extern "C" int vkwr_emb_ln0_bf16_to_f16(int64_t V, int C, const uint16_t* emb,
   return launch_ln<0, true>(fn, p, false, (hipStream_t)stream);
 }
 
-extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* x,
-                                           const uint16_t* residual, uint16_t* shift_state,
-                                           const uint16_t* weight, const uint16_t* bias, int n_mix,
-                                           const uint16_t* const* mix, float eps, uint16_t* x_out,
-                                           uint16_t* const* out, const int32_t* x_rows,
-                                           const int32_t* shift_slots, void* stream) {
-  clear_error();
-  const char* fn = "vkwr_add_layer_norm_mix_f16";
+namespace {
+int add_ln_mix(const char* fn, int64_t rows, int C, const uint16_t* x, const uint16_t* residual,
+               uint16_t* shift_state, const uint16_t* weight, const uint16_t* bias, int n_mix,
+               const uint16_t* const* mix, float eps, uint16_t* x_out, uint16_t* const* out,
+               const int32_t* x_rows, const int32_t* shift_slots, int frag, void* stream) {
   VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
   VK_REQUIRE(mix && out, "%s: null pointer", fn);
   LnArgs p{};
@@ -294,6 +312,7 @@ extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* 
   p.shift = reinterpret_cast<_Float16*>(shift_state);
   p.x_rows = x_rows;
   p.shift_slots = shift_slots;
+  p.out_frag = frag;
   bool vec = aligned16(x) && (!residual || aligned16(residual)) && aligned16(shift_state) &&
              aligned16(x_out);
   for (int i = 0; i < n_mix; ++i) {
@@ -305,6 +324,30 @@ extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* 
   VK_REQUIRE(rows == 0 || (x && shift_state && weight && bias && x_out), "%s: null pointer", fn);
   if (n_mix == 1) return launch_ln<1, false>(fn, p, vec, (hipStream_t)stream);
   return launch_ln<6, false>(fn, p, vec, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* x,
+                                           const uint16_t* residual, uint16_t* shift_state,
+                                           const uint16_t* weight, const uint16_t* bias, int n_mix,
+                                           const uint16_t* const* mix, float eps, uint16_t* x_out,
+                                           uint16_t* const* out, const int32_t* x_rows,
+                                           const int32_t* shift_slots, void* stream) {
+  clear_error();
+  return add_ln_mix("vkwr_add_layer_norm_mix_f16", rows, C, x, residual, shift_state, weight, bias, n_mix,
+                    mix, eps, x_out, out, x_rows, shift_slots, 0, stream);
+}
+
+extern "C" int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint16_t* x,
+                                                const uint16_t* residual, uint16_t* shift_state,
+                                                const uint16_t* weight, const uint16_t* bias,
+                                                int n_mix, const uint16_t* const* mix, float eps,
+                                                uint16_t* x_out, uint16_t* const* out,
+                                                const int32_t* x_rows, const int32_t* shift_slots,
+                                                void* stream) {
+  clear_error();
+  return add_ln_mix("vkwr_add_layer_norm_mix_frag_f16", rows, C, x, residual, shift_state, weight, bias,
+                    n_mix, mix, eps, x_out, out, x_rows, shift_slots, 1, stream);
 }
 
 extern "C" int vkwr_add_f16(int64_t n, const uint16_t* x, const uint16_t* y, uint16_t* out,

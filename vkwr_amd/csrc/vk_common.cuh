@@ -123,4 +123,21 @@ __device__ __forceinline__ float bf16f(uint16_t b) {
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// ---------------------------------------------------------------- frag layout
+
+// Half index of element (r, k) of a matrix stored in the fragment order of
+// v_mfma_f32_32x32x16_f16 operands (row blocks of 32, K padded to kpad, a
+// multiple of 16): the 64 lanes x 8 halfs of one (row block, 16-k step)
+// operand are contiguous, lane = ((k / 8) % 2) * 32 + r % 32.  Eight
+// consecutive k starting at a multiple of 8 are contiguous.
+__device__ __forceinline__ int64_t frag_index(int64_t r, int64_t k, int64_t kpad) {
+  return (((r >> 5) * (kpad >> 4) + (k >> 4)) * 64 + ((k >> 3) & 1) * 32 + (r & 31)) * 8 + (k & 7);
+}
+
+constexpr int kFragPad = 128;  // rows and K of frag matrices are padded to multiples of this
+
+__host__ __device__ __forceinline__ int64_t frag_pad(int64_t x) {
+  return (x + kFragPad - 1) / kFragPad * kFragPad;
+}
+
 }  // namespace vk

@@ -24,6 +24,16 @@ layout [out, in]; the embedding table is stored after its LN0.  All
 activations are fp16, the WKV state fp32.  `DecodeEngine` preallocates every
 buffer (activations, GEMM workspace), so a decode step allocates nothing and
 can be captured into a HIP graph.
+
+GEMM path: by default the engine packs every projection weight once into the
+fragment layout of include/vkwr_amd.h (vkwr_frag_pack_f16) and the producers
+of each projection input (the LN + token-shift fusions, the GroupNorm gate, the
+final LN, and the GEMMs whose output only feeds another GEMM: the low-rank
+inputs and the FFN hidden) write it directly in that layout, so every GEMM is a
+vkwr_frag_gemm_f16 launch streaming the weights with fully coalesced loads.
+The low-rank activations (tanh, sigmoid) are applied to the fp32 accumulator
+of the producing GEMM and rounded to fp16 once.  `frag=False` runs the same
+step on row-major weights through vkwr_gemm_f16 (the reference-op GEMM).
 """
 import math
 from dataclasses import dataclass
@@ -131,14 +141,20 @@ class RWKV7State:
         return cfg.n_layer * (2 * cfg.n_head * HEAD * HEAD * 4 + 2 * 2 * cfg.n_embd * 2)
 
 
+FRAG_WEIGHTS = ("Wr", "Wk", "Wv", "Wo", "w1", "w2", "a1", "a2", "g1", "g2", "v1", "v2", "key", "value")
+
+
 class DecodeEngine:
     """Batched T=1 decode of up to `max_batch` sequences with preallocated buffers."""
 
-    def __init__(self, model, max_batch):
+    def __init__(self, model, max_batch, frag=True):
         cfg = model.cfg
-        self.model, self.cfg, self.max_batch = model, cfg, max_batch
+        self.model, self.cfg, self.max_batch, self.frag = model, cfg, max_batch, frag
         dev = model.head.device
         B, C, F = max_batch, cfg.n_embd, cfg.dim_ffn
+        if frag:
+            self._init_frag(dev)
+            return
 
         def buf(*shape):
             return torch.empty(*shape, dtype=torch.float16, device=dev)
@@ -158,6 +174,84 @@ class DecodeEngine:
         need = max(capi.gemm_workspace_bytes(ps) for b in sorted({B, 128, 64, 32, 16, 8, 4, 2, 1})
                    if b <= B for ps in self._all_gemms(b))
         self.ws = torch.empty(max(need, 0), dtype=torch.uint8, device=dev)
+
+    def _init_frag(self, dev):
+        cfg, m = self.cfg, self.model
+        B, C, F = self.max_batch, cfg.n_embd, cfg.dim_ffn
+
+        def packed(w):
+            n, k = w.shape
+            out = capi.frag_empty(n, k, dev, zero=False)
+            capi.frag_pack(w.contiguous(), n, k, out)
+            return out
+
+        self.pw = [{name: packed(L[name]) for name in FRAG_WEIGHTS if name in L} for L in m.layers]
+        self.p_head = packed(m.head)
+
+        def buf(*shape):
+            return torch.empty(*shape, dtype=torch.float16, device=dev)
+
+        fr = lambda k: capi.frag_empty(B, k, dev)  # noqa: E731
+        self.res = [buf(B, C), buf(B, C)]
+        self.mixf = [fr(C) for _ in range(6)]
+        self.r, self.k, self.v, self.v_first, self.v_new = buf(B, C), buf(B, C), buf(B, C), buf(B, C), buf(B, C)
+        self.w1f, self.a1f, self.g1f, self.v1f = fr(cfg.rank_w), fr(cfg.rank_a), fr(cfg.rank_g), fr(cfg.rank_v)
+        self.w, self.a12, self.g = buf(B, C), buf(B, C), buf(B, C)
+        self.new_k, self.neg_kk, self.kka = buf(B, C), buf(B, C), buf(B, C)
+        self.y, self.o = buf(B, C), buf(B, C)
+        self.o_in_f, self.xk_f, self.act_f, self.h_f = fr(C), fr(C), fr(F), fr(C)
+        self.ffn = buf(B, C)
+        self.logits = buf(B, cfg.vocab)
+
+    def _step_frag(self, state, tokens, slots):
+        cfg, m, s = self.cfg, self.model, self
+        B = tokens.shape[0]
+        C, H, F = cfg.n_embd, cfg.n_head, cfg.dim_ffn
+        fp = capi.frag_problem
+        x, res_in = None, None
+        for l, L in enumerate(m.layers):
+            first = l == 0
+            P = s.pw[l]
+            res = s.res[l % 2][:B]
+            # ---- time mix
+            capi.add_layer_norm_mix(
+                m.emb if first else x, None if first else res_in, state.att_shift[l], L["ln1_w"], L["ln1_b"],
+                [L["x_r"], L["x_w"], L["x_k"], L["x_v"], L["x_a"], L["x_g"]], res, s.mixf,
+                x_rows=tokens if first else None, shift_slots=slots, frag=True)
+            xr, xw, xk, xv, xa, xg = s.mixf
+            v_out = (s.v_first if first else s.v)[:B]
+            probs = [fp(xr, P["Wr"], s.r, B, C, C), fp(xk, P["Wk"], s.k, B, C, C), fp(xv, P["Wv"], v_out, B, C, C),
+                     fp(xw, P["w1"], s.w1f, B, cfg.rank_w, C, epilogue=capi.EPI_TANH, c_frag=True),
+                     fp(xa, P["a1"], s.a1f, B, cfg.rank_a, C, c_frag=True),
+                     fp(xg, P["g1"], s.g1f, B, cfg.rank_g, C, epilogue=capi.EPI_SIGMOID, c_frag=True)]
+            if not first:
+                probs.append(fp(xv, P["v1"], s.v1f, B, cfg.rank_v, C, c_frag=True))
+            capi.frag_gemm(probs)
+            probs = [fp(s.w1f, P["w2"], s.w, B, C, cfg.rank_w, epilogue=capi.EPI_BIAS, v0=L["w0"]),
+                     fp(s.a1f, P["a2"], s.a12, B, C, cfg.rank_a),
+                     fp(s.g1f, P["g2"], s.g, B, C, cfg.rank_g)]
+            if not first:
+                probs.append(fp(s.v1f, P["v2"], s.v_new, B, C, cfg.rank_v, epilogue=capi.EPI_VALUE_RESIDUAL,
+                                v=s.v, v_first=s.v_first, v0=L["v0"]))
+            capi.frag_gemm(probs)
+            v = (s.v_first if first else s.v_new)[:B]
+            capi.kk_a_gate(B, 1, C, H, s.k[:B], L["k_k"], L["a0"], s.a12[:B], L["k_a"], s.new_k[:B],
+                           s.neg_kk[:B], s.kka[:B])
+            capi.wkv_slots(B, 1, C, H, state.wkv[l], slots, s.r[:B], s.w[:B], s.new_k[:B], v, s.neg_kk[:B],
+                           s.kka[:B], s.y[:B])
+            capi.groupnorm_bonus_gate(B, 1, C, H, s.y[:B], s.r[:B], s.new_k[:B], v, L["r_k"], L["lnx_w"],
+                                      L["lnx_b"], s.g[:B], s.o_in_f, frag=True)
+            capi.frag_gemm([fp(s.o_in_f, P["Wo"], s.o, B, C, C)])
+            # ---- channel mix
+            res2 = s.res[(l + 1) % 2][:B]
+            capi.add_layer_norm_mix(s.o[:B], res, state.ffn_shift[l], L["ln2_w"], L["ln2_b"], [L["x_k_ffn"]],
+                                    res2, [s.xk_f], shift_slots=slots, frag=True)
+            capi.frag_gemm([fp(s.xk_f, P["key"], s.act_f, B, F, C, epilogue=capi.EPI_RELU_SQUARE, c_frag=True)])
+            capi.frag_gemm([fp(s.act_f, P["value"], s.ffn, B, C, F)])
+            x, res_in = s.ffn[:B], res2
+        capi.add_last_layer_norm(B, 1, C, x, res_in, m.ln_out_w, m.ln_out_b, s.h_f, frag=True)
+        capi.frag_gemm([fp(s.h_f, s.p_head, s.logits, B, cfg.vocab, C)])
+        return s.logits[:B]
 
     # -- GEMM batches of one layer (shared by planning and execution)
     def _proj_problems(self, L, B, first):
@@ -201,9 +295,11 @@ class DecodeEngine:
         """One decode step for B = len(tokens) sequences: tokens, slots int32 [B] on the
         device (slots distinct, < state.n_slots).  Updates `state` in place and returns
         the logits view [B, vocab] (valid until the next step)."""
-        cfg, m, s = self.cfg, self.model, self
         B = tokens.shape[0]
         assert 0 < B <= self.max_batch and slots.shape[0] == B
+        if self.frag:
+            return self._step_frag(state, tokens, slots)
+        cfg, m, s = self.cfg, self.model, self
         C, H = cfg.n_embd, cfg.n_head
         ws = self.ws
         x, res_in = None, None
