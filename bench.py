@@ -117,7 +117,9 @@ def model_decode(dev, steps, warmup=3, frag=True):
     cfg = RWKV7Config.preset("1.5b")
     B = 128
     model = RWKV7Model(cfg, dev, seed=0)
-    state = RWKV7State(cfg, 160, dev, std=0.1, seed=1)
+    from vkwr_amd import capi
+    state = RWKV7State(cfg, 160, dev, std=0.1, seed=1,
+                       layout=capi.WKV_STATE_ILV if frag else capi.WKV_STATE_STD)
     eng = DecodeEngine(model, B, frag=frag)
     g = torch.Generator().manual_seed(3)
     slots = torch.randperm(160, generator=g)[:B].to(torch.int32).to(dev)

@@ -73,6 +73,43 @@ VKWR_EXPORT int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* 
                                  const uint16_t* a, const uint16_t* b, uint16_t* y,
                                  void* stream);
 
+/* Layouts of an fp32 64x64 WKV state block (16 KiB) in a pool.
+ *   VKWR_WKV_STATE_STD: row-major S[i][j] at float 64 i + j (the reference's
+ *     [.., H, 64, 64] layout; every other entry point uses it).
+ *   VKWR_WKV_STATE_ILV: interleaved, S[i][4q + e] at float (64 q + i) * 4 + e:
+ *     column chunk q of all 64 rows is one contiguous kilobyte, which the fused
+ *     decode kernel streams straight into registers (lane i = row i). */
+enum { VKWR_WKV_STATE_STD = 0, VKWR_WKV_STATE_ILV = 1 };
+
+/* Converts n_blocks state blocks from src to dst (not aliased) into layout
+ * to_layout (from the other one).  No counterpart in the reference. */
+VKWR_EXPORT int vkwr_wkv7_state_layout_f32(int64_t n_blocks, const float* src, float* dst, int to_layout,
+                                           void* stream);
+
+/* Fused time-mix decode step (T = 1) on a slot pool, one pass per (sequence, head):
+ *   kk = normalize_head(k * k_k), a = sigmoid(a0 + a12),
+ *   new_k = k * (a * k_a + 1 - k_a), then the WKV-7 update of pool[slots[b]]
+ *   with (r, w, new_k, v, -kk, kk * a) as in vkwr_wkv7_fp32_forward_slots,
+ *   then out = ((y - mean_h) * rstd_h * ln_w + ln_b + (sum_h r * new_k * r_k) * v) * g
+ *   (GroupNorm eps 64e-5), with the fp16 roundings of the unfused sequence
+ *   vkwr_tmix_kk_a_gate_f16 -> vkwr_wkv7_fp32_forward_slots ->
+ *   vkwr_tmix_groupnorm_bonus_gate_f16, so the result is bit-identical to it.
+ *   r, w, k, v, a12, g [B, C] fp16; k_k, a0, k_a, r_k, ln_w, ln_b [C];
+ *   out [B, C] row-major, or a frag matrix [B, C] when out_frag = 1
+ *   (C % 128 == 0).  pool [n_slots, H] blocks in state_layout (VKWR_WKV_STATE_*).
+ *   A slot outside [0, n_slots) leaves the pool untouched and writes NaN to
+ *   that sequence's out row.
+ * No single reference function: fuses tmix_kk_a_gate (csrc/v1/mix/mix_ops.cu:
+ * 1015-1049), the fp32 WKV (csrc/v1/wkv/wkv_fp32_v2.cu:230-288) with the
+ * caller's slot gather/scatter, and tmix_lnx_rkvres_xg (mix_ops.cu:1051-1083). */
+VKWR_EXPORT int vkwr_wkv7_decode_fused_f16(int B, int C, int H, float* pool, int n_slots,
+                                           int state_layout, const int32_t* slots, const uint16_t* r, const uint16_t* w,
+                                           const uint16_t* k, const uint16_t* v, const uint16_t* a12,
+                                           const uint16_t* g, const uint16_t* k_k, const uint16_t* a0,
+                                           const uint16_t* k_a, const uint16_t* r_k, const uint16_t* ln_w,
+                                           const uint16_t* ln_b, uint16_t* out, int out_frag,
+                                           void* stream);
+
 /* fp16-state WKV-7 with the dither decay delta.
  *   state [B,H,64,64] fp16 (in place); r..y [B,T,C] fp16; w0 NULL or >= C fp16
  *   values added to w per channel; elapsed_t [B] int32 (read only).

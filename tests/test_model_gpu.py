@@ -26,10 +26,12 @@ STATE_TOL = 1e-3
 
 
 def _setup(gpu, preset, B, P, seed=0, frag=True):
+    from vkwr_amd import capi
     from vkwr_amd.model_executor import RWKV7Config, RWKV7Model, RWKV7State, DecodeEngine
     cfg = RWKV7Config.preset(preset)
     model = RWKV7Model(cfg, gpu, seed=seed)
-    state = RWKV7State(cfg, P, gpu, std=0.1, seed=seed + 1)
+    layout = capi.WKV_STATE_ILV if frag else capi.WKV_STATE_STD
+    state = RWKV7State(cfg, P, gpu, std=0.1, seed=seed + 1, layout=layout)
     eng = DecodeEngine(model, B, frag=frag)
     g = torch.Generator().manual_seed(seed)
     slots = torch.randperm(P, generator=g)[:B].to(torch.int32).to(gpu)
@@ -39,7 +41,8 @@ def _setup(gpu, preset, B, P, seed=0, frag=True):
 @pytest.mark.parametrize("frag", [True, False], ids=["frag_gemm", "rowmajor_gemm"])
 def test_tiny_model_matches_cpu_oracle_over_steps(gpu, frag):
     cfg, model, state, eng, slots, g = _setup(gpu, "tiny", B=4, P=9, frag=frag)
-    wkv = state.wkv.cpu().clone()
+    wkv = state.wkv_standard().cpu()
+    wkv0 = wkv.clone()
     att, ffn = state.att_shift.cpu().clone(), state.ffn_shift.cpu().clone()
     wkv_r, att_r, ffn_r = wkv.clone(), att.clone(), ffn.clone()
     for step in range(3):
@@ -49,15 +52,9 @@ def test_tiny_model_matches_cpu_oracle_over_steps(gpu, frag):
         ref32 = model_ref.decode_step(model, wkv_r, att_r, ffn_r, tokens, slots.cpu(), round_fp16=False)
         assert (logits - ref).abs().max() <= 1e-2, (step, float((logits - ref).abs().max()))
         assert (logits - ref32).abs().max() <= LOGIT_TOL, (step, float((logits - ref32).abs().max()))
-        assert (state.wkv.cpu() - wkv).abs().max() <= STATE_TOL
+        assert (state.wkv_standard().cpu() - wkv).abs().max() <= STATE_TOL
     others = [s for s in range(9) if s not in slots.cpu().tolist()]
-    assert torch.equal(state.wkv.cpu()[:, others], RWKV7StateInit(cfg, gpu)[:, others])
-
-
-def RWKV7StateInit(cfg, gpu):
-    """The untouched initial pool (same seed as _setup)."""
-    from vkwr_amd.model_executor import RWKV7State
-    return RWKV7State(cfg, 9, gpu, std=0.1, seed=1).wkv.cpu()
+    assert torch.equal(state.wkv_standard().cpu()[:, others], wkv0[:, others])
 
 
 @pytest.mark.parametrize("frag", [True, False], ids=["frag_gemm", "rowmajor_gemm"])
@@ -66,7 +63,8 @@ def test_1p5b_decode_step_bs128_logits(gpu, frag):
     and states against the float32 composition evaluated with torch on the GPU."""
     cfg, model, state, eng, slots, g = _setup(gpu, "1.5b", B=128, P=160, frag=frag)
     tokens = torch.randint(0, cfg.vocab, (128,), generator=g, dtype=torch.int32).to(gpu)
-    wkv = state.wkv.clone()
+    wkv = state.wkv_standard()
+    wkv0 = wkv.clone()
     att, ffn = state.att_shift.clone(), state.ffn_shift.clone()
     logits = eng.step(state, tokens, slots).float()
     torch.cuda.synchronize()
@@ -75,10 +73,11 @@ def test_1p5b_decode_step_bs128_logits(gpu, frag):
     err = (logits - ref).abs().max().item()
     assert err <= LOGIT_TOL, err
     sl = slots.long()
-    assert (state.wkv[:, sl] - wkv[:, sl]).abs().max().item() <= 2.5e-2
+    got = state.wkv_standard()
+    assert (got[:, sl] - wkv[:, sl]).abs().max().item() <= 2.5e-2
     others = torch.ones(160, dtype=torch.bool, device=gpu)
     others[sl] = False
-    assert torch.equal(state.wkv[:, others], wkv[:, others])  # untouched by both
+    assert torch.equal(got[:, others], wkv0[:, others])  # untouched
 
 
 @pytest.mark.parametrize("frag", [True, False], ids=["frag_gemm", "rowmajor_gemm"])

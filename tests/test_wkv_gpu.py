@@ -140,6 +140,68 @@ def test_slots_out_of_range_is_skipped(gpu):
         ops.wkv_forward_slots_fp32(B, 1, C, H, pool, slots, *ins, validate=True)
 
 
+@pytest.mark.parametrize("layout", ["std", "ilv"])
+@pytest.mark.parametrize("frag", [False, True], ids=["rowmajor_out", "frag_out"])
+def test_decode_fused_equals_gate_wkv_groupnorm_sequence(gpu, frag, layout):
+    """vkwr_wkv7_decode_fused_f16 == kk_a_gate -> wkv7_fp32_forward_slots ->
+    groupnorm_bonus_gate, bit for bit (pool and output), including an
+    out-of-range slot (pool untouched, NaN output row) and a ragged batch; with
+    the pool in either block layout (the interleaved pool converted back)."""
+    from vkwr_amd import capi
+    rng = np.random.default_rng(5)
+    B, H, P = 37, 4, 50
+    C = 64 * H
+    h16 = lambda *s, sc=1.0: torch.from_numpy((rng.standard_normal(s) * sc).astype(np.float16)).to(gpu)  # noqa
+    r, w, k, v, a12, g = h16(B, C), h16(B, C, sc=2.0), h16(B, C), h16(B, C), h16(B, C), h16(B, C)
+    k_k = torch.from_numpy((0.85 + 0.1 * rng.random(C)).astype(np.float16)).to(gpu)
+    a0, k_a, r_k, ln_w, ln_b = h16(C, sc=0.5), h16(C, sc=0.1) + 1, h16(C, sc=0.5), h16(C, sc=0.1) + 1, h16(C, sc=0.1)
+    slots_np = rng.permutation(P)[:B].astype(np.int32)
+    slots_np[7] = P  # out of range
+    slots = torch.from_numpy(slots_np).to(gpu)
+    pool0 = torch.from_numpy((rng.standard_normal((P, H, 64, 64)) * 0.1).astype(np.float32)).to(gpu)
+    # unfused
+    pool_u = pool0.clone()
+    new_k, neg_kk, kka, y = (torch.empty(B, C, dtype=torch.float16, device=gpu) for _ in range(4))
+    capi.kk_a_gate(B, 1, C, H, k, k_k, a0, a12, k_a, new_k, neg_kk, kka)
+    capi.wkv_slots(B, 1, C, H, pool_u, slots, r, w, new_k, v, neg_kk, kka, y)
+    out_u = torch.empty(B, C, dtype=torch.float16, device=gpu)
+    capi.groupnorm_bonus_gate(B, 1, C, H, y, r, new_k, v, r_k, ln_w, ln_b, g, out_u)
+    # fused
+    ilv = layout == "ilv"
+    pool_f = pool0.clone()
+    if ilv:
+        capi.wkv_state_layout(pool0, pool_f, capi.WKV_STATE_ILV)
+    out_f = capi.frag_empty(B, C, gpu) if frag else torch.empty(B, C, dtype=torch.float16, device=gpu)
+    capi.wkv_decode_fused(B, C, H, pool_f, slots, r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_w, ln_b, out_f,
+                          frag=frag, state_layout=capi.WKV_STATE_ILV if ilv else capi.WKV_STATE_STD)
+    if ilv:
+        back = torch.empty_like(pool_f)
+        capi.wkv_state_layout(pool_f, back, capi.WKV_STATE_STD)
+        pool_f = back
+    assert torch.equal(pool_f, pool_u)
+    if frag:
+        out_f_rm = torch.empty(B, C, dtype=torch.float16, device=gpu)
+        capi.frag_unpack(out_f, B, C, out_f_rm)
+        out_f = out_f_rm
+    ok = torch.ones(B, dtype=torch.bool, device=gpu)
+    ok[7] = False
+    assert torch.equal(out_f[ok], out_u[ok])
+    assert torch.isnan(out_f[7]).all() and torch.isnan(out_u[7]).all()
+
+
+def test_state_layout_round_trip_and_definition(gpu):
+    """Interleaved block layout: S[i][4q+e] at float (64q + i)*4 + e; std -> ilv -> std is the identity."""
+    from vkwr_amd import capi
+    x = torch.randn(3, 2, 64, 64, device=gpu)
+    ilv = torch.empty_like(x)
+    capi.wkv_state_layout(x, ilv, capi.WKV_STATE_ILV)
+    want = x.reshape(6, 64, 16, 4).permute(0, 2, 1, 3).reshape(3, 2, 64, 64)
+    assert torch.equal(ilv, want)
+    back = torch.empty_like(x)
+    capi.wkv_state_layout(ilv, back, capi.WKV_STATE_STD)
+    assert torch.equal(back, x)
+
+
 def test_prefill_config2_reduced_matches_oracle(gpu):
     """BASELINE config 2 shape (T=1024, H=32) at B=2, slots gathered from a pool."""
     from vkwr_amd._ops.v1 import v1_wkv_ops as ops

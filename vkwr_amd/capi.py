@@ -79,6 +79,9 @@ _ln_mix_frag = _sig("vkwr_add_layer_norm_mix_frag_f16",
                     [_i64, _i, _p, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p, _p, _p])
 _ln_last_frag = _sig("vkwr_add_last_layer_norm_frag_f16", [_i, _i, _i, _p, _p, _p, _p, _f, _p, _p])
 _gn_frag = _sig("vkwr_tmix_groupnorm_bonus_gate_frag_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p])
+_wkv_fused = _sig("vkwr_wkv7_decode_fused_f16", [_i, _i, _i, _p, _i, _i, _p] + [_p] * 13 + [_i, _p])
+_wkv_layout = _sig("vkwr_wkv7_state_layout_f32", [_i64, _p, _p, _i, _p])
+WKV_STATE_STD, WKV_STATE_ILV = 0, 1
 _shift = _sig("vkwr_token_shift_mix_f16", [_i, _i, _i, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 
 
@@ -197,6 +200,20 @@ def _arr_frag(problems):
 def wkv_slots(B, T, C, H, pool, slots, r, w, k, v, a, b, y):
     _check(_wkv_slots(B, T, C, H, _ptr(pool), pool.shape[0], _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
                       _ptr(a), _ptr(b), _ptr(y), _stream()), "vkwr_wkv7_fp32_forward_slots")
+
+
+def wkv_decode_fused(B, C, H, pool, slots, r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_w, ln_b, out, frag=False,
+                     state_layout=WKV_STATE_STD):
+    """gate -> WKV-7 (slot pool, T = 1) -> GroupNorm + bonus + gate in one launch."""
+    _check(_wkv_fused(B, C, H, _ptr(pool), pool.shape[0], state_layout, _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
+                      _ptr(a12), _ptr(g), _ptr(k_k), _ptr(a0), _ptr(k_a), _ptr(r_k), _ptr(ln_w), _ptr(ln_b),
+                      _ptr(out), 1 if frag else 0, _stream()), "vkwr_wkv7_decode_fused_f16")
+
+
+def wkv_state_layout(src, dst, to_layout):
+    """Copies fp32 state blocks (src, dst: [..., 64, 64] views of the same shape) into layout to_layout."""
+    assert src.shape == dst.shape and src.dtype == dst.dtype == torch.float32 and src.numel() % 4096 == 0
+    _check(_wkv_layout(src.numel() // 4096, _ptr(src), _ptr(dst), to_layout, _stream()), "vkwr_wkv7_state_layout_f32")
 
 
 def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False):

@@ -22,8 +22,6 @@ namespace vk {
 namespace {
 
 constexpr int kTokRun = 16;
-constexpr float kKkEps = 1.0e-12f;      // L2-normalisation floor of kk
-constexpr float kGroupNormEps = 64.0e-5f;  // GroupNorm eps of the time-mix output
 
 struct ShiftArgs {
   int B, T, C;

@@ -12,6 +12,9 @@
 namespace vk {
 
 constexpr int kHead = 64;  // RWKV-7 head size (the only one the ops accept)
+// Time-mix epsilons (reference csrc/v1/mix/mix_ops.cu:17-18).
+constexpr float kKkEps = 1.0e-12f;         // L2-normalisation floor of kk
+constexpr float kGroupNormEps = 64.0e-5f;  // GroupNorm eps of the time-mix output
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));

@@ -26,6 +26,8 @@
 // The fp16-state family stages its 8 KiB head in one phase (128-byte rows, 8
 // chunks per row, slot i*8 + (q ^ ((i >> 1) & 7))).
 
+#include <algorithm>
+
 #include "vk_capi.h"
 #include "vk_common.cuh"
 
@@ -86,19 +88,20 @@ __device__ __forceinline__ void store_state_fp32(float* S, f4* st, const float* 
   }
 }
 
-// One token of the fp32-state recurrence for row `lane` (state row in s[]).
-// vb: 5*64 floats of LDS for the token's channel vectors (r, decay, k, a, b),
-// written here one channel per lane and read back as broadcasts.
-__device__ __forceinline__ _Float16 token_fp32(float* s, float* vb, int lane, _Float16 xr,
-                                               _Float16 xw, _Float16 xk, _Float16 xv,
-                                               _Float16 xa, _Float16 xb) {
+// One token of the fp32-state recurrence for row `lane` (state row in s[]),
+// in two parts: token_stage writes the token's channel vectors (r, decay, k,
+// a, b; one channel per lane) to vb (5*64 floats of LDS), token_run reads them
+// back as broadcasts after a barrier.
+__device__ __forceinline__ void token_stage(float* vb, int lane, _Float16 xr, _Float16 xw, _Float16 xk,
+                                            _Float16 xa, _Float16 xb) {
   vb[lane] = (float)xr;
   vb[kHead + lane] = decay((float)xw);
   vb[2 * kHead + lane] = (float)xk;
   vb[3 * kHead + lane] = (float)xa;
   vb[4 * kHead + lane] = (float)xb;
-  const float vi = (float)xv;
-  __syncthreads();
+}
+
+__device__ __forceinline__ _Float16 token_run(float* s, const float* vb, float vi) {
   const f4* R4 = reinterpret_cast<const f4*>(vb);
   const f4* D4 = R4 + 16;
   const f4* K4 = R4 + 32;
@@ -131,6 +134,14 @@ __device__ __forceinline__ _Float16 token_fp32(float* s, float* vb, int lane, _F
   // v_fma_mixlo_f16, which rounds once instead of f32-then-f16.
   asm volatile("" : "+v"(acc));
   return (_Float16)acc;
+}
+
+__device__ __forceinline__ _Float16 token_fp32(float* s, float* vb, int lane, _Float16 xr,
+                                               _Float16 xw, _Float16 xk, _Float16 xv,
+                                               _Float16 xa, _Float16 xb) {
+  token_stage(vb, lane, xr, xw, xk, xa, xb);
+  __syncthreads();
+  return token_run(s, vb, (float)xv);
 }
 
 // Resolves the state block of (sequence bi, head h); with slots, an entry
@@ -215,6 +226,104 @@ void launch_fp32(const Fp32Args& p, int B, hipStream_t stream) {
   } else {
     hipLaunchKernelGGL(wkv7_fp32_seq_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   }
+}
+
+// ---- fused decode step of the time mix: kk/a gate -> WKV-7 -> GroupNorm,
+// bonus and output gate, one wave per (sequence, head).  Each stage is the
+// arithmetic of its stand-alone kernel (mix.hip kk_a_gate_kernel,
+// token_fp32 above, mix.hip groupnorm_bonus_gate_kernel) with the fp16
+// roundings of their stored intermediates (new_k, -kk, kk*a, y), so the fused
+// result is bit-identical to the three-kernel sequence; the intermediates
+// never leave registers and the per-head reductions are wave reductions.
+struct FusedArgs {
+  int C, H, n_slots;
+  float* pool;
+  const int32_t* slots;
+  const _Float16 *r, *w, *k, *v, *a12, *g;
+  const _Float16 *k_k, *a0, *k_a, *r_k, *ln_w, *ln_b;
+  _Float16* out;
+  int out_frag;
+};
+
+// kIlv: the pool is in the interleaved layout (vkwr_amd.h VKWR_WKV_STATE_ILV):
+// chunk q (columns 4q..4q+3) of the 64 rows is one contiguous kilobyte, so
+// lane i loads its row straight into registers with 16 fully coalesced
+// 16-byte loads, all in flight at once, and stores it back the same way -- no
+// LDS staging, no barriers.  Otherwise the standard [64][64] row-major block
+// goes through the two-phase LDS transpose.
+template <bool kIlv>
+__global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
+  __shared__ f4 st[512];
+  __shared__ float vb[5 * kHead];  // the token's channel vectors, staged before the state phase
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const int c = h * kHead + lane;
+  const size_t tok = (size_t)bi * p.C + c;
+  auto out_index = [&]() { return p.out_frag ? frag_index(bi, c, p.C) : (int64_t)tok; };
+  const int sl = p.slots[bi];
+  if (sl < 0 || sl >= p.n_slots) {
+    p.out[out_index()] = (_Float16)__builtin_nanf("");
+    return;
+  }
+  float* S = p.pool + ((size_t)sl * p.H + h) * (kHead * kHead);
+  const _Float16 xr = p.r[tok], xw = p.w[tok], xv = p.v[tok];
+  const float kv = (float)p.k[tok], a12 = (float)p.a12[tok];
+  // kk / a gate
+  const float u = kv * (float)p.k_k[c];
+  const float inv = 1.0f / fmaxf(sqrtf(wave_sum(u * u)), kKkEps);
+  const float kk = u * inv;
+  const float a = sigmoidf((float)p.a0[c] + a12);
+  const float ka = (float)p.k_a[c];
+  const _Float16 new_k = (_Float16)(kv * __builtin_fmaf(a, ka, 1.0f - ka));
+  const _Float16 neg_kk = (_Float16)(-kk);
+  const _Float16 kka = (_Float16)(kk * a);
+  // The r.k bonus does not depend on the WKV output: reduce it now (a
+  // wave-uniform scalar) so r and new_k need not stay live across the state phase.
+  const float rkv = wave_sum((float)xr * (float)new_k * (float)p.r_k[c]);
+  // WKV-7 (the channel vectors go to LDS first: only v stays in a register
+  // across the state load)
+  token_stage(vb, lane, xr, xw, new_k, neg_kk, kka);
+  const float vi = (float)xv;
+  float s[kHead];
+  if constexpr (kIlv) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const f4 x = *reinterpret_cast<const f4*>(S + (q * kHead + lane) * 4);
+      s[4 * q + 0] = x.x;
+      s[4 * q + 1] = x.y;
+      s[4 * q + 2] = x.z;
+      s[4 * q + 3] = x.w;
+    }
+    __syncthreads();  // orders the vb writes before token_run's broadcast reads
+  } else {
+    load_state_fp32(S, st, s, lane);  // its barriers also order the vb writes
+  }
+  const float y = (float)token_run(s, vb, vi);
+  // Recompute the store addresses instead of keeping the load's 16 per-lane
+  // addresses live across the token (they would spill): launder S and lane.
+  float* S2 = S;
+  int lane2 = lane;
+  asm volatile("" : "+s"(S2), "+v"(lane2));
+  if constexpr (kIlv) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      *reinterpret_cast<f4*>(S2 + (q * kHead + lane2) * 4) = f4{s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]};
+  } else {
+    store_state_fp32(S2, st, s, lane2);
+  }
+  // GroupNorm over the head + r.k bonus + gate.  The memory clobber keeps these
+  // loads below the state phase (hoisted, they would hold registers across it).
+  asm volatile("" ::: "memory");
+  const float gv = (float)p.g[tok], lw = (float)p.ln_w[c], lb = (float)p.ln_b[c];
+  const float mean = wave_sum(y) * (1.0f / 64.0f);
+  const float d = y - mean;
+  const float var = wave_sum(d * d) * (1.0f / 64.0f);
+  const float rstd = rsqrtf(var + kGroupNormEps);
+  float z = __builtin_fmaf(d * rstd, lw, lb);
+  z = __builtin_fmaf(rkv, vi, z);
+  p.out[out_index()] = (_Float16)(z * gv);
 }
 
 struct Fp16Args {
@@ -368,6 +477,23 @@ int check_wkv_dims(const char* fn, int B, int T, int C, int H) {
   return VKWR_OK;
 }
 
+// Converts n_blocks 64x64 fp32 state blocks between the standard row-major
+// layout and the interleaved one (float (q*64 + i)*4 + e holds S[i][4q+e]).
+__global__ __launch_bounds__(256) void wkv_state_layout_kernel(int64_t n_blocks, const float* src, float* dst,
+                                                               int to_ilv) {
+  const int64_t n = n_blocks * 1024;  // 16-byte chunks
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < n; t += stride) {
+    const int64_t blk = t >> 10;
+    const int c = (int)(t & 1023);
+    const int i = c >> 4, q = c & 15;  // standard chunk c = (row i, column chunk q)
+    const int64_t std_off = blk * 4096 + (int64_t)c * 4;
+    const int64_t ilv_off = blk * 4096 + ((int64_t)q * kHead + i) * 4;
+    if (to_ilv) *reinterpret_cast<f4*>(dst + ilv_off) = *reinterpret_cast<const f4*>(src + std_off);
+    else *reinterpret_cast<f4*>(dst + std_off) = *reinterpret_cast<const f4*>(src + ilv_off);
+  }
+}
+
 }  // namespace
 }  // namespace vk
 
@@ -409,6 +535,48 @@ extern "C" int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* p
              reinterpret_cast<_Float16*>(y)};
   launch_fp32<true>(p, B, (hipStream_t)stream);
   return check_launch("vkwr_wkv7_fp32_forward_slots");
+}
+
+extern "C" int vkwr_wkv7_decode_fused_f16(int B, int C, int H, float* pool, int n_slots, int state_layout,
+                                          const int32_t* slots, const uint16_t* r, const uint16_t* w,
+                                          const uint16_t* k, const uint16_t* v, const uint16_t* a12,
+                                          const uint16_t* g, const uint16_t* k_k, const uint16_t* a0,
+                                          const uint16_t* k_a, const uint16_t* r_k, const uint16_t* ln_w,
+                                          const uint16_t* ln_b, uint16_t* out, int out_frag,
+                                          void* stream) {
+  clear_error();
+  const char* fn = "vkwr_wkv7_decode_fused_f16";
+  if (int e = check_wkv_dims(fn, B, 1, C, H)) return e;
+  VK_REQUIRE(n_slots >= 0, "%s: negative pool size", fn);
+  VK_REQUIRE(out_frag == 0 || out_frag == 1, "%s: bad out_frag", fn);
+  VK_REQUIRE(state_layout == VKWR_WKV_STATE_STD || state_layout == VKWR_WKV_STATE_ILV, "%s: bad state_layout", fn);
+  VK_REQUIRE(!out_frag || C % kFragPad == 0, "%s: frag output needs C %% %d == 0", fn, kFragPad);
+  if (B == 0 || H == 0) return VKWR_OK;
+  VK_REQUIRE(pool && slots && r && w && k && v && a12 && g && k_k && a0 && k_a && r_k && ln_w && ln_b && out,
+             "%s: null pointer", fn);
+  auto h = [](const uint16_t* x) { return reinterpret_cast<const _Float16*>(x); };
+  FusedArgs p{C, H, n_slots, pool, slots, h(r), h(w), h(k), h(v), h(a12), h(g),
+              h(k_k), h(a0), h(k_a), h(r_k), h(ln_w), h(ln_b), reinterpret_cast<_Float16*>(out), out_frag};
+  if (state_layout == VKWR_WKV_STATE_ILV)
+    hipLaunchKernelGGL(wkv7_decode_fused_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(wkv7_decode_fused_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  return check_launch(fn);
+}
+
+extern "C" int vkwr_wkv7_state_layout_f32(int64_t n_blocks, const float* src, float* dst, int to_layout,
+                                          void* stream) {
+  clear_error();
+  const char* fn = "vkwr_wkv7_state_layout_f32";
+  VK_REQUIRE(n_blocks >= 0, "%s: negative size", fn);
+  VK_REQUIRE(to_layout == VKWR_WKV_STATE_STD || to_layout == VKWR_WKV_STATE_ILV, "%s: bad layout", fn);
+  if (n_blocks == 0) return VKWR_OK;
+  VK_REQUIRE(src && dst && src != dst, "%s: null or aliased pointers", fn);
+  VK_REQUIRE((((uintptr_t)src | (uintptr_t)dst) & 15) == 0, "%s: pointers must be 16-byte aligned", fn);
+  const int64_t blocks = std::min<int64_t>((n_blocks * 1024 + 255) / 256, 16384);
+  hipLaunchKernelGGL(wkv_state_layout_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n_blocks,
+                     src, dst, to_layout == VKWR_WKV_STATE_ILV);
+  return check_launch(fn);
 }
 
 static int launch_fp16(const char* fn, bool legacy, int B, int T, int C, int H, uint16_t* state,

@@ -32,7 +32,12 @@ final LN, and the GEMMs whose output only feeds another GEMM: the low-rank
 inputs and the FFN hidden) write it directly in that layout, so every GEMM is a
 vkwr_frag_gemm_f16 launch streaming the weights with fully coalesced loads.
 The low-rank activations (tanh, sigmoid) are applied to the fp32 accumulator
-of the producing GEMM and rounded to fp16 once.  `frag=False` runs the same
+of the producing GEMM and rounded to fp16 once.  The kk/a gate, the WKV
+update and the GroupNorm/bonus/gate run as one kernel
+(vkwr_wkv7_decode_fused_f16, bit-identical to the three separate launches),
+which streams the WKV pool in the interleaved block layout
+(capi.WKV_STATE_ILV: lane i loads row i with fully coalesced 16-byte loads, no
+LDS staging).  `frag=False` runs the same
 step on row-major weights through vkwr_gemm_f16 (the reference-op GEMM).
 """
 import math
@@ -125,16 +130,35 @@ class RWKV7Model:
 
 class RWKV7State:
     """Per-sequence recurrent state in slot pools: WKV [L, P, H, 64, 64] fp32 and
-    the two token-shift rows [L, P, C] fp16 (time mix, channel mix)."""
+    the two token-shift rows [L, P, C] fp16 (time mix, channel mix).
 
-    def __init__(self, cfg, n_slots, device, std=0.1, seed=1):
+    `layout` is the layout of each 64x64 WKV block: capi.WKV_STATE_STD (row-major,
+    the reference ops' layout) or capi.WKV_STATE_ILV (interleaved; what the fused
+    decode kernel streams, the default).  wkv_standard() returns a row-major copy."""
+
+    def __init__(self, cfg, n_slots, device, std=0.1, seed=1, layout=capi.WKV_STATE_ILV):
         g = torch.Generator(device=device).manual_seed(seed)
         H, C = cfg.n_head, cfg.n_embd
-        self.n_slots = n_slots
+        self.n_slots, self.layout = n_slots, layout
         self.wkv = torch.empty(cfg.n_layer, n_slots, H, HEAD, HEAD, dtype=torch.float32, device=device)
         self.wkv.normal_(0.0, std, generator=g) if std else self.wkv.zero_()
         self.att_shift = torch.zeros(cfg.n_layer, n_slots, C, dtype=torch.float16, device=device)
         self.ffn_shift = torch.zeros(cfg.n_layer, n_slots, C, dtype=torch.float16, device=device)
+
+    def wkv_standard(self):
+        """The WKV pool as row-major [L, P, H, 64, 64] blocks (a copy)."""
+        if self.layout == capi.WKV_STATE_STD:
+            return self.wkv.clone()
+        out = torch.empty_like(self.wkv)
+        capi.wkv_state_layout(self.wkv, out, capi.WKV_STATE_STD)
+        return out
+
+    def set_wkv_standard(self, wkv_std):
+        """Overwrites the pool from row-major blocks."""
+        if self.layout == capi.WKV_STATE_STD:
+            self.wkv.copy_(wkv_std)
+        else:
+            capi.wkv_state_layout(wkv_std.contiguous(), self.wkv, capi.WKV_STATE_ILV)
 
     def bytes_per_token_step(self, cfg):
         """State bytes one decode step moves per sequence (read + write)."""
@@ -147,9 +171,10 @@ FRAG_WEIGHTS = ("Wr", "Wk", "Wv", "Wo", "w1", "w2", "a1", "a2", "g1", "g2", "v1"
 class DecodeEngine:
     """Batched T=1 decode of up to `max_batch` sequences with preallocated buffers."""
 
-    def __init__(self, model, max_batch, frag=True):
+    def __init__(self, model, max_batch, frag=True, fused_wkv=True):
         cfg = model.cfg
         self.model, self.cfg, self.max_batch, self.frag = model, cfg, max_batch, frag
+        self.fused_wkv = fused_wkv  # frag path: gate + WKV + GroupNorm in one kernel
         dev = model.head.device
         B, C, F = max_batch, cfg.n_embd, cfg.dim_ffn
         if frag:
@@ -235,12 +260,17 @@ class DecodeEngine:
                                 v=s.v, v_first=s.v_first, v0=L["v0"]))
             capi.frag_gemm(probs)
             v = (s.v_first if first else s.v_new)[:B]
-            capi.kk_a_gate(B, 1, C, H, s.k[:B], L["k_k"], L["a0"], s.a12[:B], L["k_a"], s.new_k[:B],
-                           s.neg_kk[:B], s.kka[:B])
-            capi.wkv_slots(B, 1, C, H, state.wkv[l], slots, s.r[:B], s.w[:B], s.new_k[:B], v, s.neg_kk[:B],
-                           s.kka[:B], s.y[:B])
-            capi.groupnorm_bonus_gate(B, 1, C, H, s.y[:B], s.r[:B], s.new_k[:B], v, L["r_k"], L["lnx_w"],
-                                      L["lnx_b"], s.g[:B], s.o_in_f, frag=True)
+            if s.fused_wkv:
+                capi.wkv_decode_fused(B, C, H, state.wkv[l], slots, s.r, s.w, s.k, v, s.a12, s.g, L["k_k"],
+                                      L["a0"], L["k_a"], L["r_k"], L["lnx_w"], L["lnx_b"], s.o_in_f, frag=True,
+                                      state_layout=state.layout)
+            else:
+                capi.kk_a_gate(B, 1, C, H, s.k[:B], L["k_k"], L["a0"], s.a12[:B], L["k_a"], s.new_k[:B],
+                               s.neg_kk[:B], s.kka[:B])
+                capi.wkv_slots(B, 1, C, H, state.wkv[l], slots, s.r[:B], s.w[:B], s.new_k[:B], v,
+                               s.neg_kk[:B], s.kka[:B], s.y[:B])
+                capi.groupnorm_bonus_gate(B, 1, C, H, s.y[:B], s.r[:B], s.new_k[:B], v, L["r_k"], L["lnx_w"],
+                                          L["lnx_b"], s.g[:B], s.o_in_f, frag=True)
             capi.frag_gemm([fp(s.o_in_f, P["Wo"], s.o, B, C, C)])
             # ---- channel mix
             res2 = s.res[(l + 1) % 2][:B]
@@ -298,7 +328,9 @@ class DecodeEngine:
         B = tokens.shape[0]
         assert 0 < B <= self.max_batch and slots.shape[0] == B
         if self.frag:
+            assert self.fused_wkv or state.layout == capi.WKV_STATE_STD, "unfused WKV needs the row-major pool"
             return self._step_frag(state, tokens, slots)
+        assert state.layout == capi.WKV_STATE_STD, "the row-major engine needs the row-major WKV pool"
         cfg, m, s = self.cfg, self.model, self
         C, H = cfg.n_embd, cfg.n_head
         ws = self.ws
