@@ -1,7 +1,8 @@
-"""Pins the LayerNorm / GroupNorm / token-shift / gate oracle (oracle/ops_ref.py)
-against independent routines: torch's float64 layer_norm, group_norm,
-normalize, lerp and sigmoid, and brute-force loops for the token shift.
-A planted mistake (unbiased variance) is shown to be caught."""
+"""Pins the LayerNorm / GroupNorm / token-shift / gate / GEMM oracle
+(oracle/ops_ref.py) against independent routines: torch's float64 layer_norm,
+group_norm, normalize, lerp, sigmoid and matmul, and brute-force loops for the
+token shift, the GEMM and the channel mix.  Planted mistakes (unbiased
+variance, a transposed weight) are shown to be caught."""
 import numpy as np
 import pytest
 import torch
@@ -156,3 +157,67 @@ def test_ulp16():
     assert R.ulp16(2.0) == 2 ** -9
     assert R.ulp16(0.0) == 2 ** -24
     assert R.ulp16(65504.0) == 32.0
+
+
+# ---------------------------------------------------------------- GEMM oracle
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_gemm_matches_torch_and_brute_force(layout):
+    a = h(5, 37)
+    w = h(23, 37, scale=0.1) if layout == "nk" else h(37, 23, scale=0.1)
+    y, abs_sum = R.gemm(a, w, layout)
+    wt = t64(w).t() if layout == "nk" else t64(w)
+    assert np.array_equal(y, (t64(a) @ wt).numpy().astype(np.float16))
+    assert np.allclose(abs_sum, (t64(a).abs() @ wt.abs()).numpy())
+    # brute-force loop on a few entries
+    for i, j in [(0, 0), (4, 22), (2, 11)]:
+        s = sum(float(a[i, k]) * float(w[j, k] if layout == "nk" else w[k, j]) for k in range(37))
+        assert abs(float(y[i, j]) - s) <= float(R.ulp16(s))
+
+
+def test_gemm_planted_transposition_is_caught():
+    a, w = h(8, 16), h(16, 16, scale=0.1)  # square: both layouts are shape-valid
+    y_nk, _ = R.gemm(a, w, "nk")
+    y_kn, _ = R.gemm(a, w, "kn")
+    assert not np.array_equal(y_nk, y_kn)
+    assert np.array_equal(y_nk, R.gemm(a, np.ascontiguousarray(w.T), "kn")[0])
+
+
+def test_gemm_activation_and_epilogues():
+    a, w = h(6, 40), h(30, 40, scale=0.2)
+    for act, f in (("tanh", torch.tanh), ("sigmoid", torch.sigmoid), ("relu2", lambda x: torch.relu(x) ** 2)):
+        a_act = f(t64(a)).numpy()
+        y, _ = R.gemm(a, w, "nk", a_act=act)  # round_act: the activation is rounded to fp16 first
+        assert np.array_equal(y, (torch.from_numpy(a_act.astype(np.float16).astype(np.float64)) @ t64(w).t())
+                              .numpy().astype(np.float16))
+        y32, _ = R.gemm(a, w, "nk", a_act=act, round_act=False)
+        assert np.array_equal(y32, (torch.from_numpy(a_act) @ t64(w).t()).numpy().astype(np.float16))
+    acc = (t64(a) @ t64(w).t()).numpy()
+    y, _ = R.gemm(a, w, "nk", epi="relu2")
+    assert np.array_equal(y, R.relu_square(acc))
+    v, vf, v0 = h(6, 30), h(6, 30), h(30)
+    y, _ = R.gemm(a, w, "nk", epi="vres", v=v, v_first=vf, v0=v0)
+    assert np.array_equal(y, R.vres_gate(v, vf, v0, acc))  # the independently pinned gate on the fp64 accumulator
+    eye = np.eye(40, dtype=np.float16)
+    assert np.array_equal(R.gemm(a, eye, "nk")[0], a)  # identity weight
+
+
+def test_cmix_sparse_brute_force():
+    B, T, C, F = 2, 3, 8, 5
+    x, shift = h(B, T, C), h(B, C)
+    x_k = rng.random(C).astype(np.float16)
+    key, value = h(F, C, scale=0.3), h(F, C, scale=0.3)
+    shift_ref = shift.copy()
+    out, act, _ = R.cmix_sparse(x, shift, x_k, key, value)
+    assert np.array_equal(shift, x[:, -1])
+    for b in range(B):
+        for t in range(T):
+            prev = shift_ref[b] if t == 0 else x[b, t - 1]
+            mixed = [np.float16(float(x[b, t, c]) + (float(prev[c]) - float(x[b, t, c])) * float(x_k[c]))
+                     for c in range(C)]
+            hid = [np.float16(max(sum(float(mixed[c]) * float(key[f, c]) for c in range(C)), 0.0) ** 2)
+                   for f in range(F)]
+            assert np.array_equal(np.array(hid, dtype=np.float16), act[b * T + t])
+            for c in range(C):
+                s = sum(float(hid[f]) * float(value[f, c]) for f in range(F))
+                assert abs(float(out[b, t, c]) - s) <= float(R.ulp16(s))
