@@ -44,6 +44,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--model-steps", type=int, default=20,
                     help="timed decode steps of the 1.5B-shape model at bs=128 (0: skip)")
+    ap.add_argument("--serve-steps", type=int, default=3,
+                    help="timed steps of the 7B mixed prefill+decode step (BASELINE config 4; 0: skip)")
     ap.add_argument("--rowmajor-gemm", action="store_true",
                     help="run the model decode step on the row-major GEMM instead of the frag GEMM")
     ap.add_argument("--eager", action="store_true",
@@ -156,6 +158,55 @@ def model_decode(dev, steps, warmup=3, frag=True):
         "gemm_tflops": round(flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
         "gemm_path": "frag (vkwr_frag_gemm_f16, weights packed at load)" if frag else "row-major (vkwr_gemm_f16)",
         "timing": "one decode step captured as a HIP graph, replayed; HIP events on the replay stream",
+    }
+
+
+def serve_mixed_7b(dev, steps, warmup=1):
+    """the RWKV-7 7B shape (L=32, C=4096, F=16384, random fp16 weights),
+    one continuous-batching step = 256 decode rows + 4 prefill chunks of 512 tokens
+    (2304 GEMM rows) on a 2048-slot fp32 state pool.  Eager launches (shapes vary per
+    step in serving); HIP events on the current stream."""
+    from vkwr_amd import capi
+    from vkwr_amd.model_executor import MixedEngine, RWKV7Config, RWKV7Model, RWKV7State
+    from vkwr_amd.model_executor.mixed import gemm_flops
+
+    cfg = RWKV7Config.preset("7b")
+    Bd, Bp, T, P = 256, 4, 512, 2048
+    model = RWKV7Model(cfg, dev, seed=0)
+    state = RWKV7State(cfg, P, dev, std=0.1, seed=1, layout=capi.WKV_STATE_STD)
+    eng = MixedEngine(model, Bd + Bp * T, max_seqs=Bd + Bp)
+    g = torch.Generator().manual_seed(5)
+    dec = (torch.randint(0, cfg.vocab, (Bd,), generator=g).to(torch.int32).to(dev),
+           torch.arange(0, Bd, dtype=torch.int32).to(dev))
+    pre = [(torch.randint(0, cfg.vocab, (Bp, T), generator=g).to(torch.int32).to(dev),
+            torch.arange(Bd, Bd + Bp, dtype=torch.int32).to(dev))]
+    for _ in range(warmup):
+        eng.step(state, decode=dec, prefill=pre)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        eng.step(state, decode=dec, prefill=pre)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    rows = Bd + Bp * T
+    tflops = gemm_flops(cfg, rows, Bd + Bp) / (ms * 1e-3) / 1e12
+    del eng, state, model
+    torch.cuda.empty_cache()
+    return {
+        "workload": "RWKV-7 7B shape (BASELINE config 4): L=32, C=4096, H=64, F=16384, ranks w/a/v/g "
+                    "128/128/96/480, V=65536; one continuous-batching step = 256 decode rows + 4 prefill "
+                    "chunks x 512 tokens (2304 GEMM rows), 2048-slot fp32 state pool, random fp16 weights",
+        "ms_per_step": round(ms, 3),
+        "steps": steps,
+        "rows_per_step": rows,
+        "tokens_per_s": round(rows / (ms * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4),
+                     "flops_per_step": gemm_flops(cfg, rows, Bd + Bp)},
+        "gemm_path": "row-major vkwr_gemm_f16 (128x128 MFMA tiles)",
+        "timing": "eager launches, HIP events around the timed steps",
     }
 
 
@@ -315,6 +366,9 @@ def main():
         del inputs
         torch.cuda.empty_cache()
         result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm)
+        torch.cuda.empty_cache()
+    if args.serve_steps > 0 and not args.eager:
+        result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

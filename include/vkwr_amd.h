@@ -216,6 +216,17 @@ VKWR_EXPORT int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
                                          const uint16_t* const* mix, uint16_t* const* out,
                                          int half_math, void* stream);
 
+/* Token-shift lerp of T tokens for B sequences whose shift rows live in a slot
+ * pool: sequence b's shift row is shift_pool[shift_slots[b]] (the caller
+ * guarantees distinct, in-range slots); otherwise identical to
+ * vkwr_token_shift_mix_f16.  No single reference function: replaces gathering
+ * the shift rows, tmix_mix6 / cmix_mix (csrc/v1/mix/mix_ops.cu:42-160,
+ * 432-462) and scattering them back, for the mixed prefill + decode step. */
+VKWR_EXPORT int vkwr_token_shift_mix_slots_f16(int B, int T, int C, const uint16_t* x, uint16_t* shift_pool,
+                                               const int32_t* shift_slots, int n_mix,
+                                               const uint16_t* const* mix, uint16_t* const* out,
+                                               int half_math, void* stream);
+
 /* Per-head key normalisation and in-context learning-rate gate of RWKV-7 time mix:
  *   u = k * k_k; kk = u / max(||u||_2 over the head, 1e-12); a = sigmoid(a0 + a12);
  *   new_k = k * (a * k_a + (1 - k_a)); neg_kk = -kk; kka = kk * a.

@@ -1,0 +1,121 @@
+"""GPU tests of the mixed prefill + decode step (vkwr_amd.model_executor.mixed)
+and the continuous-batching scheduler (scheduler.py) on the tiny RWKV-7 shape.
+
+Bar: a prefill chunk of T tokens gives the last-token logits and recurrent
+state of T decode steps, decode rows give DecodeEngine's logits, and groups
+batched into one step give what each gives alone -- all at the end-to-end
+logits tolerance 5e-2 of the north_star (measured differences are fp16
+rounding flips of GEMM outputs between launches of different M).  The
+scheduler's greedy tokens are checked against a teacher-forced replay of each
+request on DecodeEngine: every emitted token must be an argmax of the replay's
+logits to within that tolerance (robust to near ties), and the decode and
+prefill paths (with slot reuse: fewer slots than requests) must agree.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-2
+
+
+def _tiny(gpu, n_slots, seed=0):
+    from vkwr_amd import capi
+    from vkwr_amd.model_executor import RWKV7Config, RWKV7Model, RWKV7State
+    cfg = RWKV7Config.preset("tiny")
+    model = RWKV7Model(cfg, gpu, seed=seed)
+    state = RWKV7State(cfg, n_slots, gpu, std=0.1, seed=seed + 1, layout=capi.WKV_STATE_STD)
+    return cfg, model, state
+
+
+def _clone(state):
+    import copy
+    s = copy.copy(state)
+    s.wkv, s.att_shift, s.ffn_shift = state.wkv.clone(), state.att_shift.clone(), state.ffn_shift.clone()
+    return s
+
+
+def _i32(x, gpu):
+    return torch.tensor(x, dtype=torch.int32, device=gpu)
+
+
+def test_decode_rows_match_decode_engine(gpu):
+    from vkwr_amd.model_executor import DecodeEngine, MixedEngine
+    cfg, model, state = _tiny(gpu, 12)
+    s2 = _clone(state)
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.randint(0, cfg.vocab, (6,), generator=g).to(torch.int32).to(gpu)
+    slots = _i32([7, 0, 3, 11, 5, 2], gpu)
+    ref = DecodeEngine(model, 8, frag=False).step(state, tokens, slots).float()
+    got = MixedEngine(model, 64).step(s2, decode=(tokens, slots)).float()
+    assert (got - ref).abs().max().item() <= TOL
+    assert (s2.wkv - state.wkv).abs().max().item() <= 1e-3
+    assert (s2.att_shift.float() - state.att_shift.float()).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("T", [1, 5, 16])
+def test_prefill_chunk_equals_decode_steps(gpu, T):
+    from vkwr_amd.model_executor import DecodeEngine, MixedEngine
+    cfg, model, state = _tiny(gpu, 6)
+    s2 = _clone(state)
+    g = torch.Generator().manual_seed(T)
+    tokens = torch.randint(0, cfg.vocab, (3, T), generator=g).to(torch.int32).to(gpu)
+    slots = _i32([4, 1, 2], gpu)
+    eng = DecodeEngine(model, 4, frag=False)
+    for t in range(T):
+        ref = eng.step(state, tokens[:, t].contiguous(), slots).float().clone()
+    got = MixedEngine(model, 64).step(s2, prefill=[(tokens, slots)]).float()
+    assert (got - ref).abs().max().item() <= TOL
+    sl = slots.long()
+    assert (s2.wkv[:, sl] - state.wkv[:, sl]).abs().max().item() <= 2e-2
+    others = [i for i in range(6) if i not in slots.tolist()]
+    assert torch.equal(s2.wkv[:, others], state.wkv[:, others])
+
+
+def test_mixed_groups_equal_separate_steps(gpu):
+    from vkwr_amd.model_executor import MixedEngine
+    cfg, model, state = _tiny(gpu, 16)
+    g = torch.Generator().manual_seed(9)
+    dec = (torch.randint(0, cfg.vocab, (4,), generator=g).to(torch.int32).to(gpu), _i32([0, 1, 2, 3], gpu))
+    p1 = (torch.randint(0, cfg.vocab, (2, 7), generator=g).to(torch.int32).to(gpu), _i32([4, 5], gpu))
+    p2 = (torch.randint(0, cfg.vocab, (3, 3), generator=g).to(torch.int32).to(gpu), _i32([6, 7, 8], gpu))
+    eng = MixedEngine(model, 64)
+    sa = _clone(state)
+    both = eng.step(sa, decode=dec, prefill=[p1, p2]).float().clone()
+    sb = _clone(state)
+    parts = [eng.step(sb, decode=dec).float().clone(), eng.step(sb, prefill=[p1]).float().clone(),
+             eng.step(sb, prefill=[p2]).float().clone()]
+    assert (both - torch.cat(parts)).abs().max().item() <= TOL
+    assert (sa.wkv - sb.wkv).abs().max().item() <= 2e-2
+
+
+def test_scheduler_matches_teacher_forced_replay(gpu):
+    """12 requests, prompts 1..23 tokens (chunk 8, so up to three chunks), budgets 1..6 tokens,
+    only 5 slots: admission waits for slots, slots are recycled and reset."""
+    from vkwr_amd.model_executor import ContinuousBatcher, DecodeEngine, MixedEngine
+    cfg, model, state = _tiny(gpu, 5)
+    g = torch.Generator().manual_seed(11)
+    eng = MixedEngine(model, 48, max_seqs=16)
+    sched = ContinuousBatcher(eng, state, max_decode=4, max_prefill_chunks=2, chunk=8)
+    reqs = []
+    for i in range(12):
+        n = 1 + int(torch.randint(0, 23, (1,), generator=g))
+        prompt = torch.randint(0, cfg.vocab, (n,), generator=g).tolist()
+        reqs.append(sched.submit(prompt, 1 + i % 6))
+    done = sched.run(max_steps=400)
+    assert len(done) == 12 and all(r.done for r in reqs)
+    assert sched.slots.available == 5
+    # replay each request alone on a fresh slot, teacher-forced with the scheduler's tokens
+    from vkwr_amd import capi
+    from vkwr_amd.model_executor import RWKV7State
+    ref_state = RWKV7State(cfg, 1, gpu, std=0.0, layout=capi.WKV_STATE_STD)
+    dec = DecodeEngine(model, 1, frag=False)
+    slot = _i32([0], gpu)
+    for r in reqs:
+        ref_state.wkv.zero_(), ref_state.att_shift.zero_(), ref_state.ffn_shift.zero_()
+        seq = r.prompt + r.output
+        for t in range(len(r.prompt) + len(r.output) - 1):
+            logits = dec.step(ref_state, _i32([seq[t]], gpu), slot).float()[0]
+            if t >= len(r.prompt) - 1:
+                tok = seq[t + 1]
+                assert logits[tok] >= logits.max() - TOL, (r.rid, t, float(logits.max() - logits[tok]))

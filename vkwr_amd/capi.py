@@ -83,6 +83,8 @@ _wkv_fused = _sig("vkwr_wkv7_decode_fused_f16", [_i, _i, _i, _p, _i, _i, _p] + [
 _wkv_layout = _sig("vkwr_wkv7_state_layout_f32", [_i64, _p, _p, _i, _p])
 WKV_STATE_STD, WKV_STATE_ILV = 0, 1
 _shift = _sig("vkwr_token_shift_mix_f16", [_i, _i, _i, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
+_shift_slots = _sig("vkwr_token_shift_mix_slots_f16",
+                    [_i, _i, _i, _p, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 
 
 def _check(st, what):
@@ -216,8 +218,13 @@ def wkv_state_layout(src, dst, to_layout):
     _check(_wkv_layout(src.numel() // 4096, _ptr(src), _ptr(dst), to_layout, _stream()), "vkwr_wkv7_state_layout_f32")
 
 
-def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False):
+def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False, shift_slots=None):
+    """Token-shift lerp of [B,T,C] x; shift_state [B,C], or a pool [P,C] indexed by shift_slots [B]."""
     mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
-    _check(_shift(B, T, C, _ptr(x), _ptr(shift_state), len(mixes), mp, op, 1 if half_math else 0, _stream()),
-           "vkwr_token_shift_mix_f16")
+    if shift_slots is None:
+        _check(_shift(B, T, C, _ptr(x), _ptr(shift_state), len(mixes), mp, op, 1 if half_math else 0, _stream()),
+               "vkwr_token_shift_mix_f16")
+    else:
+        _check(_shift_slots(B, T, C, _ptr(x), _ptr(shift_state), _ptr(shift_slots), len(mixes), mp, op,
+                            1 if half_math else 0, _stream()), "vkwr_token_shift_mix_slots_f16")

@@ -27,6 +27,7 @@ struct ShiftArgs {
   int B, T, C;
   const _Float16* x;
   _Float16* shift;
+  const int32_t* shift_slots;  // may be null: sequence b uses shift row b
   const _Float16* mix[6];
   _Float16* out[6];
 };
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(256) void token_shift_kernel(ShiftArgs p) {
     for (int e = 0; e < VW; ++e) mu[i][e] = p.mix[i][c0 + e];
 
   _Float16 prev[VW];
-  const int64_t srow = (int64_t)b * p.C + c0;
+  const int64_t srow = (int64_t)(p.shift_slots ? p.shift_slots[b] : b) * p.C + c0;
   const _Float16* xs = p.x + ((int64_t)b * p.T) * p.C + c0;
   if (t0 == 0) {
 #pragma unroll
@@ -225,12 +226,10 @@ void launch_shift(const ShiftArgs& p, bool half, unsigned blocks, hipStream_t s)
 
 using namespace vk;
 
-extern "C" int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
-                                        uint16_t* shift_state, int n_mix,
-                                        const uint16_t* const* mix, uint16_t* const* out,
-                                        int half_math, void* stream) {
-  clear_error();
-  const char* fn = "vkwr_token_shift_mix_f16";
+namespace {
+int token_shift_mix(const char* fn, int B, int T, int C, const uint16_t* x, uint16_t* shift_state,
+                    const int32_t* shift_slots, int n_mix, const uint16_t* const* mix, uint16_t* const* out,
+                    int half_math, void* stream) {
   VK_REQUIRE(B >= 0 && T >= 0 && C >= 0, "%s: negative size", fn);
   VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
   if ((int64_t)B * T * C == 0) return VKWR_OK;
@@ -241,6 +240,7 @@ extern "C" int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
   p.C = C;
   p.x = reinterpret_cast<const _Float16*>(x);
   p.shift = reinterpret_cast<_Float16*>(shift_state);
+  p.shift_slots = shift_slots;
   bool vec = (C % 8 == 0) && aligned16(x) && aligned16(shift_state);
   for (int i = 0; i < n_mix; ++i) {
     VK_REQUIRE(mix[i] && out[i], "%s: null pointer", fn);
@@ -262,6 +262,26 @@ extern "C" int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
     else launch_shift<1, 6>(p, half, blocks, s);
   }
   return check_launch(fn);
+}
+}  // namespace
+
+extern "C" int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
+                                        uint16_t* shift_state, int n_mix,
+                                        const uint16_t* const* mix, uint16_t* const* out,
+                                        int half_math, void* stream) {
+  clear_error();
+  return token_shift_mix("vkwr_token_shift_mix_f16", B, T, C, x, shift_state, nullptr, n_mix, mix, out, half_math,
+                         stream);
+}
+
+extern "C" int vkwr_token_shift_mix_slots_f16(int B, int T, int C, const uint16_t* x, uint16_t* shift_pool,
+                                              const int32_t* shift_slots, int n_mix,
+                                              const uint16_t* const* mix, uint16_t* const* out,
+                                              int half_math, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_token_shift_mix_slots_f16";
+  VK_REQUIRE((int64_t)B * T * C == 0 || shift_slots, "%s: null shift_slots", fn);
+  return token_shift_mix(fn, B, T, C, x, shift_pool, shift_slots, n_mix, mix, out, half_math, stream);
 }
 
 extern "C" int vkwr_tmix_kk_a_gate_f16(int B, int T, int C, int H, const uint16_t* k,

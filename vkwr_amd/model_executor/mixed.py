@@ -1,0 +1,185 @@
+"""RWKV-7 forward step over a mixed batch: decode rows plus prefill chunks.
+
+A continuous-batching server (256 decode rows plus 4 prefill
+chunks of 512 tokens per step on the 7B shape) runs every row of a step through
+the same projection / FFN GEMM launches -- M = all rows, so the GEMMs are large
+and matrix-core bound -- while the per-sequence recurrent parts run per group:
+
+  group = (B sequences, T tokens each, first row, slots); decode rows form one
+          group with T = 1, each prefill chunk length another.
+
+Per layer (x: previous block output, res: residual stream, rows = all rows):
+  res, xx = add + LN1 over rows
+  xr..xg  = token-shift lerps per group (slot-indexed att shift pool)
+  r, k, v, w1, a1, g1, v1 = projections over rows            (one GEMM launch)
+  w, a12, g, v = low-rank outputs (tanh / - / sigmoid / value residual) (one launch)
+  k', -kk, kk*a = kk/a gate over rows
+  y   = WKV-7 per group on the slot pool (T = 1 decode kernel, T > 1 prefill kernel)
+  o   = (GroupNorm(y) + bonus) * g  W_o^T over rows
+  res, xx = add + LN2; xk = token shift per group (ffn shift pool)
+  x   = relu(xk K^T)^2 V^T over rows
+logits of the last row of every group's sequences = LN_out(x + res) Head^T.
+
+The same layer composition as DecodeEngine (rwkv7.py), on the reference-op GEMM
+(vkwr_gemm_f16, row-major weights) and the row-major WKV pool.  A prefill chunk
+of T tokens gives the same recurrent state and last-token logits as T decode
+steps (same arithmetic per token, GEMM rows independent); tests/test_serving_gpu.py
+checks that, and the decode rows against DecodeEngine.
+
+Every buffer is preallocated for `max_rows` rows, so a step allocates nothing.
+"""
+import torch
+
+from vkwr_amd import capi
+from vkwr_amd.model_executor.rwkv7 import HEAD
+
+TMIX_MIX = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
+
+
+class MixedEngine:
+    """Forward step over up to `max_rows` rows in decode and prefill groups."""
+
+    def __init__(self, model, max_rows, max_seqs=None):
+        cfg = model.cfg
+        self.model, self.cfg, self.max_rows = model, cfg, max_rows
+        self.max_seqs = max_seqs or max_rows
+        dev = model.head.device
+        R, C, F = max_rows, cfg.n_embd, cfg.dim_ffn
+
+        def buf(*shape):
+            return torch.empty(*shape, dtype=torch.float16, device=dev)
+
+        self.tok = torch.empty(R, dtype=torch.int32, device=dev)
+        self.x0 = buf(R, C)
+        self.res = [buf(R, C), buf(R, C)]
+        self.xx = buf(R, C)
+        self.mix = [buf(R, C) for _ in range(6)]
+        self.r, self.k, self.v, self.v_first, self.v_new = (buf(R, C) for _ in range(5))
+        self.w1, self.a1, self.g1, self.v1 = buf(R, cfg.rank_w), buf(R, cfg.rank_a), buf(R, cfg.rank_g), buf(R, cfg.rank_v)
+        self.w, self.a12, self.g = buf(R, C), buf(R, C), buf(R, C)
+        self.new_k, self.neg_kk, self.kka, self.y, self.o_in, self.o = (buf(R, C) for _ in range(6))
+        self.xk = buf(R, C)
+        self.act = buf(R, F)
+        self.ffn = buf(R, C)
+        self.h = buf(self.max_seqs, C)
+        self.logits = buf(self.max_seqs, cfg.vocab)
+        sizes = sorted({max_rows} | {1 << i for i in range(20) if (1 << i) <= max_rows})
+        need = max(capi.gemm_workspace_bytes(ps) for m in sizes for ps in self._gemm_batches(m, 1))
+        need = max(need, max(capi.gemm_workspace_bytes(self._head_problem(s)) for s in
+                             sorted({self.max_seqs} | {1 << i for i in range(20) if (1 << i) <= self.max_seqs})))
+        self.ws = torch.empty(max(need, 0), dtype=torch.uint8, device=dev)
+
+    # -- GEMM batches (shared by planning and execution)
+    def _proj(self, L, R, first):
+        s, gp = self, capi.gemm_problem
+        ps = [gp(s.mix[0][:R], L["Wr"], s.r[:R]), gp(s.mix[2][:R], L["Wk"], s.k[:R]),
+              gp(s.mix[3][:R], L["Wv"], (s.v_first if first else s.v)[:R]),
+              gp(s.mix[1][:R], L["w1"], s.w1[:R]), gp(s.mix[4][:R], L["a1"], s.a1[:R]),
+              gp(s.mix[5][:R], L["g1"], s.g1[:R])]
+        if not first:
+            ps.append(gp(s.mix[3][:R], L["v1"], s.v1[:R]))
+        return ps
+
+    def _rank_out(self, L, R, first):
+        s, gp = self, capi.gemm_problem
+        ps = [gp(s.w1[:R], L["w2"], s.w[:R], a_act=capi.ACT_TANH, epilogue=capi.EPI_BIAS, v0=L["w0"]),
+              gp(s.a1[:R], L["a2"], s.a12[:R]),
+              gp(s.g1[:R], L["g2"], s.g[:R], a_act=capi.ACT_SIGMOID)]
+        if not first:
+            ps.append(gp(s.v1[:R], L["v2"], s.v_new[:R], epilogue=capi.EPI_VALUE_RESIDUAL, v=s.v[:R],
+                         v_first=s.v_first[:R], v0=L["v0"]))
+        return ps
+
+    def _gemm_batches(self, R, nl):
+        m, s, gp = self.model, self, capi.gemm_problem
+        out = []
+        for l, L in enumerate(m.layers[:max(nl, 2)]):
+            out += [self._proj(L, R, l == 0), self._rank_out(L, R, l == 0)]
+        L = m.layers[-1]
+        out += [[gp(s.o_in[:R], L["Wo"], s.o[:R])],
+                [gp(s.xk[:R], L["key"], s.act[:R], epilogue=capi.EPI_RELU_SQUARE)],
+                [gp(s.act[:R], L["value"], s.ffn[:R])]]
+        return out
+
+    def _head_problem(self, S):
+        return [capi.gemm_problem(self.h[:S], self.model.head, self.logits[:S])]
+
+    # -- the step
+    def step(self, state, decode=None, prefill=()):
+        """decode: (tokens [Bd] int32, slots [Bd] int32) or None; prefill: sequence of
+        (tokens [Bg, Tg] int32, slots [Bg] int32).  All on the device, slots distinct over the
+        whole step and < state.n_slots.  Updates `state` in place and returns logits
+        [Bd + sum Bg, V]: the decode rows, then each prefill sequence's last chunk token
+        (a view valid until the next step)."""
+        cfg, m, s = self.cfg, self.model, self
+        assert state.layout == capi.WKV_STATE_STD, "the mixed step uses the row-major WKV pool"
+        C, H = cfg.n_embd, cfg.n_head
+        groups = []  # (B, T, row0, slots, seq0)
+        row, seq = 0, 0
+        if decode is not None:
+            tokens, slots = decode
+            B = tokens.shape[0]
+            s.tok[row:row + B].copy_(tokens)
+            groups.append((B, 1, row, slots, seq))
+            row, seq = row + B, seq + B
+        for tokens, slots in prefill:
+            B, T = tokens.shape
+            s.tok[row:row + B * T].copy_(tokens.reshape(-1))
+            groups.append((B, T, row, slots, seq))
+            row, seq = row + B * T, seq + B
+        R, S = row, seq
+        assert 0 < R <= self.max_rows and S <= self.max_seqs
+        ws = self.ws
+        torch.index_select(m.emb, 0, s.tok[:R], out=s.x0[:R])
+        x, res_in = s.x0[:R], None
+        for l, L in enumerate(m.layers):
+            first = l == 0
+            res = s.res[l % 2][:R]
+            # ---- time mix
+            capi.layer_norm(x, L["ln1_w"], L["ln1_b"], s.xx[:R], residual=res_in, x_out=res)  # res = x + res_in
+            mixes = [L[k] for k in TMIX_MIX]
+            for B, T, r0, slots, _ in groups:
+                n = B * T
+                capi.token_shift(B, T, C, s.xx[r0:r0 + n], state.att_shift[l], mixes,
+                                 [t[r0:r0 + n] for t in s.mix], shift_slots=slots)
+            capi.gemm(self._proj(L, R, first), ws)
+            capi.gemm(self._rank_out(L, R, first), ws)
+            v = (s.v_first if first else s.v_new)[:R]
+            capi.kk_a_gate(R, 1, C, H, s.k[:R], L["k_k"], L["a0"], s.a12[:R], L["k_a"], s.new_k[:R],
+                           s.neg_kk[:R], s.kka[:R])
+            for B, T, r0, slots, _ in groups:
+                n = B * T
+                sl = slice(r0, r0 + n)
+                capi.wkv_slots(B, T, C, H, state.wkv[l], slots, s.r[sl], s.w[sl], s.new_k[sl], v[sl],
+                               s.neg_kk[sl], s.kka[sl], s.y[sl])
+            capi.groupnorm_bonus_gate(R, 1, C, H, s.y[:R], s.r[:R], s.new_k[:R], v, L["r_k"], L["lnx_w"],
+                                      L["lnx_b"], s.g[:R], s.o_in[:R])
+            capi.gemm([capi.gemm_problem(s.o_in[:R], L["Wo"], s.o[:R])], ws)
+            # ---- channel mix
+            res2 = s.res[(l + 1) % 2][:R]
+            capi.layer_norm(s.o[:R], L["ln2_w"], L["ln2_b"], s.xx[:R], residual=res, x_out=res2)
+            for B, T, r0, slots, _ in groups:
+                n = B * T
+                capi.token_shift(B, T, C, s.xx[r0:r0 + n], state.ffn_shift[l], [L["x_k_ffn"]],
+                                 [s.xk[r0:r0 + n]], shift_slots=slots)
+            capi.gemm([capi.gemm_problem(s.xk[:R], L["key"], s.act[:R], epilogue=capi.EPI_RELU_SQUARE)], ws)
+            capi.gemm([capi.gemm_problem(s.act[:R], L["value"], s.ffn[:R])], ws)
+            x, res_in = s.ffn[:R], res2
+        for B, T, r0, _, q0 in groups:
+            n = B * T
+            capi.add_last_layer_norm(B, T, C, x[r0:r0 + n], res_in[r0:r0 + n], m.ln_out_w, m.ln_out_b,
+                                     s.h[q0:q0 + B])
+        capi.gemm(self._head_problem(S), ws)
+        return s.logits[:S]
+
+
+def gemm_flops(cfg, rows, seqs):
+    """Matrix-core flops of one mixed step: every projection and FFN GEMM over `rows`
+    rows, the head over `seqs` rows."""
+    C, F = cfg.n_embd, cfg.dim_ffn
+    r = cfg.rank_w + cfg.rank_a + cfg.rank_g + cfg.rank_v
+    per_layer = 2 * rows * (4 * C * C + 2 * C * r + 2 * C * F)
+    return cfg.n_layer * per_layer + 2 * seqs * C * cfg.vocab
+
+
+__all__ = ["MixedEngine", "gemm_flops", "HEAD"]

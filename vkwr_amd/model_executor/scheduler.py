@@ -1,0 +1,151 @@
+"""Continuous batching over a WKV slot pool (the reference has no serving code).
+
+Requests arrive with a prompt and a generation budget.  The batcher admits them
+into free slots of the recurrent-state pool (resetting the slot's WKV state and
+both shift rows), then every step runs one MixedEngine forward over
+
+  * up to `max_decode` sequences that are generating (one token each: the last
+    token they produced), and
+  * up to `max_prefill_chunks` prompt chunks of at most `chunk` tokens from
+    sequences still consuming their prompt (chunks of equal length share one
+    prefill group),
+
+within `max_rows` rows in total.  A sequence's first generated token comes from
+the logits of its last prompt chunk; each later one from its decode row.
+Finished sequences release their slot immediately, so waiting requests are
+admitted the next step (256 decode rows + 4 x 512 prefill
+rows per step, 2048-slot pool).  The default sampler is greedy (argmax); pass
+`sample` to use another.
+"""
+from collections import deque
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass
+class Request:
+    prompt: list
+    max_new_tokens: int
+    rid: int = -1
+    slot: int = -1
+    pos: int = 0                       # prompt tokens consumed
+    output: list = field(default_factory=list)
+
+    @property
+    def prefilling(self):
+        return self.pos < len(self.prompt)
+
+    @property
+    def done(self):
+        return len(self.output) >= self.max_new_tokens
+
+
+class SlotAllocator:
+    """Free list over the state pool's slots (FIFO reuse)."""
+
+    def __init__(self, n_slots):
+        self.n_slots = n_slots
+        self._free = deque(range(n_slots))
+
+    def alloc(self):
+        return self._free.popleft() if self._free else None
+
+    def free(self, slot):
+        assert 0 <= slot < self.n_slots
+        self._free.append(slot)
+
+    @property
+    def available(self):
+        return len(self._free)
+
+
+class ContinuousBatcher:
+    def __init__(self, engine, state, max_decode=256, max_prefill_chunks=4, chunk=512, sample=None):
+        assert chunk >= 1 and max_decode + chunk <= engine.max_rows
+        self.engine, self.state = engine, state
+        self.max_decode, self.max_prefill_chunks, self.chunk = max_decode, max_prefill_chunks, chunk
+        self.max_rows = engine.max_rows
+        self.slots = SlotAllocator(state.n_slots)
+        self.waiting = deque()
+        self.running = []
+        self.sample = sample or (lambda logits: torch.argmax(logits.float(), dim=-1))
+        self.device = engine.model.head.device
+        self._next_id = 0
+        self.steps = 0
+        self.tokens_processed = 0
+
+    def submit(self, prompt, max_new_tokens):
+        assert len(prompt) >= 1 and max_new_tokens >= 1
+        req = Request(list(prompt), max_new_tokens, rid=self._next_id)
+        self._next_id += 1
+        self.waiting.append(req)
+        return req
+
+    def _reset_slot(self, slot):
+        st = self.state
+        st.wkv[:, slot].zero_()
+        st.att_shift[:, slot].zero_()
+        st.ffn_shift[:, slot].zero_()
+
+    def _i32(self, values):
+        return torch.tensor(values, dtype=torch.int32).to(self.device, non_blocking=True)
+
+    def step(self):
+        """Runs one forward step; returns the requests that finished in it."""
+        while self.waiting and self.slots.available:
+            req = self.waiting.popleft()
+            req.slot = self.slots.alloc()
+            self._reset_slot(req.slot)
+            self.running.append(req)
+        dec = [r for r in self.running if not r.prefilling][: self.max_decode]
+        rows = len(dec)
+        groups = {}  # chunk length -> requests
+        n_chunks = 0
+        for r in self.running:
+            if not r.prefilling or n_chunks == self.max_prefill_chunks:
+                continue
+            t = min(self.chunk, len(r.prompt) - r.pos, self.max_rows - rows)
+            if t <= 0:
+                break
+            groups.setdefault(t, []).append(r)
+            rows += t
+            n_chunks += 1
+        if rows == 0:
+            return []
+        decode = None
+        if dec:
+            decode = (self._i32([r.output[-1] for r in dec]), self._i32([r.slot for r in dec]))
+        prefill, order = [], []
+        for t, reqs in groups.items():
+            toks = self._i32([r.prompt[r.pos:r.pos + t] for r in reqs])
+            prefill.append((toks, self._i32([r.slot for r in reqs])))
+            order.append((t, reqs))
+        logits = self.engine.step(self.state, decode=decode, prefill=prefill)
+        nxt = self.sample(logits).tolist()
+        for i, r in enumerate(dec):
+            r.output.append(nxt[i])
+        j = len(dec)
+        for t, reqs in order:
+            for r in reqs:
+                r.pos += t
+                if not r.prefilling:
+                    r.output.append(nxt[j])
+                j += 1
+        self.steps += 1
+        self.tokens_processed += rows
+        finished = [r for r in self.running if r.done]
+        for r in finished:
+            self.slots.free(r.slot)
+        self.running = [r for r in self.running if not r.done]
+        return finished
+
+    def run(self, max_steps=1 << 30):
+        """Steps until every submitted request finished; returns them in completion order."""
+        done = []
+        while (self.waiting or self.running) and self.steps < max_steps:
+            done += self.step()
+        return done
+
+
+__all__ = ["Request", "SlotAllocator", "ContinuousBatcher"]
