@@ -44,6 +44,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--model-steps", type=int, default=20,
                     help="timed decode steps of the 1.5B-shape model at bs=128 (0: skip)")
+    ap.add_argument("--prefill-calls", type=int, default=20,
+                    help="timed calls of the config-2 prefill (B=8, T=1024, H=32; 0: skip)")
     ap.add_argument("--serve-steps", type=int, default=3,
                     help="timed steps of the 7B mixed prefill+decode step (BASELINE config 4; 0: skip)")
     ap.add_argument("--rowmajor-gemm", action="store_true",
@@ -158,6 +160,55 @@ def model_decode(dev, steps, warmup=3, frag=True):
         "gemm_tflops": round(flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
         "gemm_path": "frag (vkwr_frag_gemm_f16, weights packed at load)" if frag else "row-major (vkwr_gemm_f16)",
         "timing": "one decode step captured as a HIP graph, replayed; HIP events on the replay stream",
+    }
+
+
+def prefill_c2(dev, steps, warmup=2):
+    """WKV-7 prefill, B=8 sequences x T=1024 tokens, H=32, fp32 state
+    gathered from / scattered back to random slots of the 512-slot pool in the same call
+    (vkwr_v1_wkv::wkv_forward_slots_fp32 -> the row-split prefill kernel).  Inputs drawn as
+    in config 0, resident in HBM; eager calls (each is hundreds of microseconds) bracketed
+    by HIP events on the current stream."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    Bp, Tp = 8, 1024
+    g = torch.Generator(device=dev).manual_seed(2)
+    shp = (Bp, Tp, C)
+    r, k, v = (torch.randn(shp, device=dev, generator=g).half() for _ in range(3))
+    w = torch.exp(-0.6065 * torch.sigmoid(torch.randn(shp, device=dev, generator=g))).half()
+    kk = torch.nn.functional.normalize(k.float().view(Bp, Tp, H, HEAD), dim=-1)
+    a_vec = torch.sigmoid(torch.randn(Bp, Tp, H, HEAD, device=dev, generator=g))
+    a = (-kk).reshape(shp).half()
+    b = (kk * a_vec).reshape(shp).half()
+    pool = (torch.randn(P_SLOTS, H, HEAD, HEAD, device=dev, generator=g) * 0.1)
+    slots = torch.randperm(P_SLOTS, device=dev, generator=g)[:Bp].to(torch.int32)
+    y = torch.empty(shp, dtype=torch.float16, device=dev)
+    call = lambda: torch.ops.vkwr_v1_wkv.wkv_forward_slots_fp32(Bp, Tp, C, H, pool, slots, r, w, k, v, a, b, y)
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        call()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    nbytes = 7 * Bp * Tp * C * 2 + 2 * Bp * H * HEAD * HEAD * 4 + Bp * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del r, w, k, v, a, b, pool, y
+    torch.cuda.empty_cache()
+    return {
+        "workload": "WKV-7 prefill (BASELINE config 2): B=8, T=1024, H=32, fp32 state in a 512-slot pool "
+                    "(gather + scatter in the call), fp16 inputs drawn as in config 0",
+        "ms_per_call": round(ms, 4),
+        "calls": steps,
+        "tokens_per_s": round(Bp * Tp / (ms * 1e-3), 1),
+        "ns_per_token_step": round(ms * 1e6 / Tp, 1),
+        "roofline": {"bound": "latency (sequential in T: 1024 dependent token steps per head)",
+                     "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes},
+        "kernel": "wkv7_fp32_rows_kernel (256 lanes per (sequence, head), row-split dot products)",
     }
 
 
@@ -367,6 +418,8 @@ def main():
         torch.cuda.empty_cache()
         result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm)
         torch.cuda.empty_cache()
+    if args.prefill_calls > 0 and not args.eager:
+        result["prefill_c2"] = prefill_c2(dev, args.prefill_calls)
     if args.serve_steps > 0 and not args.eager:
         result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
     if not args.no_cpu_baseline:

@@ -24,6 +24,7 @@ def lib():
         p = ctypes.c_void_p
         i = ctypes.c_int
         L.oracle_wkv_fp32.argtypes = [i, i, i, i, p, p, p, p, p, p, p, p]
+        L.oracle_wkv_fp32_rows.argtypes = [i, i, i, i, p, p, p, p, p, p, p, p]
         L.oracle_wkv_fp16.argtypes = [i, i, i, i, p, p, p, p, p, p, p, p, p, p, i]
         L.oracle_advance_i32.argtypes = [p, ctypes.c_int64, ctypes.c_int32]
         L.oracle_decay.argtypes = [ctypes.c_float]
@@ -65,13 +66,18 @@ def get_threads():
     return lib().oracle_get_threads()
 
 
-def wkv_fp32(B, T, C, H, state, r, w, k, v, a, b):
-    """fp32-state WKV-7 (wkv_fp32_v2.cu:59-125). state [B,H,64,64] f32 (in place)."""
+def wkv_fp32(B, T, C, H, state, r, w, k, v, a, b, order="seq"):
+    """fp32-state WKV-7 (wkv_fp32_v2.cu:59-125). state [B,H,64,64] f32 (in place).
+
+    order "seq": each dot product one FMA chain over j (the reference's row-per-thread
+    kernel); "rows": the row-split order of the prefill kernel (wkv_oracle.c row_dot)."""
     assert state.dtype == np.float32 and state.flags.c_contiguous
     assert state.shape == (B, H, 64, 64) and C == H * 64
+    assert order in ("seq", "rows"), order
     ins = [_c16(x).reshape(B, T, C) for x in (r, w, k, v, a, b)]
     y = np.empty((B, T, C), dtype=np.float16)
-    lib().oracle_wkv_fp32(B, T, C, H, _ptr(state), *[_ptr(x) for x in ins], _ptr(y))
+    fn = lib().oracle_wkv_fp32 if order == "seq" else lib().oracle_wkv_fp32_rows
+    fn(B, T, C, H, _ptr(state), *[_ptr(x) for x in ins], _ptr(y))
     return y
 
 
@@ -89,10 +95,10 @@ def wkv_fp16(B, T, C, H, state, r, w, k, v, a, b, elapsed_t, w0=None, legacy=Fal
     return y
 
 
-def wkv_fp32_slots(B, T, C, H, pool, slots, r, w, k, v, a, b):
+def wkv_fp32_slots(B, T, C, H, pool, slots, r, w, k, v, a, b, order="seq"):
     """Slot-indexed reference semantics: pool[slots] -> wkv_fp32 -> pool[slots] = result."""
     st = np.ascontiguousarray(pool[slots])
-    y = wkv_fp32(B, T, C, H, st, r, w, k, v, a, b)
+    y = wkv_fp32(B, T, C, H, st, r, w, k, v, a, b, order=order)
     pool[slots] = st
     return y
 

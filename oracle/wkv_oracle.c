@@ -29,7 +29,8 @@
  *     division; accuracy ~1e-7 relative, checked against float64 closed forms;
  *   - `s*w + sa*b + k*v` (wkv_fp32_v2.cu:114) is evaluated as
  *     fma(k, v, fma(sa, b, s*w)), and the sa/y dot products as sequential FMA
- *     chains over j = 0..63 (wkv_fp32_v2.cu:103-117);
+ *     chains over j = 0..63 (wkv_fp32_v2.cu:103-117); oracle_wkv_fp32_rows
+ *     evaluates them in the row-split order of row_dot below;
  *   - the legacy half2 operators (state_fwd_fp16.cu:69,79-80) are evaluated as
  *     separately rounded fp16 multiplies and adds, left to right.
  */
@@ -197,12 +198,41 @@ int oracle_get_threads(void) {
 
 /* ---------------------------------------------------------------- fp32 WKV */
 
-/* wkv_forward_fp32 family (all four dispatch modes compute this).
- * state [B,H,64,64] fp32 in place; r,w,k,v,a,b,y [B,T,C] fp16 bits. */
-void oracle_wkv_fp32(int B, int T, int C, int H, float* state,
-                     const uint16_t* r, const uint16_t* w, const uint16_t* k,
-                     const uint16_t* v, const uint16_t* a, const uint16_t* b,
-                     uint16_t* y) {
+/* Dot product of one state row with a token vector in one of two orders:
+ *   order 0: one FMA chain over j = 0..63 (the reference's row-per-thread
+ *            kernel, wkv_fp32_v2.cu:103-117);
+ *   order 1: eight FMA chains, chain g over the columns 4g..4g+3 then
+ *            32+4g..32+4g+3 in that order, combined by the pairwise tree
+ *            ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)).  This is the row-split
+ *            order of vkwr_amd's prefill kernel (eight lanes per state row).
+ *            The reference's own split-row kernels (wkv_fp32_v2.cu:127-166
+ *            warp-split, :169-218 block-split) likewise reduce partial sums
+ *            across lanes instead of one chain; the order here is this build's. */
+static float row_dot(const float* s, const float* x, int order) {
+  if (order == 0) {
+    float acc = 0.0f;
+    for (int j = 0; j < HS; ++j) acc = fmaf(s[j], x[j], acc);
+    return acc;
+  }
+  float p[8];
+  for (int g = 0; g < 8; ++g) {
+    float acc = 0.0f;
+    for (int e = 0; e < 8; ++e) {
+      const int j = (e < 4) ? 4 * g + e : 32 + 4 * g + (e - 4);
+      acc = fmaf(s[j], x[j], acc);
+    }
+    p[g] = acc;
+  }
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
+/* wkv_forward_fp32 family.  state [B,H,64,64] fp32 in place; r,w,k,v,a,b,y
+ * [B,T,C] fp16 bits.  `order` selects the dot-product order (row_dot); the
+ * per-element update fma(k, v, fma(sa, b, s*d)) is the same in both. */
+static void wkv_fp32_impl(int B, int T, int C, int H, float* state,
+                          const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                          const uint16_t* v, const uint16_t* a, const uint16_t* b,
+                          uint16_t* y, int order) {
 #pragma omp parallel for schedule(static)
   for (int bh = 0; bh < B * H; ++bh) {
     const int bi = bh / H, h = bh % H;
@@ -219,21 +249,36 @@ void oracle_wkv_fp32(int B, int T, int C, int H, float* state,
       }
       for (int i = 0; i < HS; ++i) {
         float* row = S + i * HS;
-        float sa = 0.0f;
-        for (int j = 0; j < HS; ++j) sa = fmaf(row[j], aa[j], sa);
+        const float sa = row_dot(row, aa, order);
         const float vi = oracle_f16_to_f32(v[base + i]);
-        float acc = 0.0f;
         for (int j = 0; j < HS; ++j) {
           float s = row[j] * dd[j];
           s = fmaf(sa, bb[j], s);
           s = fmaf(kk[j], vi, s);
           row[j] = s;
-          acc = fmaf(s, rr[j], acc);
         }
-        y[base + i] = oracle_f32_to_f16(acc);
+        y[base + i] = oracle_f32_to_f16(row_dot(row, rr, order));
       }
     }
   }
+}
+
+/* Row-per-thread order: the reference's wkv_fp32_v2_kernel (all four of this
+ * build's fp32 dispatch modes at T == 1, and modes 1-3 at T > 1). */
+void oracle_wkv_fp32(int B, int T, int C, int H, float* state,
+                     const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                     const uint16_t* v, const uint16_t* a, const uint16_t* b,
+                     uint16_t* y) {
+  wkv_fp32_impl(B, T, C, H, state, r, w, k, v, a, b, y, 0);
+}
+
+/* Row-split order (row_dot order 1): this build's prefill path (mode 0 and the
+ * slot-pool entry point at T > 1). */
+void oracle_wkv_fp32_rows(int B, int T, int C, int H, float* state,
+                          const uint16_t* r, const uint16_t* w, const uint16_t* k,
+                          const uint16_t* v, const uint16_t* a, const uint16_t* b,
+                          uint16_t* y) {
+  wkv_fp32_impl(B, T, C, H, state, r, w, k, v, a, b, y, 1);
 }
 
 /* ---------------------------------------------------------------- fp16 WKV */

@@ -143,7 +143,11 @@ def _zeros16(B, T, C):
     return np.zeros((B, T, C), dtype=np.float16)
 
 
-def test_fp32_case_decay_only():
+ORDERS = ["seq", "rows"]
+
+
+@pytest.mark.parametrize("order", ORDERS)
+def test_fp32_case_decay_only(order):
     """a=b=0, k=v=0: S' = S diag(d), y = S' r."""
     B, T, H = 1, 1, 2
     C = H * 64
@@ -151,7 +155,7 @@ def test_fp32_case_decay_only():
     S0 = make_state(B, H, seed=3, std=1.0)
     S = S0.copy()
     z = _zeros16(B, T, C)
-    y = orc.wkv_fp32(B, T, C, H, S, r, w, z, z, z, z)
+    y = orc.wkv_fp32(B, T, C, H, S, r, w, z, z, z, z, order=order)
     d = decay64(w.astype(np.float64)).reshape(B, H, 64)
     S64 = S0.astype(np.float64) * d[:, :, None, :]
     np.testing.assert_allclose(S, S64, rtol=3e-7, atol=0)
@@ -159,7 +163,8 @@ def test_fp32_case_decay_only():
     np.testing.assert_allclose(y.astype(np.float64), y64, rtol=1e-3, atol=1e-3)
 
 
-def test_fp32_case_rank1_update():
+@pytest.mark.parametrize("order", ORDERS)
+def test_fp32_case_rank1_update(order):
     """a=b=0: S' = S diag(d) + v k^T (outer product)."""
     B, T, H = 1, 1, 1
     C = 64
@@ -167,7 +172,7 @@ def test_fp32_case_rank1_update():
     S0 = make_state(B, H, seed=4, std=1.0)
     S = S0.copy()
     z = _zeros16(B, T, C)
-    orc.wkv_fp32(B, T, C, H, S, r, w, k, v, z, z)
+    orc.wkv_fp32(B, T, C, H, S, r, w, k, v, z, z, order=order)
     d = decay64(w.astype(np.float64))[0, 0]
     S64 = S0[0, 0].astype(np.float64) * d[None, :] + np.outer(v[0, 0].astype(np.float64), k[0, 0].astype(np.float64))
     np.testing.assert_allclose(S[0, 0], S64, rtol=1e-6, atol=1e-6)
@@ -191,11 +196,12 @@ def _delta_rule_expect(S0, kk16, k, v):
         v[0, 0].astype(np.float64), k[0, 0].astype(np.float64))
 
 
-def test_fp32_case_classic_delta_rule():
+@pytest.mark.parametrize("order", ORDERS)
+def test_fp32_case_classic_delta_rule(order):
     """d=1, a=-kk, b=kk (unit kk): S' = S (I - kk kk^T) + v k^T."""
     r, w, k, v, kk16, S0 = _delta_rule_case(5)
     S = S0.copy()
-    orc.wkv_fp32(1, 1, 64, 1, S, r, w, k, v, -kk16, kk16)
+    orc.wkv_fp32(1, 1, 64, 1, S, r, w, k, v, -kk16, kk16, order=order)
     np.testing.assert_allclose(S[0, 0], _delta_rule_expect(S0, kk16, k, v), rtol=1e-5, atol=2e-5)
 
 
@@ -208,13 +214,14 @@ def test_planted_mistake_is_caught_by_delta_rule_case():
     assert not np.allclose(wrong, _delta_rule_expect(S0, kk16, k, v), rtol=1e-5, atol=2e-5)
 
 
-def test_fp32_case_zero_state_single_token():
+@pytest.mark.parametrize("order", ORDERS)
+def test_fp32_case_zero_state_single_token(order):
     """S=0, T=1: y_i = v_i (k . r) per head."""
     B, T, H = 2, 1, 3
     C = H * 64
     r, w, k, v, a, b = make_wkv_inputs(B, T, H, seed=7)
     S = np.zeros((B, H, 64, 64), dtype=np.float32)
-    y = orc.wkv_fp32(B, T, C, H, S, r, w, k, v, a, b)
+    y = orc.wkv_fp32(B, T, C, H, S, r, w, k, v, a, b, order=order)
     kr = (k.astype(np.float64) * r.astype(np.float64)).reshape(B, H, 64).sum(-1)
     want = v.astype(np.float64).reshape(B, H, 64) * kr[:, :, None]
     np.testing.assert_allclose(y.astype(np.float64).reshape(B, H, 64), want, rtol=2e-3, atol=2e-3)
@@ -239,29 +246,99 @@ def _wkv_fp32_float64(S, r, w, k, v, a, b):
     return S, y
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("B,T,H,dist", [(1, 4, 1, "baseline"), (2, 3, 2, "realistic"), (1, 16, 1, "realistic")])
-def test_fp32_matches_float64_brute_force(B, T, H, dist):
+def test_fp32_matches_float64_brute_force(B, T, H, dist, order):
     C = H * 64
     ins = make_wkv_inputs(B, T, H, seed=11, dist=dist)
     S0 = make_state(B, H, seed=11)
     S = S0.copy()
-    y = orc.wkv_fp32(B, T, C, H, S, *ins)
+    y = orc.wkv_fp32(B, T, C, H, S, *ins, order=order)
     S64, y64 = _wkv_fp32_float64(S0, *ins)
     np.testing.assert_allclose(S, S64, rtol=1e-4, atol=1e-4)
     # y is rounded to fp16: allow one fp16 ulp plus fp32 drift
     np.testing.assert_allclose(y.astype(np.float64), y64, rtol=2e-3, atol=2e-3)
 
 
-def test_fp32_prefill_equals_repeated_decode():
+@pytest.mark.parametrize("order", ORDERS)
+def test_fp32_prefill_equals_repeated_decode(order):
     B, T, H = 2, 9, 2
     C = H * 64
     ins = make_wkv_inputs(B, T, H, seed=12)
     S_seq = make_state(B, H, seed=12)
     S_one = S_seq.copy()
-    y_seq = orc.wkv_fp32(B, T, C, H, S_seq, *ins)
-    ys = [orc.wkv_fp32(B, 1, C, H, S_one, *(x[:, t:t + 1] for x in ins)) for t in range(T)]
+    y_seq = orc.wkv_fp32(B, T, C, H, S_seq, *ins, order=order)
+    ys = [orc.wkv_fp32(B, 1, C, H, S_one, *(x[:, t:t + 1] for x in ins), order=order) for t in range(T)]
     assert np.array_equal(S_seq, S_one)
     assert np.array_equal(y_seq, np.concatenate(ys, axis=1))
+
+
+def _sa_probe(cols):
+    """One token with d = 1, k = v = r = 0, a = 1 on every column, b = e_63 and state row 0 =
+    2^24 at column cols[0], 1 at cols[1] and cols[2] (column 63 zero): the updated S[0, 63]
+    is exactly sa = the row's sum in the oracle's order."""
+    S = np.zeros((1, 1, 64, 64), dtype=np.float32)
+    S[0, 0, 0, cols[0]] = 2.0 ** 24
+    S[0, 0, 0, cols[1]] = 1.0
+    S[0, 0, 0, cols[2]] = 1.0
+    ones = np.ones((1, 1, 64), dtype=np.float16)
+    z = np.zeros((1, 1, 64), dtype=np.float16)
+    w = np.full((1, 1, 64), -np.inf, dtype=np.float16)  # decay exactly 1
+    b = z.copy()
+    b[0, 0, 63] = 1.0
+    return S, (z, w, z, z, ones, b)
+
+
+# 2^24 + 1 is a tie that rounds (to even) back to 2^24; 2^24 + 2 is exact.  So the sum is
+# 2^24 + 2 exactly when the two ones are added to each other before either meets 2^24.
+# Row-split order: group g = columns 4g..4g+3, 32+4g..32+4g+3; tree ((0,1),(2,3)),((4,5),(6,7)).
+DOT_PROBES = [
+    ((0, 4, 36), 2.0 ** 24 + 2),  # 4 and 36 are both group 1: its chain adds the ones first
+    ((0, 24, 28), 2.0 ** 24 + 2),  # groups 6 and 7 pair in the tree before the root
+    ((0, 12, 16), 2.0 ** 24),      # groups 3 and 4 meet only at the root, after group 0 absorbed one
+    ((0, 1, 33), 2.0 ** 24),       # all in group 0, 2^24 first in its chain
+    ((0, 8, 12), 2.0 ** 24 + 2),   # groups 2 and 3 pair before meeting groups 0-1
+]
+
+
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("cols,rows_sum", DOT_PROBES)
+def test_fp32_dot_order_known_answer(order, cols, rows_sum):
+    """One chain from column 0 loses both ones (2^24); the row-split order gives rows_sum."""
+    S, ins = _sa_probe(cols)
+    orc.wkv_fp32(1, 1, 64, 1, S, *ins, order=order)
+    want = 2.0 ** 24 if order == "seq" else rows_sum
+    assert S[0, 0, 0, 63] == np.float32(want), (order, cols, S[0, 0, 0, 63])
+
+
+def test_fp32_dot_order_planted_grouping_is_caught():
+    """Eight contiguous columns per group (a plausible mistake) fails the first probe: 4 joins
+    2^24's group, 36 sits in group 4, so both ones are absorbed."""
+    cols, rows_sum = DOT_PROBES[0]
+    row = np.zeros(64, dtype=np.float32)
+    row[cols[0]], row[cols[1]], row[cols[2]] = 2.0 ** 24, 1.0, 1.0
+    p = [np.float32(0)] * 8
+    for j in range(64):
+        p[j // 8] = np.float32(p[j // 8] + row[j])
+    wrong = np.float32(np.float32(np.float32(p[0] + p[1]) + np.float32(p[2] + p[3]))
+                       + np.float32(np.float32(p[4] + p[5]) + np.float32(p[6] + p[7])))
+    assert wrong != np.float32(rows_sum)
+
+
+def test_fp32_orders_agree_within_tolerance_and_differ_in_bits():
+    B, T, H = 2, 32, 2
+    C = H * 64
+    ins = make_wkv_inputs(B, T, H, seed=14, dist="baseline")
+    S1 = make_state(B, H, seed=14, std=0.1)
+    S2 = S1.copy()
+    y1 = orc.wkv_fp32(B, T, C, H, S1, *ins, order="seq")
+    y2 = orc.wkv_fp32(B, T, C, H, S2, *ins, order="rows")
+    assert np.abs(S1.astype(np.float64) - S2).max() <= 1e-5
+    # y is rounded to fp16 from fp32 sums that differ by rounding only: at most one fp16 ulp
+    y1d, y2d = y1.astype(np.float64), y2.astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(y1d), 2.0 ** -14))) - 10)
+    assert (np.abs(y1d - y2d) <= ulp).all()
+    assert not np.array_equal(S1, S2)
 
 
 def test_fp32_slots_leave_other_slots_untouched():

@@ -34,6 +34,8 @@
 namespace vk {
 namespace {
 
+typedef _Float16 hv8 __attribute__((ext_vector_type(8)));
+
 struct Fp32Args {
   int T, C, H, n_slots;
   float* state;
@@ -219,10 +221,266 @@ __global__ __launch_bounds__(64) void wkv7_fp32_seq_kernel(Fp32Args p) {
   store_state_fp32(S, st, s, lane);
 }
 
+// ---- row-split prefill (T > 1): one 256-lane workgroup per (sequence, head).
+//
+// The rows of the state are independent recurrences; only the two per-row dot
+// products couple a row's 64 columns.  So the head's 4096 state values are
+// spread over 256 lanes -- wave v owns rows 16v..16v+15, lane (g = lane & 7,
+// q = lane >> 3) owns rows 16v+2q and 16v+2q+1 at columns 4g..4g+3 and
+// 32+4g..32+4g+3 -- and each dot product is eight 8-term FMA chains (one per
+// lane) combined by a DPP butterfly over the eight lanes of the row:
+// ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)) in every lane (IEEE addition commutes,
+// so both lanes of each pair hold the same bits).  All four SIMDs of the CU
+// work on the head, and a lane issues 16 FMAs per dot product pair instead of 64.
+//
+// Per token t a lane updates its 16 state values with (decay_t, sa_t, b_t,
+// k_t, v_t), then forms y_t = S.r_t and sa_{t+1} = S.a_{t+1} together: both
+// read the same updated state, so the four FMA chains (2 rows x 2 vectors)
+// and the four butterflies interleave and the dependent latency of one hides
+// behind the others.  The arithmetic of every value is unchanged.
+//
+// Token vectors: the workgroup stages chunks of kRowsTC tokens' r, decay(w),
+// k, v, a, b (fp16 in HBM) as fp32 in LDS -- the decay is computed once per
+// (token, channel) here instead of once per row group.  Three buffers: chunk
+// c is read, chunk c+1 is ready (its first token's a is needed by chunk c's
+// last token), chunk c+2 is written at the end of chunk c from registers
+// loaded one chunk earlier.  Lanes read their columns as 16-byte LDS reads
+// (eight distinct addresses per instruction, 128 contiguous bytes: no bank
+// conflicts).  y goes through a per-wave LDS tile and leaves as 8-byte stores
+// once per chunk, after the prefetch has landed, so no wait for outstanding
+// loads covers freshly issued stores.
+constexpr int kRowsTC = 16;    // tokens per staged chunk
+constexpr int kRowsVecs = 6;   // r, decay, k, v, a, b
+constexpr int kRowsBufs = 3;
+
+// Sum over the 8 lanes 8m..8m+7 (see above); every lane gets the same value.
+__device__ __forceinline__ float sum8(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+  return x;
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations
+// and joins the workgroup, without the wait for outstanding global loads and
+// stores that __syncthreads' fence implies.  The memory clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+struct RowsArgs {
+  Fp32Args a;
+  int vec;  // 16-byte aligned r..b and 8-byte aligned y: vector loads/stores
+};
+
 template <bool kSlots>
-void launch_fp32(const Fp32Args& p, int B, hipStream_t stream) {
+__global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
+  const Fp32Args& p = ra.a;
+  __shared__ f4 vl[kRowsBufs * kRowsTC * kRowsVecs * 16];  // [buffer][token][vector][16 x f4]
+  __shared__ h2 ybuf[4][kRowsTC][8];                        // per wave: 16 tokens x 16 rows
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g = lane & 7, q = lane >> 3;
+  const int i0 = 16 * wv + 2 * q;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const int T = p.T;
+  const size_t tok0 = (size_t)bi * T * p.C + (size_t)h * kHead;
+  float* S = state_block<kSlots>(p, bi, h);
+  if (S == nullptr) {
+    for (int idx = tid; idx < T * kHead; idx += 256)
+      p.y[tok0 + (size_t)(idx >> 6) * p.C + (idx & 63)] = (_Float16)__builtin_nanf("");
+    return;
+  }
+
+  // staging: piece c = tid + 256 u (u = 0..2) is vector c >> 7, token (c >> 3) & 15,
+  // channels 8 (c & 7) .. + 7; tokens past T re-read token T - 1 (never used)
+  const _Float16* src[kRowsVecs] = {p.r, p.w, p.k, p.v, p.a, p.b};
+  hv8 stg[3];
+  auto stage_load = [&](int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int c = tid + 256 * u;
+      const int tt = (c >> 3) & 15, part = c & 7;
+      const int t = min(t0 + tt, T - 1);
+      const _Float16* x = (c & 128) ? src[2 * u + 1] : src[2 * u];
+      const _Float16* at = x + tok0 + (size_t)t * p.C + part * 8;
+      if (ra.vec) {
+        stg[u] = *reinterpret_cast<const hv8*>(at);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) stg[u][e] = at[e];
+      }
+    }
+  };
+  auto stage_store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int c = tid + 256 * u;
+      const int vec = c >> 7, tt = (c >> 3) & 15, part = c & 7;
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (u == 0 && vec == 1) ? decay((float)stg[u][e]) : (float)stg[u][e];
+      f4* d = &vl[((buf * kRowsTC + tt) * kRowsVecs + vec) * 16 + part * 2];
+      d[0] = f4{f[0], f[1], f[2], f[3]};
+      d[1] = f4{f[4], f[5], f[6], f[7]};
+    }
+  };
+
+  float s[2][8];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const float* row = S + (i0 + rr) * kHead;
+    const f4 lo = *reinterpret_cast<const f4*>(row + 4 * g);
+    const f4 hi = *reinterpret_cast<const f4*>(row + 32 + 4 * g);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s[rr][e] = lo[e];
+      s[rr][4 + e] = hi[e];
+    }
+  }
+
+  struct Tok {
+    f4 a[2], r[2], d[2], k[2], b[2];
+    float v0, v1;
+  };
+  // slot = buffer * kRowsTC + token; a is read first (it is needed first)
+  auto read_tok = [&](int slot) __attribute__((always_inline)) {
+    const f4* base = &vl[slot * kRowsVecs * 16];
+    Tok o;
+    o.a[0] = base[4 * 16 + g], o.a[1] = base[4 * 16 + 8 + g];
+    o.r[0] = base[0 * 16 + g], o.r[1] = base[0 * 16 + 8 + g];
+    o.d[0] = base[1 * 16 + g], o.d[1] = base[1 * 16 + 8 + g];
+    o.k[0] = base[2 * 16 + g], o.k[1] = base[2 * 16 + 8 + g];
+    o.b[0] = base[5 * 16 + g], o.b[1] = base[5 * 16 + 8 + g];
+    const float* vv = reinterpret_cast<const float*>(base + 3 * 16) + i0;
+    o.v0 = vv[0];
+    o.v1 = vv[1];
+    return o;
+  };
+
+  float sa[2];
+  // token `cur` (chunk token tt): state update, then y_t with cur.r and sa_{t+1} with nx.a
+  auto token = [&](const Tok& cur, const Tok& nx, int tt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const float vi = rr ? cur.v1 : cur.v0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = s[rr][e] * cur.d[e >> 2][e & 3];
+        x = __builtin_fmaf(sa[rr], cur.b[e >> 2][e & 3], x);
+        s[rr][e] = __builtin_fmaf(cur.k[e >> 2][e & 3], vi, x);
+      }
+    }
+    float py[2] = {0.0f, 0.0f}, pa[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        py[rr] = __builtin_fmaf(s[rr][e], cur.r[e >> 2][e & 3], py[rr]);
+        pa[rr] = __builtin_fmaf(s[rr][e], nx.a[e >> 2][e & 3], pa[rr]);
+      }
+    }
+    float y[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      y[rr] = sum8(py[rr]);
+      sa[rr] = sum8(pa[rr]);
+      // keep the sum an fp32 value before the fp16 conversion (no fused mixed-precision op)
+      asm volatile("" : "+v"(y[rr]));
+    }
+    // the eight lanes of a row group hold the same bits: all write the same word
+    ybuf[wv][tt][q] = h2{(_Float16)y[0], (_Float16)y[1]};
+  };
+
+  const int nchunk = (T + kRowsTC - 1) / kRowsTC;
+  stage_load(0);
+  stage_store(0);
+  if (nchunk > 1) {
+    stage_load(kRowsTC);
+    stage_store(1);
+    if (nchunk > 2) stage_load(2 * kRowsTC);
+  }
+  lds_barrier();
+  {
+    const Tok t0v = read_tok(0);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(s[rr][e], t0v.a[e >> 2][e & 3], acc);
+      sa[rr] = sum8(acc);
+    }
+  }
+  int buf = 0;
+  for (int c = 0; c < nchunk; ++c) {
+    const int nbuf = buf == kRowsBufs - 1 ? 0 : buf + 1;
+    const int t0 = c * kRowsTC;
+    const int nt = min(kRowsTC, T - t0);
+    // LDS slot of chunk token j, j <= kRowsTC + 2: past the chunk, the next buffer's
+    // first tokens (past T they hold stale values that are never used)
+    auto slot = [&](int j) { return j < kRowsTC ? buf * kRowsTC + j : nbuf * kRowsTC + (j - kRowsTC); };
+    // three token register sets: token j's vectors are read while token j - 2 computes,
+    // so the read has a whole token step to land before token j - 1 needs j's a
+    Tok ta = read_tok(slot(0)), tb = read_tok(slot(1));
+    for (int tt = 0; tt < nt; tt += 3) {
+      Tok tc = read_tok(slot(tt + 2));
+      token(ta, tb, tt);
+      if (tt + 1 >= nt) break;
+      ta = read_tok(slot(tt + 3));
+      token(tb, tc, tt + 1);
+      if (tt + 2 >= nt) break;
+      tb = read_tok(slot(tt + 4));
+      token(tc, ta, tt + 2);
+    }
+    // chunk c + 2 -> the buffer chunk c - 1 used (its readers passed the last barrier)
+    if (c + 2 < nchunk) {
+      stage_store(nbuf == kRowsBufs - 1 ? 0 : nbuf + 1);
+      if (c + 3 < nchunk) stage_load((c + 3) * kRowsTC);
+    }
+    // this wave's y tile -> HBM: lane -> token lane >> 2, rows 16 wv + 4 (lane & 3) .. + 3
+    {
+      const int tt = lane >> 2, r4 = lane & 3;
+      if (tt < nt) {
+        const h2 lo = ybuf[wv][tt][2 * r4], hi = ybuf[wv][tt][2 * r4 + 1];
+        _Float16* yd = p.y + tok0 + (size_t)(t0 + tt) * p.C + 16 * wv + 4 * r4;
+        if (ra.vec) {
+          typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<hv4*>(yd) = hv4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          yd[0] = lo[0];
+          yd[1] = lo[1];
+          yd[2] = hi[0];
+          yd[3] = hi[1];
+        }
+      }
+    }
+    lds_barrier();
+    buf = nbuf;
+  }
+
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    float* row = S + (i0 + rr) * kHead;
+    *reinterpret_cast<f4*>(row + 4 * g) = f4{s[rr][0], s[rr][1], s[rr][2], s[rr][3]};
+    *reinterpret_cast<f4*>(row + 32 + 4 * g) = f4{s[rr][4], s[rr][5], s[rr][6], s[rr][7]};
+  }
+}
+
+bool rows_vec_ok(const Fp32Args& p) {
+  auto al = [](const void* x, uintptr_t m) { return ((uintptr_t)x & (m - 1)) == 0; };
+  return al(p.r, 16) && al(p.w, 16) && al(p.k, 16) && al(p.v, 16) && al(p.a, 16) && al(p.b, 16) &&
+         al(p.y, 8);
+}
+
+// rows: T > 1 uses the row-split kernel (dot products in its order); otherwise
+// the row-per-lane kernels (one FMA chain per dot product).
+template <bool kSlots>
+void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
   if (p.T == 1) {
     hipLaunchKernelGGL(wkv7_fp32_step_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
+  } else if (rows) {
+    RowsArgs ra{p, rows_vec_ok(p) ? 1 : 0};
+    hipLaunchKernelGGL(wkv7_fp32_rows_kernel<kSlots>, dim3(B * p.H), dim3(256), 0, stream, ra);
   } else {
     hipLaunchKernelGGL(wkv7_fp32_seq_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   }
@@ -513,7 +771,7 @@ extern "C" int vkwr_wkv7_fp32_forward(int B, int T, int C, int H, int mode, floa
              reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
              reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
              reinterpret_cast<_Float16*>(y)};
-  launch_fp32<false>(p, B, (hipStream_t)stream);
+  launch_fp32<false>(p, B, (hipStream_t)stream, mode == 0);
   return check_launch("vkwr_wkv7_fp32_forward");
 }
 
@@ -533,7 +791,7 @@ extern "C" int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* p
              reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
              reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
              reinterpret_cast<_Float16*>(y)};
-  launch_fp32<true>(p, B, (hipStream_t)stream);
+  launch_fp32<true>(p, B, (hipStream_t)stream, true);
   return check_launch("vkwr_wkv7_fp32_forward_slots");
 }
 
