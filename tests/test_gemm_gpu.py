@@ -250,3 +250,65 @@ def test_cmix_down_ops(gpu):
         x100 = dev(h(1, 1, 100), gpu)
         M.cmix_sparse_one(100, 128, x100, dev(h(1, 100), gpu), dev(h(100), gpu), dev(h(128, 100), gpu),
                           dev(h(128, 100), gpu))
+
+
+# ---------------------------------------------------------------- large-M path
+
+def _big_vs_rowmajor(gpu, shapes, epis, seed):
+    """One launch over `shapes` ([N,K] weights: the 256x256 large-M kernel when eligible) and
+    the same launch over the transposed [K,N] copies (never eligible: the row-major kernel,
+    unsplit for M > 256).  Both feed the same MFMA operands in the same k order from zero
+    and apply the same epilogue arithmetic, so the results are the same bits."""
+    from vkwr_amd import capi
+    outs = []
+    for layout in (capi.GEMM_B_NK, capi.GEMM_B_KN):
+        probs, keep = [], []
+        for i, ((M, K, N), epi) in enumerate(zip(shapes, epis)):
+            g = torch.Generator(device=gpu).manual_seed(seed + 1000 * i)  # same tensors for both layouts
+            a = torch.randn(M, K, device=gpu, generator=g).half()
+            w = (torch.randn(N, K, device=gpu, generator=g) * 0.05).half()
+            c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+            v = torch.randn(M, N, device=gpu, generator=g).half()
+            vf = torch.randn(M, N, device=gpu, generator=g).half()
+            v0 = torch.randn(N, device=gpu, generator=g).half()
+            b = w if layout == capi.GEMM_B_NK else w.t().contiguous()
+            probs.append(capi.gemm_problem(a, b, c, b_layout=layout, epilogue=epi, v=v, v_first=vf, v0=v0))
+            keep += [a, b, c, v, vf, v0]
+        ws = torch.empty(max(capi.gemm_workspace_bytes(probs), 0), dtype=torch.uint8, device=gpu)
+        capi.gemm(probs, ws)
+        torch.cuda.synchronize()
+        outs.append([keep[i * 6 + 2].clone() for i in range(len(shapes))])
+    return outs
+
+
+@pytest.mark.parametrize("shapes,epis", [
+    ([(300, 1024, 768)], [0]),
+    ([(257, 64, 1000)], [1]),                        # one row past a tile, K of one stage, relu^2
+    ([(768, 448, 1280)], [3]),                       # 15 tiles (not a multiple of the 8 XCDs), bias
+    ([(600, 512, 700), (600, 512, 96), (600, 512, 256), (600, 512, 512)], [1, 0, 3, 2]),  # mixed epilogues
+    ([(2304, 4096, 4096)], [0]),                     # the 7B o-projection shape of a mixed step
+])
+def test_big_gemm_bitwise_equals_rowmajor_kernel(gpu, shapes, epis):
+    big, ref = _big_vs_rowmajor(gpu, shapes, epis, seed=11)
+    for i, (x, y) in enumerate(zip(big, ref)):
+        assert torch.equal(x, y), (shapes[i], epis[i], float((x.float() - y.float()).abs().max()))
+
+
+def test_big_gemm_batch_with_empty_problem_and_oracle(gpu):
+    """A launch whose batch holds an empty problem between eligible ones; every output against
+    the float64 oracle."""
+    from vkwr_amd import capi
+    shapes = [(384, 256, 520), (0, 256, 64), (384, 256, 200)]
+    a = [h(M, K) for M, K, N in shapes]
+    w = [h(N, K, scale=0.05) for M, K, N in shapes]
+    da = [dev(x, gpu) for x in a]
+    dw = [dev(x, gpu) for x in w]
+    c = [torch.full((M, N), float("nan"), dtype=torch.float16, device=gpu) for M, K, N in shapes]
+    probs = [capi.gemm_problem(x, y, z) for x, y, z in zip(da, dw, c)]
+    capi.gemm(probs, torch.empty(0, dtype=torch.uint8, device=gpu))
+    torch.cuda.synchronize()
+    for i, (M, K, N) in enumerate(shapes):
+        if M == 0:
+            continue
+        ref, abs_sum = R.gemm(a[i], w[i], "nk")
+        check(c[i], ref, ACC * abs_sum, f"batch problem {i}")

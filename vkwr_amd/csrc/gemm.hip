@@ -248,7 +248,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(Batch bt) {
         if (P.splits > 1) {
           P.ws[((int64_t)split * P.m + row) * P.n + col] = acc[i][j][r];
         } else {
-          P.c[(int64_t)row * P.n + col] = (_Float16)epilogue(P, acc[i][j][r], row, col);
+          float y = epilogue(P, acc[i][j][r], row, col);
+          asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+          P.c[(int64_t)row * P.n + col] = (_Float16)y;
         }
       }
     }
@@ -266,7 +268,170 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(Batch bt) {
     float s = P.ws[i];
     for (int z = 1; z < P.splits; ++z) s += P.ws[z * mn + i];
     const int row = (int)(i / P.n), col = (int)(i % P.n);
-    P.c[i] = (_Float16)epilogue(P, s, row, col);
+    float y = epilogue(P, s, row, col);
+    asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+    P.c[i] = (_Float16)y;
+  }
+}
+
+// ---- large-M path (prefill / mixed batches): 256x256 output tiles, matrix-core bound.
+//
+// Eligible batches: A without activation, B as [N,K], K a multiple of 64, 16-byte aligned
+// operands, M >= 256 somewhere in the batch.  256 lanes = 4 waves in a 2x2 grid, each wave
+// a 128x128 sub-tile of 4x4 v_mfma_f32_32x32x16_f16 blocks (256 fp32 accumulators).  K
+// advances 64 per stage through two 64 KiB LDS buffers (A and B tiles of 256 rows x 64):
+//   * the next stage's tiles are copied global -> LDS by the DMA form of the vector load
+//     (global_load_lds_dwordx4: 16 bytes per lane straight into LDS, no VGPR staging),
+//     issued at the start of the current stage; the lanes of one load instruction cover
+//     8 whole 128-byte rows, and row r's 16-byte chunk c lands at LDS slot
+//     r*8 + (c ^ ((r >> 1) & 7)), so that the fragment reads below touch 16 distinct
+//     16-byte bank groups per 16 lanes (conflict-free);
+//   * fragments for the next k16 group are read (ds_read_b128) while the current group's
+//     16 MFMAs run;
+//   * one barrier per stage, after the third group: this wave's DMA has landed
+//     (vmcnt(0)) and its reads of the current buffer are done (lgkmcnt(0)); after the
+//     barrier both hold for every wave, so the next stage's buffer may be read and the
+//     current one reloaded.
+// The DMA is written as inline assembly: the compiler would otherwise make every LDS read
+// wait for all outstanding DMA (it cannot tell the two buffers apart); the waits are placed
+// here instead, as described.  Accumulation runs over k16 chunks in increasing order from
+// zero, as in gemm_kernel without K splits, so both give the same bits.
+//
+// Workgroup b runs on XCD b % 8; logical tiles are handed out so that each XCD holds a
+// contiguous range, walked in groups of 4 tile rows, which keeps the A row blocks and B
+// column blocks an XCD needs at once few (its own L2).
+constexpr int kBigBM = 256, kBigBK = 64, kBigTile = 256 * kBigBK;  // halves per operand tile
+
+__device__ __forceinline__ int big_slot(int row, int c) { return row * 8 + (c ^ ((row >> 1) & 7)); }
+
+// 16 bytes per lane: global (base + voff) -> LDS (lds + 16 * lane); base and lds wave-uniform
+__device__ __forceinline__ void dma16_m0(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
+// kEpi >= 0: every problem of the batch has that epilogue; -1: each its own
+template <int kEpi>
+__global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_tiles) {
+  __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];  // [buffer][A/B]: 128 KiB
+  // logical tile of this workgroup (XCD-contiguous), its problem and (tile row, tile col)
+  const int xb = blockIdx.x & 7, idx = blockIdx.x >> 3, q8 = total_tiles >> 3, r8 = total_tiles & 7;
+  const int L = (xb < r8 ? xb * (q8 + 1) : r8 * (q8 + 1) + (xb - r8) * q8) + idx;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProblems; ++i)
+    if (i < bt.n && L >= bt.p[i].tile_begin) pi = i;
+  const Prob& P = bt.p[pi];
+  const int lt = L - P.tile_begin;
+  constexpr int kGroup = 4;
+  const int per = kGroup * P.tiles_n, grp = lt / per, in = lt - grp * per;
+  const int g0 = grp * kGroup, gs = min(kGroup, P.tiles_m - g0);
+  const int m0 = (g0 + in % gs) * kBigBM, n0 = (in / gs) * kBigBM;
+  const int M = P.m, N = P.n, K = P.k;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  // DMA instruction j (0..7) of wave w fills slots j*256 + w*64 + lane of a tile
+  uint32_t ao[8], bo[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int sl = j * 256 + w * 64 + lane, row = sl >> 3, c = (sl & 7) ^ ((row >> 1) & 7);
+    ao[j] = (uint32_t)((min(m0 + row, M - 1) * (int64_t)K + c * 8) * 2);
+    bo[j] = (uint32_t)((min(n0 + row, N - 1) * (int64_t)K + c * 8) * 2);
+  }
+  const uint32_t wl = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sm[0][0][0] + w * 64 * 16);
+  const int lr = lane & 31, lh = lane >> 5;
+  int fra[4][4], frb[4][4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      fra[kk][rb] = big_slot(wm * 128 + 32 * rb + lr, 2 * kk + lh) * 8;
+      frb[kk][rb] = big_slot(wn * 128 + 32 * rb + lr, 2 * kk + lh) * 8;
+    }
+  fv16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nst = K / kBigBK;
+  auto dma = [&](int buf, int st) __attribute__((always_inline)) {
+    const int k0 = min(st, nst - 1) * kBigBK;  // the last stage re-loads itself: in bounds, unused
+    const _Float16* ab = P.a + k0;
+    const _Float16* bb = P.b + k0;
+    const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2), lb = la + kBigTile * 2;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dma16_m0(ab, ao[j], la + j * 256 * 16);
+      dma16_m0(bb, bo[j], lb + j * 256 * 16);
+    }
+  };
+  hv8 fa[2][4], fb[2][4];
+  auto fread = [&](int buf, int kk, int set) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[set][i] = *reinterpret_cast<const hv8*>(&sm[buf][0][fra[kk][i]]);
+      fb[set][i] = *reinterpret_cast<const hv8*>(&sm[buf][1][frb[kk][i]]);
+    }
+  };
+  auto mfma16 = [&](int set) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+  };
+  dma(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  fread(0, 0, 0);
+  int cb = 0;
+  for (int s = 0; s < nst; ++s) {
+    const int nb = cb ^ 1;
+    fread(cb, 1, 1);
+    dma(nb, s + 1);  // buffer nb was last read before the previous barrier
+    mfma16(0);
+    __builtin_amdgcn_sched_barrier(0);
+    fread(cb, 2, 0);
+    mfma16(1);
+    __builtin_amdgcn_sched_barrier(0);
+    fread(cb, 3, 1);
+    mfma16(0);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    fread(nb, 0, 0);
+    mfma16(1);
+    __builtin_amdgcn_sched_barrier(0);
+    cb = nb;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last stage's re-load lands before exit
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn * 128 + j * 32 + lr;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (row >= M) continue;
+        float y = acc[i][j][r];
+        if constexpr (kEpi == VKWR_GEMM_EPI_RELU_SQUARE) {
+          y = fmaxf(y, 0.0f);
+          y = y * y;
+        } else if constexpr (kEpi == VKWR_GEMM_EPI_BIAS) {
+          y += (float)P.v0[col];
+        } else if constexpr (kEpi != VKWR_GEMM_EPI_NONE) {
+          y = epilogue(P, y, row, col);
+        }
+        asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+        P.c[(int64_t)row * N + col] = (_Float16)y;
+      }
+    }
   }
 }
 
@@ -274,14 +439,29 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 struct Config {
   int bm, bn;
+  bool big;  // gemm_big_kernel (256x256 tiles, no K splits)
 };
 
 // Tile shape from the largest M of the batch (all problems of one launch share it).
 Config pick_config(int max_m, int min_n) {
-  if (max_m <= 32) return {32, 128};
-  if (max_m <= 64) return {64, 128};
-  if (min_n >= 128 && max_m > 256) return {128, 128};
-  return {128, 64};
+  if (max_m <= 32) return {32, 128, false};
+  if (max_m <= 64) return {64, 128, false};
+  if (min_n >= 128 && max_m > 256) return {128, 128, false};
+  return {128, 64, false};
+}
+
+// gemm_big_kernel takes the batch when every non-empty problem has an unactivated A, a
+// [N,K] B, K a multiple of 64, 16-byte aligned rows, 32-bit byte offsets into A and B,
+// and some problem has M >= 256.
+bool big_eligible(const Batch& bt, int max_m) {
+  if (max_m < kBigBM) return false;
+  for (int i = 0; i < bt.n; ++i) {
+    const Prob& P = bt.p[i];
+    if (P.m == 0 || P.n == 0) continue;
+    if (P.b_kn || P.a_act != VKWR_GEMM_ACT_NONE || !P.vec || P.k < kBigBK || P.k % kBigBK) return false;
+    if ((int64_t)std::max(P.m, P.n) * P.k * 2 > 0xFFFF0000LL) return false;
+  }
+  return true;
 }
 
 // Fills tiling fields and returns the workspace bytes the batch needs.
@@ -299,7 +479,7 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
     const int base = P.tiles_m * P.tiles_n;
     // Split K only when the whole batch leaves CUs idle; keep >= 8 stages per split.
     int s = 1;
-    if (tiles < target_wgs && P.m <= 256) {
+    if (!cfg.big && tiles < target_wgs && P.m <= 256) {
       s = (target_wgs + tiles - 1) / tiles;
       s = std::min(s, std::max(1, P.k / (8 * kBK)));
       s = std::min(s, 16);
@@ -367,6 +547,7 @@ int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, C
     }
   }
   cfg = pick_config(max_m, min_n);
+  if (big_eligible(bt, max_m)) cfg = Config{kBigBM, kBigBM, true};
   return VKWR_OK;
 }
 
@@ -418,6 +599,22 @@ extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, 
   const int wgs = total_wgs(bt);
   if (wgs == 0) return VKWR_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (cfg.big) {
+    int epi = -2;  // the batch's common epilogue, -1 if they differ
+    for (int i = 0; i < bt.n; ++i) {
+      if (bt.p[i].m == 0 || bt.p[i].n == 0) continue;
+      epi = epi == -2 ? bt.p[i].epi : (epi == bt.p[i].epi ? epi : -1);
+    }
+    if (epi == VKWR_GEMM_EPI_NONE)
+      hipLaunchKernelGGL(gemm_big_kernel<VKWR_GEMM_EPI_NONE>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+    else if (epi == VKWR_GEMM_EPI_RELU_SQUARE)
+      hipLaunchKernelGGL(gemm_big_kernel<VKWR_GEMM_EPI_RELU_SQUARE>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+    else if (epi == VKWR_GEMM_EPI_BIAS)
+      hipLaunchKernelGGL(gemm_big_kernel<VKWR_GEMM_EPI_BIAS>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+    else
+      hipLaunchKernelGGL(gemm_big_kernel<-1>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+    return check_launch(fn);
+  }
   if (cfg.bm == 32) hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 4>), dim3(wgs), dim3(256), 0, s, bt);
   else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2>), dim3(wgs), dim3(256), 0, s, bt);
   else if (cfg.bn == 128) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2>), dim3(wgs), dim3(256), 0, s, bt);
