@@ -312,3 +312,40 @@ def test_big_gemm_batch_with_empty_problem_and_oracle(gpu):
             continue
         ref, abs_sum = R.gemm(a[i], w[i], "nk")
         check(c[i], ref, ACC * abs_sum, f"batch problem {i}")
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (1024, 16384, 2048),   # 32 tiles, long K: every tile split into 8 k-parts
+    (2304, 16384, 4096),   # the 7B FFN value shape: 144 tiles split into 3 k-parts
+    (2304, 4096, 16384),   # the 7B FFN key shape: 2 whole rounds + a 64-tile tail split in 4
+])
+def test_big_gemm_split_tail(gpu, M, K, N):
+    """Tail tiles split into k-parts (fp32 partials, ordered fixup): against the row-major
+    kernel on the transposed weight within the fp32 re-association bound, and run-to-run
+    bitwise identical (also through the relu^2 epilogue)."""
+    from vkwr_amd import capi
+    g = torch.Generator(device=gpu).manual_seed(M + K + N)
+    a = torch.randn(M, K, device=gpu, generator=g).half()
+    w = (torch.randn(N, K, device=gpu, generator=g) * 0.02).half()
+    wt = w.t().contiguous()
+
+    def run(b, layout, epi=capi.EPI_NONE):
+        c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+        p = [capi.gemm_problem(a, b, c, b_layout=layout, epilogue=epi)]
+        ws = torch.empty(max(capi.gemm_workspace_bytes(p), 0), dtype=torch.uint8, device=gpu)
+        capi.gemm(p, ws)
+        return c
+
+    nk = run(w, capi.GEMM_B_NK)
+    kn = run(wt, capi.GEMM_B_KN)
+    abs_sum = (a.abs().float() @ w.abs().float().t())
+    torch.cuda.synchronize()
+    ref = kn.double()
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - 10)
+    bound = ulp + ACC * abs_sum.double()
+    err = (nk.double() - ref).abs()
+    assert bool((err <= bound).all()), (float(err.max()), int((err > bound).sum()))
+    r1 = run(w, capi.GEMM_B_NK, capi.EPI_RELU_SQUARE)
+    r2 = run(w, capi.GEMM_B_NK, capi.EPI_RELU_SQUARE)
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2)

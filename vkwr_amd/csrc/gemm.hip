@@ -295,14 +295,38 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(Batch bt) {
 // The DMA is written as inline assembly: the compiler would otherwise make every LDS read
 // wait for all outstanding DMA (it cannot tell the two buffers apart); the waits are placed
 // here instead, as described.  Accumulation runs over k16 chunks in increasing order from
-// zero, as in gemm_kernel without K splits, so both give the same bits.
+// zero, as in gemm_kernel without K splits, so an unsplit tile has the same bits in both.
+//
+// Work distribution: with G = #CUs, the first D = T - (T % G) of the T tiles run whole
+// (gemm_big_kernel, XCD-aware order).  When the remaining R tiles would leave CUs idle
+// and the split pays for its traffic, each of them is cut into S equal k-parts, one per
+// workgroup of gemm_big_sk_kernel, which store fp32 partial tiles; gemm_big_fixup_kernel
+// adds each tile's S partials in increasing k order (deterministic) and applies the
+// epilogue.  S is chosen by a time model (plan_big).
 //
 // Workgroup b runs on XCD b % 8; logical tiles are handed out so that each XCD holds a
 // contiguous range, walked in groups of 4 tile rows, which keeps the A row blocks and B
 // column blocks an XCD needs at once few (its own L2).
 constexpr int kBigBM = 256, kBigBK = 64, kBigTile = 256 * kBigBK;  // halves per operand tile
+constexpr int kBigTileElems = kBigBM * kBigBM;                       // floats per partial tile
+
+struct BigPlan {
+  int dp_tiles;  // D: tiles computed whole
+  int sk_tiles;  // R: tiles split into k-parts
+  int parts;     // S: k-parts per split tile
+  int nst;       // k-stages per tile (all problems, when sk_tiles > 0)
+  float* ws;     // one partial tile per part: [R][S]
+};
 
 __device__ __forceinline__ int big_slot(int row, int c) { return row * 8 + (c ^ ((row >> 1) & 7)); }
+
+// A wave-uniform pointer in scalar registers (the compiler cannot always prove uniformity).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 
 // 16 bytes per lane: global (base + voff) -> LDS (lds + 16 * lane); base and lds wave-uniform
 __device__ __forceinline__ void dma16_m0(const void* base, uint32_t voff, uint32_t lds) {
@@ -310,13 +334,9 @@ __device__ __forceinline__ void dma16_m0(const void* base, uint32_t voff, uint32
                : "memory", "m0");
 }
 
-// kEpi >= 0: every problem of the batch has that epilogue; -1: each its own
-template <int kEpi>
-__global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_tiles) {
-  __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];  // [buffer][A/B]: 128 KiB
-  // logical tile of this workgroup (XCD-contiguous), its problem and (tile row, tile col)
-  const int xb = blockIdx.x & 7, idx = blockIdx.x >> 3, q8 = total_tiles >> 3, r8 = total_tiles & 7;
-  const int L = (xb < r8 ? xb * (q8 + 1) : r8 * (q8 + 1) + (xb - r8) * q8) + idx;
+// Logical tile L of the batch -> its problem index and tile origin (groups of 4 tile rows,
+// column-major inside a group).
+__device__ __forceinline__ int big_tile(const Batch& bt, int L, int& m0, int& n0) {
   int pi = 0;
 #pragma unroll
   for (int i = 1; i < kMaxProblems; ++i)
@@ -326,11 +346,36 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_ti
   constexpr int kGroup = 4;
   const int per = kGroup * P.tiles_n, grp = lt / per, in = lt - grp * per;
   const int g0 = grp * kGroup, gs = min(kGroup, P.tiles_m - g0);
-  const int m0 = (g0 + in % gs) * kBigBM, n0 = (in / gs) * kBigBM;
-  const int M = P.m, N = P.n, K = P.k;
+  m0 = (g0 + in % gs) * kBigBM;
+  n0 = (in / gs) * kBigBM;
+  return pi;
+}
 
+template <int kEpi>
+__device__ __forceinline__ float big_epilogue(const Prob& P, float y, int row, int col) {
+  if constexpr (kEpi == VKWR_GEMM_EPI_RELU_SQUARE) {
+    y = fmaxf(y, 0.0f);
+    return y * y;
+  } else if constexpr (kEpi == VKWR_GEMM_EPI_BIAS) {
+    return y + (float)P.v0[col];
+  } else if constexpr (kEpi == VKWR_GEMM_EPI_NONE) {
+    return y;
+  } else {
+    return epilogue(P, y, row, col);
+  }
+}
+
+// One 256x256 tile over k-stages [ks, ke): kPartial stores the fp32 sums to part in
+// register order -- element ((4 i + j) * 16 + r) * 256 + thread is accumulator r of block
+// (i, j) of that thread, so each store is one coalesced kilobyte -- otherwise the
+// epilogue's fp16 values (clipped to M x N) to P.c.
+template <bool kPartial, int kEpi>
+__device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], const Prob& P, int m0, int n0,
+                                             int ks, int ke, float* part) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int M = P.m, N = P.n, K = P.k;
   // DMA instruction j (0..7) of wave w fills slots j*256 + w*64 + lane of a tile
   uint32_t ao[8], bo[8];
 #pragma unroll
@@ -341,7 +386,6 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_ti
   }
   const uint32_t wl = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sm[0][0][0] + w * 64 * 16);
-  const int lr = lane & 31, lh = lane >> 5;
   int fra[4][4], frb[4][4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk)
@@ -358,11 +402,10 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_ti
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int nst = K / kBigBK;
   auto dma = [&](int buf, int st) __attribute__((always_inline)) {
-    const int k0 = min(st, nst - 1) * kBigBK;  // the last stage re-loads itself: in bounds, unused
-    const _Float16* ab = P.a + k0;
-    const _Float16* bb = P.b + k0;
+    const int k0 = min(st, ke - 1) * kBigBK;  // past the range: re-load its last stage (unused)
+    const void* ab = uniform_ptr(P.a + k0);
+    const void* bb = uniform_ptr(P.b + k0);
     const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2), lb = la + kBigTile * 2;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -385,11 +428,11 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_ti
       for (int j = 0; j < 4; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
   };
-  dma(0, 0);
+  dma(0, ks);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   fread(0, 0, 0);
   int cb = 0;
-  for (int s = 0; s < nst; ++s) {
+  for (int s = ks; s < ke; ++s) {
     const int nb = cb ^ 1;
     fread(cb, 1, 1);
     dma(nb, s + 1);  // buffer nb was last read before the previous barrier
@@ -407,31 +450,79 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int total_ti
     __builtin_amdgcn_sched_barrier(0);
     cb = nb;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last stage's re-load lands before exit
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last stage's re-load has landed
 
+  if constexpr (kPartial) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = n0 + wn * 128 + j * 32 + lr;
-      if (col >= N) continue;
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (row >= M) continue;
-        float y = acc[i][j][r];
-        if constexpr (kEpi == VKWR_GEMM_EPI_RELU_SQUARE) {
-          y = fmaxf(y, 0.0f);
-          y = y * y;
-        } else if constexpr (kEpi == VKWR_GEMM_EPI_BIAS) {
-          y += (float)P.v0[col];
-        } else if constexpr (kEpi != VKWR_GEMM_EPI_NONE) {
-          y = epilogue(P, y, row, col);
+        for (int r = 0; r < 16; ++r) part[((4 * i + j) * 16 + r) * 256 + tid] = acc[i][j][r];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = n0 + wn * 128 + j * 32 + lr;
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (row >= M) continue;
+          float y = big_epilogue<kEpi>(P, acc[i][j][r], row, col);
+          asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+          P.c[(int64_t)row * N + col] = (_Float16)y;
         }
-        asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
-        P.c[(int64_t)row * N + col] = (_Float16)y;
       }
     }
+  }
+}
+
+// Whole tiles: workgroup b takes logical tile (XCD-contiguous order) of the first `tiles`.
+// kEpi >= 0: every problem of the batch has that epilogue; -1: each its own.
+template <int kEpi>
+__global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int tiles) {
+  __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];  // [buffer][A/B]: 128 KiB
+  const int xb = blockIdx.x & 7, idx = blockIdx.x >> 3, q8 = tiles >> 3, r8 = tiles & 7;
+  const int L = (xb < r8 ? xb * (q8 + 1) : r8 * (q8 + 1) + (xb - r8) * q8) + idx;
+  int m0, n0;
+  const Prob& P = bt.p[big_tile(bt, L, m0, n0)];
+  big_tile_run<false, kEpi>(sm, P, m0, n0, 0, P.k / kBigBK, nullptr);
+}
+
+// Split tiles: workgroup b computes part b % S (k-stages [p nst / S, (p+1) nst / S)) of
+// split tile D + b / S into partial slot b.
+__global__ __launch_bounds__(256, 1) void gemm_big_sk_kernel(Batch bt, BigPlan pl) {
+  __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];
+  const int t = blockIdx.x / pl.parts, p = blockIdx.x - t * pl.parts;
+  int m0, n0;
+  const Prob& P = bt.p[big_tile(bt, pl.dp_tiles + t, m0, n0)];
+  big_tile_run<true, -1>(sm, P, m0, n0, p * pl.nst / pl.parts, (p + 1) * pl.nst / pl.parts,
+                         pl.ws + (size_t)blockIdx.x * kBigTileElems);
+}
+
+// Fixup: blockIdx.y = split tile t, blockIdx.x = accumulator block (i, j) of the partial
+// layout; adds the tile's S partials in increasing k order, applies the epilogue, stores.
+template <int kEpi>
+__global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan pl) {
+  const int t = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  int m0, n0;
+  const Prob& P = bt.p[big_tile(bt, pl.dp_tiles + t, m0, n0)];
+  const int lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lh = lane >> 5;
+  const int i = blk >> 2, j = blk & 3;
+  const int col = n0 + wn * 128 + j * 32 + lr;
+  if (col >= P.n) return;
+  const float* base = pl.ws + (size_t)t * pl.parts * kBigTileElems;
+  for (int r = 0; r < 16; ++r) {
+    const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+    if (row >= P.m) continue;
+    const size_t e = (size_t)(blk * 16 + r) * 256 + tid;
+    float acc = base[e];
+    for (int q = 1; q < pl.parts; ++q) acc += base[(size_t)q * kBigTileElems + e];
+    float y = big_epilogue<kEpi>(P, acc, row, col);
+    asm volatile("" : "+v"(y));
+    P.c[(int64_t)row * P.n + col] = (_Float16)y;
   }
 }
 
@@ -464,8 +555,14 @@ bool big_eligible(const Batch& bt, int max_m) {
   return true;
 }
 
+int64_t plan_big(Batch& bt, BigPlan& pl);
+
 // Fills tiling fields and returns the workspace bytes the batch needs.
 int64_t plan(Batch& bt, Config cfg, int target_wgs) {
+  if (cfg.big) {
+    BigPlan pl;
+    return plan_big(bt, pl);
+  }
   int tiles = 0;
   for (int i = 0; i < bt.n; ++i) {
     Prob& P = bt.p[i];
@@ -498,6 +595,62 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
     begin += bt.p[i].tiles_m * bt.p[i].tiles_n * bt.p[i].splits;
   }
   return ws;
+}
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Tiles (256x256) of a large-M batch and its stream-K split; returns the workspace bytes.
+int64_t plan_big(Batch& bt, BigPlan& pl) {
+  int T = 0, k_all = -1;
+  bool uniform_k = true;
+  for (int i = 0; i < bt.n; ++i) {
+    Prob& P = bt.p[i];
+    P.splits = 1;
+    P.k_per_split = P.k;
+    if (P.m == 0 || P.n == 0) {
+      P.tiles_m = P.tiles_n = 0;
+    } else {
+      P.tiles_m = (P.m + kBigBM - 1) / kBigBM;
+      P.tiles_n = (P.n + kBigBM - 1) / kBigBM;
+      uniform_k = uniform_k && (k_all < 0 || k_all == P.k);
+      k_all = P.k;
+    }
+    P.tile_begin = T;
+    T += P.tiles_m * P.tiles_n;
+  }
+  pl = BigPlan{T, 0, 1, 0, nullptr};
+  const int G = device_cus();
+  if (T < 32 || !uniform_k || T % G == 0) return 0;
+  // Time model of the last round, in microseconds: a tile's k-stage ~1.7 us when every CU
+  // is busy; a split tile costs its S fp32 partials written and read back (2 x 256 KiB
+  // each) at ~5 TB/s.  Take the S (1..8, >= 8 stages per part) with the least time.
+  const int R = T % G, nst = k_all / kBigBK;
+  double best = (double)nst * 1.7;
+  int best_s = 1;
+  for (int S = 2; S <= 8 && nst / S >= 8; ++S) {
+    const double rounds = (double)((R * S + G - 1) / G);
+    const double t = rounds * nst * 1.7 / S + (double)R * S * 2 * kBigTileElems * 4 / 5e6;
+    if (t < best) {
+      best = t;
+      best_s = S;
+    }
+  }
+  if (best_s == 1) return 0;
+  pl.dp_tiles = T - R;
+  pl.sk_tiles = R;
+  pl.parts = best_s;
+  pl.nst = nst;
+  return (int64_t)R * best_s * kBigTileElems * 4;
 }
 
 int total_wgs(const Batch& bt) {
@@ -600,19 +753,29 @@ extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, 
   if (wgs == 0) return VKWR_OK;
   hipStream_t s = (hipStream_t)stream;
   if (cfg.big) {
+    BigPlan pl;
+    plan_big(bt, pl);  // same plan as above (need)
+    pl.ws = reinterpret_cast<float*>(workspace);
     int epi = -2;  // the batch's common epilogue, -1 if they differ
     for (int i = 0; i < bt.n; ++i) {
       if (bt.p[i].m == 0 || bt.p[i].n == 0) continue;
       epi = epi == -2 ? bt.p[i].epi : (epi == bt.p[i].epi ? epi : -1);
     }
+    auto go = [&](auto whole, auto fix) {
+      if (pl.dp_tiles > 0) hipLaunchKernelGGL(whole, dim3(pl.dp_tiles), dim3(256), 0, s, bt, pl.dp_tiles);
+      if (pl.sk_tiles > 0) {
+        hipLaunchKernelGGL(gemm_big_sk_kernel, dim3(pl.sk_tiles * pl.parts), dim3(256), 0, s, bt, pl);
+        hipLaunchKernelGGL(fix, dim3(16, pl.sk_tiles), dim3(256), 0, s, bt, pl);
+      }
+    };
     if (epi == VKWR_GEMM_EPI_NONE)
-      hipLaunchKernelGGL(gemm_big_kernel<VKWR_GEMM_EPI_NONE>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+      go(gemm_big_kernel<VKWR_GEMM_EPI_NONE>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_NONE>);
     else if (epi == VKWR_GEMM_EPI_RELU_SQUARE)
-      hipLaunchKernelGGL(gemm_big_kernel<VKWR_GEMM_EPI_RELU_SQUARE>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+      go(gemm_big_kernel<VKWR_GEMM_EPI_RELU_SQUARE>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_RELU_SQUARE>);
     else if (epi == VKWR_GEMM_EPI_BIAS)
-      hipLaunchKernelGGL(gemm_big_kernel<VKWR_GEMM_EPI_BIAS>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+      go(gemm_big_kernel<VKWR_GEMM_EPI_BIAS>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_BIAS>);
     else
-      hipLaunchKernelGGL(gemm_big_kernel<-1>, dim3(wgs), dim3(256), 0, s, bt, wgs);
+      go(gemm_big_kernel<-1>, gemm_big_fixup_kernel<-1>);
     return check_launch(fn);
   }
   if (cfg.bm == 32) hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 4>), dim3(wgs), dim3(256), 0, s, bt);
