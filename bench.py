@@ -256,7 +256,8 @@ def serve_mixed_7b(dev, steps, warmup=1):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4),
                      "flops_per_step": gemm_flops(cfg, rows, Bd + Bp)},
-        "gemm_path": "row-major vkwr_gemm_f16 (128x128 MFMA tiles)",
+        "gemm_path": "vkwr_gemm_f16 large-M path (256x256x64 MFMA tiles, LDS DMA, split last round); "
+                     "rank-out adapters on the 128x128 row-major kernel",
         "timing": "eager launches, HIP events around the timed steps",
     }
 

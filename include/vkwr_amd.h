@@ -317,8 +317,10 @@ typedef struct vkwr_gemm_problem {
   const uint16_t* v0;
 } vkwr_gemm_problem;
 
-/* Bytes of device workspace vkwr_gemm_f16 needs for this batch (fp32 K-split
- * partials; 0 when no problem is split), or -1 on invalid arguments. */
+/* Bytes of device workspace vkwr_gemm_f16 needs for this batch (fp32 partial
+ * sums: K splits of small-M problems, or the k-parts of a large-M batch's last
+ * round of 256x256 tiles; 0 when nothing is split), or -1 on invalid arguments.
+ * The plan depends on the current device's CU count: ask on that device. */
 VKWR_EXPORT int64_t vkwr_gemm_f16_workspace_bytes(int n_problems, const vkwr_gemm_problem* problems);
 
 /* Runs 1..8 independent GEMMs in one launch on the gfx950 matrix cores.
