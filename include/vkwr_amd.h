@@ -417,6 +417,56 @@ typedef struct vkwr_frag_gemm_problem {
 VKWR_EXPORT int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* problems,
                                    void* stream);
 
+/* ---- token sampling (reference csrc/sampling/, ops vkwr_sampling::*) ----
+ *
+ * Per batch row b, on the logits of its last token (logits [B,T,V] fp32, row
+ * b*T + T-1; V a multiple of 4, at most 1048576):
+ *   u_i = sf((sf(l_i) - pen_i) log2(e) / temperature), p = base-2 softmax of u,
+ *   tau = the largest p value v with #{p >= v} >= top_k or mass{p >= v} >= top_p,
+ *   kept_i = p_i (p_i > tau), p_i * comp (p_i == tau), 0 (p_i < tau), where comp
+ *   spends exactly the top_k / top_p budget left on the entries equal to tau,
+ *   out[b] = inverse CDF of kept (vocabulary order) at one Philox uniform in (0,1].
+ * sf() maps NaN to 0 and +-inf to +-FLT_MAX.  top_k <= 0 or > V means V;
+ * top_p outside [0,1] means 1; top_p == 0 means top_k = 1 (greedy up to ties).
+ * temperature must lie in [0.001, 1000].  Every reduction has a fixed order,
+ * so a call is run-to-run deterministic for a given state.
+ * The random stream is Philox4x32-10 (counter-based; one 128-bit block per
+ * draw) and is not the curand stream of the reference: draws agree in law,
+ * not value by value. */
+#define VKWR_SAMPLING_STATE_BYTES 32 /* per batch row: key[2], counter[4], 2 reserved words */
+
+/* states [B] (B * VKWR_SAMPLING_STATE_BYTES bytes, device): key = seed, counter =
+ * (0, 0, b, 0) -- row b draws from its own counter subsequence.
+ * Replaces setup_rand_impl / setup_rand_kernel (csrc/sampling/sampling.cu:123-132),
+ * op vkwr_sampling::setup_rand (csrc/sampling/torch_bindings.cpp:37-38). */
+VKWR_EXPORT int vkwr_sampling_setup_rand(int64_t seed, int B, void* states, void* stream);
+
+/* out [B] int32.  scratch: B*V floats of device memory, required only when
+ * V > 65536 (smaller vocabularies stay in registers), else may be NULL.
+ * Replaces sampling_temperature_topk_topp_impl and its two kernels
+ * (csrc/sampling/sampling.cu:438-646, 648-835, 842-915), op
+ * vkwr_sampling::temperature_topk_topp (torch_bindings.cpp:40-42). */
+VKWR_EXPORT int vkwr_sampling_temperature_topk_topp(int B, int T, int V, const float* logits, void* states,
+                                                    int32_t* out, float* scratch, double temperature,
+                                                    int top_k, double top_p, void* stream);
+
+/* As above with per-row penalties [B,V] fp32 subtracted from the logits, then
+ * updated in place after the draw:
+ *   pen_i <- pen_i * decay + (i == out[b] ? (pen_i == 0 ? presence : repetition) : 0)
+ * (fused multiply-add).  Replaces sampling_repetition_topk_topp_impl
+ * (csrc/sampling/sampling.cu:134-359, 361-436), op vkwr_sampling::repetition_topk_topp
+ * (torch_bindings.cpp:44-47). */
+VKWR_EXPORT int vkwr_sampling_repetition_topk_topp(int B, int T, int V, const float* logits, float* penalties,
+                                                   void* states, int32_t* out, float* scratch,
+                                                   double presence_penalty, double repetition_penalty,
+                                                   double penalty_decay, double temperature, int top_k,
+                                                   double top_p, void* stream);
+
+/* Host-side Philox4x32-10 block (the generator the sampling kernels run), for
+ * checking it against published known-answer vectors.  No counterpart in the
+ * reference (which calls curand). */
+VKWR_EXPORT void vkwr_sampling_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,8 @@
 """The drop-in surface: the extension modules register the reference's torch-op
 namespaces with byte-identical schemas (reference csrc/v1/wkv/torch_bindings.cpp:
 231-258, csrc/rwkv7/torch_bindings.cpp:36-50), the Python wrappers keep the
-reference's names and signatures (vkwr/_ops/v1/v1_wkv_ops.py, vkwr/_ops/rwkv7_ops.py),
+reference's names and signatures (vkwr/_ops/v1/v1_wkv_ops.py, vkwr/_ops/rwkv7_ops.py;
+the sampling wrappers, whose module the reference does not ship, keep the op names),
 and CPU tensors are refused by the dispatcher as in the reference (CUDA-only impls)."""
 import importlib
 import inspect
@@ -40,6 +41,13 @@ REF_SCHEMAS = {
         "forward_seq(int B, int T, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
         "forward_one(int B, int C, int H, Tensor(a!) state, Tensor r, Tensor w, Tensor k, Tensor v, Tensor a, Tensor b, Tensor(a!) y, Tensor(a!) elapsed_t) -> ()",
         "spmv_forward(int D, int C, Tensor vec, Tensor mat, Tensor(a!) out) -> ()",
+    ],
+    # csrc/sampling/torch_bindings.cpp:37-47
+    "vkwr_sampling": [
+        "setup_rand(int seed, int B) -> Tensor",
+        "temperature_topk_topp(Tensor logits, Tensor states, Scalar temperature, int top_k, Scalar top_p) -> Tensor",
+        "repetition_topk_topp(Tensor logits, Tensor penalties, Tensor states, Scalar presence_penalty, "
+        "Scalar repetition_penalty, Scalar penalty_decay, Scalar temperature, int top_k, Scalar top_p) -> Tensor",
     ],
 }
 
@@ -122,6 +130,20 @@ def test_cpu_tensors_rejected_by_dispatcher():
         torch.ops.vkwr_v1_wkv.wkv_forward_fp32(B, T, C, H, state, x, x, x, x, x, x, x.clone())
     with pytest.raises(NotImplementedError):
         torch.ops.vkwr_v1_wkv.advance_i32(torch.zeros(4, dtype=torch.int32), 1)
+    with pytest.raises(NotImplementedError):
+        torch.ops.vkwr_sampling.temperature_topk_topp(torch.zeros(1, 8), torch.zeros(32, dtype=torch.int8), 1.0, 0,
+                                                      1.0)
+
+
+def test_sampling_wrappers():
+    from vkwr_amd._ops import sampling_ops
+
+    assert sampling_ops.STATE_BYTES == 32
+    for name, params in {"setup_rand": "seed, B",
+                         "temperature_topk_topp": "logits, states, temperature, top_k, top_p",
+                         "repetition_topk_topp": "logits, penalties, states, presence_penalty, repetition_penalty, "
+                                                 "penalty_decay, temperature, top_k, top_p"}.items():
+        assert ", ".join(inspect.signature(getattr(sampling_ops, name)).parameters) == params
 
 
 def test_validate_slots_host_check():

@@ -85,6 +85,13 @@ WKV_STATE_STD, WKV_STATE_ILV = 0, 1
 _shift = _sig("vkwr_token_shift_mix_f16", [_i, _i, _i, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 _shift_slots = _sig("vkwr_token_shift_mix_slots_f16",
                     [_i, _i, _i, _p, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
+_d = ctypes.c_double
+_samp_setup = _sig("vkwr_sampling_setup_rand", [_i64, _i, _p, _p])
+_samp_temp = _sig("vkwr_sampling_temperature_topk_topp", [_i, _i, _i, _p, _p, _p, _p, _d, _i, _d, _p])
+_samp_rep = _sig("vkwr_sampling_repetition_topk_topp",
+                 [_i, _i, _i, _p, _p, _p, _p, _p, _d, _d, _d, _d, _i, _d, _p])
+SAMPLING_STATE_BYTES = 32
+SAMPLING_REGISTER_VOCAB = 65536  # larger vocabularies need a B*V fp32 scratch buffer
 
 
 def _check(st, what):
@@ -228,3 +235,26 @@ def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False, shift_slo
     else:
         _check(_shift_slots(B, T, C, _ptr(x), _ptr(shift_state), _ptr(shift_slots), len(mixes), mp, op,
                             1 if half_math else 0, _stream()), "vkwr_token_shift_mix_slots_f16")
+
+
+def sampling_setup_rand(seed, states):
+    """Initialises states (int8/uint8 tensor of B * SAMPLING_STATE_BYTES bytes) for B rows."""
+    B = states.numel() // SAMPLING_STATE_BYTES
+    _check(_samp_setup(seed, B, _ptr(states), _stream()), "vkwr_sampling_setup_rand")
+
+
+def sample(logits, states, out, temperature=1.0, top_k=-1, top_p=1.0, penalties=None, presence=0.0,
+           repetition=0.0, decay=1.0, scratch=None):
+    """One token per row of fp32 logits [B, V] (or [B, T, V]: last token) into out [B] int32;
+    with penalties [B, V] the repetition variant (penalties updated in place).  scratch
+    (B*V fp32) is needed only above SAMPLING_REGISTER_VOCAB."""
+    B, V = out.shape[0], logits.shape[-1]
+    T = logits.shape[1] if logits.dim() == 3 else 1
+    if penalties is None:
+        st = _samp_temp(B, T, V, _ptr(logits), _ptr(states), _ptr(out), _ptr(scratch), temperature, top_k, top_p,
+                        _stream())
+        _check(st, "vkwr_sampling_temperature_topk_topp")
+    else:
+        st = _samp_rep(B, T, V, _ptr(logits), _ptr(penalties), _ptr(states), _ptr(out), _ptr(scratch), presence,
+                       repetition, decay, temperature, top_k, top_p, _stream())
+        _check(st, "vkwr_sampling_repetition_topk_topp")
