@@ -15,11 +15,16 @@ relative to the reference root) one batch row at a time:
   compensation    sampling.cu:284-306: entries equal to tau keep the share of the
                   top_k / top_p budget left after the entries above tau
   draw            sampling.cu:307-343: a uniform in (0, 1] times the kept total,
-                  first entry whose running kept sum reaches it
+                  first entry whose running kept sum reaches it.  The reference
+                  visits the row in its own two-level order over its threads; the
+                  product visits it in lane order (``draw_order``), which this
+                  oracle follows.  The law of the draw is the same for any order.
   penalties       sampling.cu:345-358: pen <- fma(pen, decay, tok ? (pen == 0 ?
                   presence : repetition) : 0)
   parameters      sampling.cu:896-901: top_k <= 0 or > V -> V; top_p outside
-                  [0, 1] -> 1; top_p == 0 -> top_k = 1, top_p = 1
+                  [0, 1] -> 1; top_p == 0 -> top_k = 1, top_p = 1.  top_p = 1
+                  sets no mass limit (the reference's mass test can then only
+                  fire through float rounding of a sum that should stay below 1).
 
 The draw's uniform comes from Philox4x32-10 (Salmon et al., SC'11), the
 generator the product runs: key = seed (low word, high word), counter =
@@ -41,6 +46,7 @@ FLT_MAX = np.float32(np.finfo(np.float32).max)
 PHILOX_M = (0xD2511F53, 0xCD9E8D57)
 PHILOX_W = (0x9E3779B9, 0xBB67AE85)
 MASK32 = 0xFFFFFFFF
+THREADS = 1024  # lanes of the product's sampling workgroup
 
 
 def philox4x32_10(ctr, key):
@@ -86,6 +92,17 @@ def normalize_params(V, top_k, top_p):
     return top_k, float(np.float32(top_p))
 
 
+def draw_order(V):
+    """Vocabulary indices in the order the product's draw visits them: lane t of
+    1024 owns the float4 slots t, t + 1024, t + 2048, ...; lanes in order, a lane's
+    slots in order, the 4 entries of a slot in order."""
+    V4 = V // 4
+    J = -(-V4 // THREADS)
+    slots = (np.arange(THREADS)[:, None] + THREADS * np.arange(J)[None, :]).reshape(-1)
+    slots = slots[slots < V4]
+    return (4 * slots[:, None] + np.arange(4)[None, :]).reshape(-1)
+
+
 def _sf(x):
     x = np.where(np.isnan(x), np.float32(0), x).astype(np.float32)
     return np.where(np.isinf(x), np.copysign(FLT_MAX, x), x).astype(np.float32)
@@ -108,14 +125,17 @@ def threshold(p, top_k, top_p):
     csum = np.cumsum(order)
     vals = np.unique(p)[::-1]                       # distinct values, descending
     cnt = np.searchsorted(-order, -vals, side="right")  # #(p >= v) for each distinct v
-    ok = (cnt >= top_k) | (csum[cnt - 1] >= top_p)   # the set {p >= v} is not small
+    use_mass = top_p < 1.0
+    ok = (cnt >= top_k) | (use_mass & (csum[cnt - 1] >= top_p))   # the set {p >= v} is not small
     tau = vals[int(np.argmax(ok))] if ok.any() else vals[-1]
     neq = int(np.count_nonzero(p == tau))
     gt = p > tau
     ngt, mgt = int(np.count_nonzero(gt)), float(p[gt].sum())
     comp = 1.0
     if neq > 0:
-        comp = min((top_p - mgt) / (tau * neq), (top_k - ngt) / neq, 1.0)
+        comp = min((top_k - ngt) / neq, 1.0)
+        if use_mass:
+            comp = min((top_p - mgt) / (tau * neq), comp)
         comp = max(comp, 0.0)
     return float(tau), comp
 
@@ -129,9 +149,13 @@ def kept_weights(p, top_k, top_p):
     return np.where(p > tau, p, np.where(p == tau, p * comp, 0.0))
 
 
-def inverse_cdf(w, u):
-    """(token, margin): first index whose running sum of w reaches u * sum(w), and the
-    distance of that target from the nearest CDF step, relative to the total."""
+def inverse_cdf(w, u, order=None):
+    """(token, margin): first index (visiting w in `order`, default vocabulary order)
+    whose running sum of w reaches u * sum(w), and the distance of that target from
+    the nearest CDF step, relative to the total."""
+    if order is not None:
+        tok, margin = inverse_cdf(w[order], u)
+        return int(order[tok]), margin
     c = np.cumsum(w)
     total = c[-1]
     target = total * u
@@ -142,13 +166,21 @@ def inverse_cdf(w, u):
     return tok, margin
 
 
+def cdf_interval(w, order, tok):
+    """(start, end, total): the part of [0, total] that token `tok` covers when w is
+    visited in `order`."""
+    c = np.cumsum(w[order])
+    k = int(np.flatnonzero(order == tok)[0])
+    return (float(c[k - 1]) if k else 0.0), float(c[k]), float(c[-1])
+
+
 def sample_row(logits, u, temperature=1.0, top_k=-1, top_p=1.0, penalties=None):
     """(token, margin, kept weights) of one row drawn at uniform u."""
     logits = np.asarray(logits, dtype=np.float32)
     top_k, top_p = normalize_params(logits.shape[-1], top_k, top_p)
     p = probabilities(logits, temperature, penalties)
     w = kept_weights(p, top_k, top_p)
-    tok, margin = inverse_cdf(w, u)
+    tok, margin = inverse_cdf(w, u, draw_order(logits.shape[-1]))
     return tok, margin, w
 
 

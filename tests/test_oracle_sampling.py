@@ -167,6 +167,25 @@ def test_inverse_cdf():
     assert tok == 3 and abs(margin - 0.25) < 1e-12
 
 
+def test_draw_order_is_a_permutation():
+    for V in (4, 4096, 4100, 65532, 65536, 100000):
+        o = sr.draw_order(V)
+        assert np.array_equal(np.sort(o), np.arange(V))
+    o = sr.draw_order(8192)
+    assert o[:8].tolist() == [0, 1, 2, 3, 4096, 4097, 4098, 4099]   # lane 0: slots 0 and 1024
+    assert o[8:12].tolist() == [4, 5, 6, 7]                          # then lane 1
+    w = np.zeros(8192)
+    w[[4096, 5]] = 1.0   # vocabulary order meets 5 first, the draw order 4096
+    assert sr.inverse_cdf(w, 0.5)[0] == 5
+    assert sr.inverse_cdf(w, 0.5, o)[0] == 4096
+
+
+def test_top_p_one_sets_no_mass_limit():
+    p = _probs(1000, 2)
+    w = sr.kept_weights(p, 10, 1.0)
+    assert set(np.flatnonzero(w)) == set(np.argsort(-p)[:10].tolist())
+
+
 def test_sampling_law_matches_kept_weights():
     # inverse CDF at Philox uniforms: frequencies follow the kept weights
     p = _probs(64, 3, scale=1.5)

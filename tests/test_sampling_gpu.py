@@ -4,10 +4,12 @@
 The draw is pinned value by value: the kernel's token for row b on its c-th
 call must be the oracle's inverse CDF of the kept weights at the Philox uniform
 of (seed, row b, call c) (oracle/sampling_ref.py).  Probabilities differ from
-the oracle's by float32 rounding, so a mismatch is allowed only where the draw
-target lies within a relative 1e-5 of a CDF step (the test counts those and
-requires them to be rare).  The random stream is the product's Philox4x32-10,
-not the reference's curand stream: parity of the stream itself is not claimed.
+the oracle's by float32 rounding, so where the two tokens differ, the kernel's
+token must still own the part of the oracle's CDF (in the kernel's draw order)
+that holds the draw target, to within 1e-5 of the total; on random logits such
+near-boundary draws must also be rare.  The random stream is the product's
+Philox4x32-10, not the reference's curand stream: parity of the stream itself is
+not claimed.
 """
 import numpy as np
 import pytest
@@ -42,7 +44,9 @@ def _check_draws(toks, logits, seed, call, temperature, top_k, top_p, pens=None)
         got = int(toks[b])
         assert w[got] > 0, (b, got)          # never a truncated token
         if got != want:
-            assert margin < MARGIN, (b, got, want, margin)
+            lo, hi, total = sr.cdf_interval(w, sr.draw_order(w.shape[0]), got)
+            target = u * total
+            assert lo - MARGIN * total <= target <= hi + MARGIN * total, (b, got, want, lo, hi, target)
             near += 1
     return near
 
@@ -83,6 +87,34 @@ def test_untruncated_flat_row(gpu):
     states = ops.setup_rand(77, B)
     toks = ops.temperature_topk_topp(logits.to(gpu), states, 1.0, 0, 1.0).cpu()
     assert _check_draws(toks, logits, 77, 0, 1.0, 0, 1.0) <= 1
+
+
+@pytest.mark.parametrize("V,top_k,top_p", [(65536, 2000, 1.0), (65536, -1, 0.5), (100000, 3000, 0.9)])
+def test_large_ties(gpu, V, top_k, top_p):
+    # a few large logits over a flat floor: the threshold lands on a value shared by
+    # tens of thousands of entries, so the kept weight of every tied entry is the
+    # compensation share and the search ends over more entries than it compacts
+    ops = _ops()
+    B = 4
+    logits = torch.zeros(B, V)
+    for b in range(B):
+        logits[b, torch.arange(10) * 997 + b] = 5.0
+    states = ops.setup_rand(11, B)
+    for call in range(3):
+        toks = ops.temperature_topk_topp(logits.to(gpu), states, 1.0, top_k, top_p).cpu()
+        # steps of the tied entries are below the margin: near-boundary draws are
+        # common here, each one still checked against its CDF interval
+        _check_draws(toks, logits, 11, call, 1.0, top_k, top_p)
+
+
+def test_scratch_mode_uses_last_token(gpu):
+    ops = _ops()
+    B, T, V = 3, 2, 100000
+    logits = _logits(B, V, 14, T=T)
+    a = ops.temperature_topk_topp(logits.to(gpu), ops.setup_rand(6, B), 0.8, 64, 0.9).cpu()
+    _check_draws(a, logits, 6, 0, 0.8, 64, 0.9)
+    b = ops.temperature_topk_topp(logits[:, -1].contiguous().to(gpu), ops.setup_rand(6, B), 0.8, 64, 0.9).cpu()
+    assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("V", [1000, 65536, 100000])
