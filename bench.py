@@ -48,6 +48,8 @@ def parse_args():
                     help="timed calls of the config-2 prefill (B=8, T=1024, H=32; 0: skip)")
     ap.add_argument("--serve-steps", type=int, default=3,
                     help="timed steps of the 7B mixed prefill+decode step (BASELINE config 4; 0: skip)")
+    ap.add_argument("--sampling-calls", type=int, default=50,
+                    help="timed calls per sampling setting at bs=128 over the 65536-token vocabulary (0: skip)")
     ap.add_argument("--rowmajor-gemm", action="store_true",
                     help="run the model decode step on the row-major GEMM instead of the frag GEMM")
     ap.add_argument("--eager", action="store_true",
@@ -209,6 +211,52 @@ def prefill_c2(dev, steps, warmup=2):
                      "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes},
         "kernel": "wkv7_fp32_rows_kernel (256 lanes per (sequence, head), row-split dot products)",
+    }
+
+
+def sampling_bs128(dev, calls, warmup=3):
+    """Token sampling after the config-3 decode step: 128 rows of fp32 logits over the
+    65536-token vocabulary, resident in HBM (vkwr_sampling ops, one 1024-lane workgroup
+    per row).  Eager calls bracketed by HIP events on the current stream."""
+    from vkwr_amd._ops import sampling_ops as ops
+
+    Bs, Vs = 128, 65536
+    g = torch.Generator(device=dev).manual_seed(5)
+    logits = torch.randn(Bs, Vs, device=dev, generator=g) * 3.0
+    pens = torch.zeros(Bs, Vs, device=dev)
+    states = ops.setup_rand(1234, Bs)
+    settings = {
+        "untruncated": lambda: ops.temperature_topk_topp(logits, states, 1.0, -1, 1.0),
+        "greedy": lambda: ops.temperature_topk_topp(logits, states, 1.0, 1, 1.0),
+        "top_k40_top_p0.9": lambda: ops.temperature_topk_topp(logits, states, 0.8, 40, 0.9),
+        "penalties_top_k40_top_p0.9": lambda: ops.repetition_topk_topp(logits, pens, states, 0.5, 0.5, 0.996, 0.8,
+                                                                        40, 0.9),
+    }
+    out = {}
+    for name, call in settings.items():
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(calls):
+            call()
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1000 / calls
+        nbytes = Bs * Vs * 4 * (4 if name.startswith("penalties") else 1)  # logits (+ penalties read twice, written)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us_per_call": round(us, 2), "rows_per_s": round(Bs / (us * 1e-6), 1),
+                     "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del logits, pens, states
+    torch.cuda.empty_cache()
+    return {
+        "workload": "token sampling, B=128 rows x V=65536 fp32 logits (the config-3 decode step's head output)",
+        "calls": calls,
+        "settings": out,
+        "roofline_note": "VALU-bound: one 1024-lane workgroup per row keeps 64 logits per lane in registers and "
+                         "makes ~15 vector operations per logit (128 rows fill half of the 256 CUs)",
+        "kernel": "sampling_kernel<16> (vkwr_amd/csrc/sampling.hip)",
     }
 
 
@@ -423,6 +471,8 @@ def main():
         result["prefill_c2"] = prefill_c2(dev, args.prefill_calls)
     if args.serve_steps > 0 and not args.eager:
         result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
+    if args.sampling_calls > 0 and not args.eager:
+        result["sampling_bs128"] = sampling_bs128(dev, args.sampling_calls)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

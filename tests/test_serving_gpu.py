@@ -119,3 +119,26 @@ def test_scheduler_matches_teacher_forced_replay(gpu):
             if t >= len(r.prompt) - 1:
                 tok = seq[t + 1]
                 assert logits[tok] >= logits.max() - TOL, (r.rid, t, float(logits.max() - logits[tok]))
+
+
+def test_scheduler_with_gpu_sampler(gpu):
+    """The scheduler with the GPU sampler: top_k = 1 reproduces the greedy run token for
+    token; temperature sampling with one seed is reproducible and stays in the vocabulary."""
+    from vkwr_amd.model_executor import ContinuousBatcher, GpuSampler, MixedEngine
+
+    def run(sample):
+        cfg, model, state = _tiny(gpu, 4)
+        eng = MixedEngine(model, 48, max_seqs=16)
+        sched = ContinuousBatcher(eng, state, max_decode=4, max_prefill_chunks=2, chunk=8, sample=sample)
+        g = torch.Generator().manual_seed(5)
+        reqs = [sched.submit(torch.randint(0, cfg.vocab, (3 + i,), generator=g).tolist(), 4) for i in range(6)]
+        sched.run(max_steps=200)
+        return cfg, [r.output for r in reqs]
+
+    cfg, greedy = run(None)
+    _, top1 = run(GpuSampler(16, cfg.vocab, gpu, seed=3, top_k=1))
+    assert top1 == greedy
+    _, s1 = run(GpuSampler(16, cfg.vocab, gpu, seed=9, temperature=1.3, top_k=20, top_p=0.9))
+    _, s2 = run(GpuSampler(16, cfg.vocab, gpu, seed=9, temperature=1.3, top_k=20, top_p=0.9))
+    assert s1 == s2
+    assert all(0 <= t < cfg.vocab for out in s1 for t in out)

@@ -250,6 +250,11 @@ def sample(logits, states, out, temperature=1.0, top_k=-1, top_p=1.0, penalties=
     (B*V fp32) is needed only above SAMPLING_REGISTER_VOCAB."""
     B, V = out.shape[0], logits.shape[-1]
     T = logits.shape[1] if logits.dim() == 3 else 1
+    assert logits.dtype == torch.float32 and logits.is_contiguous() and logits.numel() == B * T * V
+    assert out.dtype == torch.int32 and states.numel() * states.element_size() >= B * SAMPLING_STATE_BYTES
+    assert penalties is None or (penalties.dtype == torch.float32 and penalties.is_contiguous()
+                                 and penalties.numel() == B * V)
+    assert scratch is None or (scratch.dtype == torch.float32 and scratch.numel() >= B * V)
     if penalties is None:
         st = _samp_temp(B, T, V, _ptr(logits), _ptr(states), _ptr(out), _ptr(scratch), temperature, top_k, top_p,
                         _stream())

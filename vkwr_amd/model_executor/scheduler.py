@@ -15,7 +15,8 @@ the logits of its last prompt chunk; each later one from its decode row.
 Finished sequences release their slot immediately, so waiting requests are
 admitted the next step (256 decode rows + 4 x 512 prefill
 rows per step, 2048-slot pool).  The default sampler is greedy (argmax); pass
-`sample` to use another.
+`sample` to use another, e.g. a ``GpuSampler`` (temperature / top-k / top-p on
+the vkwr_sampling kernels).
 """
 from collections import deque
 from dataclasses import dataclass, field
