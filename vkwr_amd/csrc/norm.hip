@@ -70,13 +70,35 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
   const int64_t dst = row * (int64_t)C;
   const int64_t sdst = (p.shift_slots ? (int64_t)p.shift_slots[row] : row) * (int64_t)C;
 
+  // Vector path: every input of the row -- x, residual, the LN weight and bias, the
+  // previous token's shift row and the mix vectors -- is requested here, before the
+  // two reductions, so the row costs one memory round trip instead of three.
+  constexpr bool kVec = VW == 8 && !kBf16;
+  constexpr int kPre = kVec ? NV : 1;
+  h8 wpre[kPre], bpre[kPre], ppre[kPre], mpre[kPre][NMIX > 0 ? NMIX : 1];
+  if constexpr (kVec) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int c0 = (tid + n * kThreads) * VW;
+      if (c0 < C) {
+        wpre[n] = ld8(reinterpret_cast<const _Float16*>(p.weight) + c0);
+        bpre[n] = ld8(reinterpret_cast<const _Float16*>(p.bias) + c0);
+        if constexpr (NMIX > 0) {
+          ppre[n] = ld8(p.shift + sdst + c0);
+#pragma unroll
+          for (int i = 0; i < NMIX; ++i) mpre[n][i] = ld8(p.mix[i] + c0);
+        }
+      }
+    }
+  }
+
   float v[NV][VW];
   float sum = 0.0f;
 #pragma unroll
   for (int n = 0; n < NV; ++n) {
     const int c0 = (tid + n * kThreads) * VW;
     if (c0 < C) {
-      if constexpr (VW == 8 && !kBf16) {
+      if constexpr (kVec) {
         const h8 xv = ld8(reinterpret_cast<const _Float16*>(p.x) + src + c0);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[n][e] = (float)xv.v[e];
@@ -119,7 +141,9 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
 #pragma unroll
     for (int e = 0; e < VW; ++e) {
       const float t = (v[n][e] - mean) * rstd;
-      yh[e] = (_Float16)__builtin_fmaf(t, ld_in<kBf16>(p.weight, c0 + e), ld_in<kBf16>(p.bias, c0 + e));
+      const float wt = kVec ? (float)wpre[n % kPre].v[e] : ld_in<kBf16>(p.weight, c0 + e);
+      const float bs = kVec ? (float)bpre[n % kPre].v[e] : ld_in<kBf16>(p.bias, c0 + e);
+      yh[e] = (_Float16)__builtin_fmaf(t, wt, bs);
       xo[e] = (_Float16)v[n][e];
     }
     const int64_t odst = p.out_frag ? frag_index(row, c0, C) : dst + c0;  // y / out[] element offset
@@ -138,7 +162,8 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       // Token-shift lerp of the fp16-rounded LN output with the previous token's.
       _Float16 prev[VW];
       if constexpr (VW == 8) {
-        *reinterpret_cast<h8*>(prev) = ld8(p.shift + sdst + c0);
+        if constexpr (kVec) *reinterpret_cast<h8*>(prev) = ppre[n % kPre];
+        else *reinterpret_cast<h8*>(prev) = ld8(p.shift + sdst + c0);
         st8(p.x_out + dst + c0, *reinterpret_cast<const h8*>(xo));
         st8(p.shift + sdst + c0, *reinterpret_cast<const h8*>(yh));
       } else {
@@ -155,7 +180,8 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           const float yv = (float)yh[e];
-          o[e] = (_Float16)__builtin_fmaf((float)prev[e] - yv, (float)p.mix[i][c0 + e], yv);
+          const float mv = kVec ? (float)mpre[n % kPre][i % (NMIX > 0 ? NMIX : 1)].v[e] : (float)p.mix[i][c0 + e];
+          o[e] = (_Float16)__builtin_fmaf((float)prev[e] - yv, mv, yv);
         }
         if constexpr (VW == 8) {
           st8(p.out[i] + odst, *reinterpret_cast<const h8*>(o));
