@@ -59,6 +59,7 @@ FP32_CASES = [
     (2, 128, 12, "baseline", 0.0),
     (1, 33, 2, "realistic", 0.1),    # row-split kernel: two full 16-token chunks + a 1-token tail
     (2, 47, 3, "baseline", 0.1),     # ... odd tail inside the last chunk
+    (16, 20, 32, "realistic", 0.1),  # B*H = 512: one workgroup per (sequence, head), 2 rows per lane
 ]
 
 
@@ -286,6 +287,29 @@ def test_prefill_config2_full_rows_chunking_and_tolerance(gpu):
     assert err.sum().item() / y4.double().abs().sum().item() <= Y_MEAN_REL
     assert (s1 - s4).abs().max().item() <= STATE_MAX_ABS
     assert not torch.equal(s1, s4)  # the two kernels really reduce in different orders
+
+
+def test_rows_kernel_split_forms_are_identical(gpu):
+    """Below 2 x CUs (sequence, head) pairs the row-split kernel gives each pair two
+    workgroups of 32 rows; above, one workgroup of 64.  Both keep every row's lane
+    mapping and reduction order: a B=16, H=32 call (512 pairs, one workgroup each) equals
+    the same work as two B=8 calls (256 pairs, two workgroups each), bitwise."""
+    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+
+    B, T, H = 16, 37, 32
+    C = H * 64
+    ins = _dev(make_wkv_inputs(B, T, H, seed=44, dist="realistic"), gpu)
+    s_all = torch.from_numpy(make_state(B, H, seed=44, std=0.1)).to(gpu)
+    s_half = s_all.clone()
+    y_all = ops.wkv_forward_fp32(B, T, C, H, s_all, *ins)
+    ys = []
+    for b0 in (0, 8):
+        st = s_half[b0:b0 + 8].contiguous()
+        ys.append(ops.wkv_forward_fp32(8, T, C, H, st, *(x[b0:b0 + 8].contiguous() for x in ins)))
+        s_half[b0:b0 + 8] = st
+    torch.cuda.synchronize()
+    assert torch.equal(y_all, torch.cat(ys, dim=0))
+    assert torch.equal(s_all, s_half)
 
 
 def test_rows_kernel_unaligned_inputs_match_oracle(gpu):

@@ -25,6 +25,19 @@ int check_launch(const char* what) {
   return VKWR_OK;
 }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 }  // namespace vk
 
 extern "C" const char* vkwr_status_string(int status) {

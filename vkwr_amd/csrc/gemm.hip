@@ -597,18 +597,6 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
   return ws;
 }
 
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 // Tiles (256x256) of a large-M batch and its stream-K split; returns the workspace bytes.
 int64_t plan_big(Batch& bt, BigPlan& pl) {
   int T = 0, k_all = -1;

@@ -16,6 +16,9 @@ void clear_error();
 // Returns VKWR_OK, or VKWR_ERR_LAUNCH with the HIP error text recorded.
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cus();
+
 #define VK_REQUIRE(cond, ...)          \
   do {                                 \
     if (!(cond)) {                     \

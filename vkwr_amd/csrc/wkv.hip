@@ -272,23 +272,32 @@ struct RowsArgs {
   int vec;  // 16-byte aligned r..b and 8-byte aligned y: vector loads/stores
 };
 
-template <bool kSlots>
+// kRPL = state rows per lane.  2: one workgroup per (sequence, head), lanes own rows
+// 16 wv + 2 q, +1.  1: two workgroups per (sequence, head), each owning 32 rows
+// (32 half + 8 wv + q): rows are independent (sa and y reduce within a row), so the
+// halves share nothing but the staged token vectors, which each stages itself.  With
+// fewer (sequence, head) pairs than twice the CUs this puts two waves on each SIMD to
+// hide the dependent-chain latency of a token step.  Every row sees the same lane
+// column mapping and reduction order in both forms, so the results are identical.
+template <bool kSlots, int kRPL>
 __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
   const Fp32Args& p = ra.a;
   __shared__ f4 vl[kRowsBufs * kRowsTC * kRowsVecs * 16];  // [buffer][token][vector][16 x f4]
-  __shared__ h2 ybuf[4][kRowsTC][8];                        // per wave: 16 tokens x 16 rows
+  __shared__ _Float16 ybuf[4][kRowsTC][8][kRPL];            // per wave: 16 tokens x 8 kRPL rows
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = lane & 7, q = lane >> 3;
-  const int i0 = 16 * wv + 2 * q;
-  const int bh = blockIdx.x;
+  const int bh = kRPL == 2 ? blockIdx.x : blockIdx.x >> 1;
+  const int half = kRPL == 2 ? 0 : blockIdx.x & 1;
+  const int i0 = kRPL == 2 ? 16 * wv + 2 * q : 32 * half + 8 * wv + q;
   const int bi = bh / p.H;
   const int h = bh - bi * p.H;
   const int T = p.T;
   const size_t tok0 = (size_t)bi * T * p.C + (size_t)h * kHead;
   float* S = state_block<kSlots>(p, bi, h);
   if (S == nullptr) {
-    for (int idx = tid; idx < T * kHead; idx += 256)
-      p.y[tok0 + (size_t)(idx >> 6) * p.C + (idx & 63)] = (_Float16)__builtin_nanf("");
+    constexpr int kRows = 32 * kRPL;  // rows of this workgroup
+    for (int idx = tid; idx < T * kRows; idx += 256)
+      p.y[tok0 + (size_t)(idx / kRows) * p.C + 32 * half + (idx % kRows)] = (_Float16)__builtin_nanf("");
     return;
   }
 
@@ -326,9 +335,9 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
     }
   };
 
-  float s[2][8];
+  float s[kRPL][8];
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
+  for (int rr = 0; rr < kRPL; ++rr) {
     const float* row = S + (i0 + rr) * kHead;
     const f4 lo = *reinterpret_cast<const f4*>(row + 4 * g);
     const f4 hi = *reinterpret_cast<const f4*>(row + 32 + 4 * g);
@@ -341,7 +350,7 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
 
   struct Tok {
     f4 a[2], r[2], d[2], k[2], b[2];
-    float v0, v1;
+    float v[kRPL];
   };
   // slot = buffer * kRowsTC + token; a is read first (it is needed first)
   auto read_tok = [&](int slot) __attribute__((always_inline)) {
@@ -353,17 +362,17 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
     o.k[0] = base[2 * 16 + g], o.k[1] = base[2 * 16 + 8 + g];
     o.b[0] = base[5 * 16 + g], o.b[1] = base[5 * 16 + 8 + g];
     const float* vv = reinterpret_cast<const float*>(base + 3 * 16) + i0;
-    o.v0 = vv[0];
-    o.v1 = vv[1];
+#pragma unroll
+    for (int rr = 0; rr < kRPL; ++rr) o.v[rr] = vv[rr];
     return o;
   };
 
-  float sa[2];
+  float sa[kRPL];
   // token `cur` (chunk token tt): state update, then y_t with cur.r and sa_{t+1} with nx.a
   auto token = [&](const Tok& cur, const Tok& nx, int tt) __attribute__((always_inline)) {
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const float vi = rr ? cur.v1 : cur.v0;
+    for (int rr = 0; rr < kRPL; ++rr) {
+      const float vi = cur.v[rr];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float x = s[rr][e] * cur.d[e >> 2][e & 3];
@@ -371,25 +380,31 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
         s[rr][e] = __builtin_fmaf(cur.k[e >> 2][e & 3], vi, x);
       }
     }
-    float py[2] = {0.0f, 0.0f}, pa[2] = {0.0f, 0.0f};
+    float py[kRPL], pa[kRPL];
+#pragma unroll
+    for (int rr = 0; rr < kRPL; ++rr) py[rr] = pa[rr] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < kRPL; ++rr) {
         py[rr] = __builtin_fmaf(s[rr][e], cur.r[e >> 2][e & 3], py[rr]);
         pa[rr] = __builtin_fmaf(s[rr][e], nx.a[e >> 2][e & 3], pa[rr]);
       }
     }
-    float y[2];
+    float y[kRPL];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < kRPL; ++rr) {
       y[rr] = sum8(py[rr]);
       sa[rr] = sum8(pa[rr]);
       // keep the sum an fp32 value before the fp16 conversion (no fused mixed-precision op)
       asm volatile("" : "+v"(y[rr]));
     }
-    // the eight lanes of a row group hold the same bits: all write the same word
-    ybuf[wv][tt][q] = h2{(_Float16)y[0], (_Float16)y[1]};
+    // the eight lanes of a row group hold the same bits: all write the same words
+    if constexpr (kRPL == 2) {
+      *reinterpret_cast<h2*>(&ybuf[wv][tt][q][0]) = h2{(_Float16)y[0], (_Float16)y[1]};
+    } else {
+      ybuf[wv][tt][q][0] = (_Float16)y[0];
+    }
   };
 
   const int nchunk = (T + kRowsTC - 1) / kRowsTC;
@@ -404,7 +419,7 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
   {
     const Tok t0v = read_tok(0);
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < kRPL; ++rr) {
       float acc = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(s[rr][e], t0v.a[e >> 2][e & 3], acc);
@@ -437,20 +452,29 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
       stage_store(nbuf == kRowsBufs - 1 ? 0 : nbuf + 1);
       if (c + 3 < nchunk) stage_load((c + 3) * kRowsTC);
     }
-    // this wave's y tile -> HBM: lane -> token lane >> 2, rows 16 wv + 4 (lane & 3) .. + 3
+    // this wave's y tile -> HBM: lane -> token lane >> 2 and 2 kRPL consecutive rows
+    // (row groups 2 (lane & 3), +1 of this wave)
     {
       const int tt = lane >> 2, r4 = lane & 3;
       if (tt < nt) {
-        const h2 lo = ybuf[wv][tt][2 * r4], hi = ybuf[wv][tt][2 * r4 + 1];
-        _Float16* yd = p.y + tok0 + (size_t)(t0 + tt) * p.C + 16 * wv + 4 * r4;
-        if (ra.vec) {
-          typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
-          *reinterpret_cast<hv4*>(yd) = hv4{lo[0], lo[1], hi[0], hi[1]};
+        const _Float16* yb = &ybuf[wv][tt][2 * r4][0];  // 2 kRPL values, row order
+        const int row0 = kRPL == 2 ? 16 * wv + 4 * r4 : 32 * half + 8 * wv + 2 * r4;
+        _Float16* yd = p.y + tok0 + (size_t)(t0 + tt) * p.C + row0;
+        if constexpr (kRPL == 2) {
+          if (ra.vec) {
+            typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<hv4*>(yd) = hv4{yb[0], yb[1], yb[2], yb[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) yd[e] = yb[e];
+          }
         } else {
-          yd[0] = lo[0];
-          yd[1] = lo[1];
-          yd[2] = hi[0];
-          yd[3] = hi[1];
+          if (ra.vec) {
+            *reinterpret_cast<h2*>(yd) = h2{yb[0], yb[1]};
+          } else {
+            yd[0] = yb[0];
+            yd[1] = yb[1];
+          }
         }
       }
     }
@@ -459,7 +483,7 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
   }
 
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
+  for (int rr = 0; rr < kRPL; ++rr) {
     float* row = S + (i0 + rr) * kHead;
     *reinterpret_cast<f4*>(row + 4 * g) = f4{s[rr][0], s[rr][1], s[rr][2], s[rr][3]};
     *reinterpret_cast<f4*>(row + 32 + 4 * g) = f4{s[rr][4], s[rr][5], s[rr][6], s[rr][7]};
@@ -480,7 +504,10 @@ void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
     hipLaunchKernelGGL(wkv7_fp32_step_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   } else if (rows) {
     RowsArgs ra{p, rows_vec_ok(p) ? 1 : 0};
-    hipLaunchKernelGGL(wkv7_fp32_rows_kernel<kSlots>, dim3(B * p.H), dim3(256), 0, stream, ra);
+    if (ra.vec && B * p.H < 2 * device_cus())
+      hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 1>), dim3(2 * B * p.H), dim3(256), 0, stream, ra);
+    else
+      hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 2>), dim3(B * p.H), dim3(256), 0, stream, ra);
   } else {
     hipLaunchKernelGGL(wkv7_fp32_seq_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   }
