@@ -297,7 +297,9 @@ enum {
   VKWR_GEMM_EPI_NONE = 0,
   VKWR_GEMM_EPI_RELU_SQUARE = 1,    /* y = max(acc, 0)^2 */
   VKWR_GEMM_EPI_VALUE_RESIDUAL = 2, /* y = v + (v_first - v) * sigmoid(v0[n] + acc) */
-  VKWR_GEMM_EPI_BIAS = 3            /* y = acc + v0[n] */
+  VKWR_GEMM_EPI_BIAS = 3,           /* y = acc + v0[n] */
+  VKWR_GEMM_EPI_TANH = 4,           /* y = tanh(acc) (same value as VKWR_FRAG_EPI_TANH) */
+  VKWR_GEMM_EPI_SIGMOID = 5         /* y = sigmoid(acc) (same value as VKWR_FRAG_EPI_SIGMOID) */
 };
 
 /* One GEMM of a batch: c[m,n] = epilogue(sum_k act(a[m,k]) * B(k,n)), fp16

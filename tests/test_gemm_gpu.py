@@ -287,11 +287,31 @@ def _big_vs_rowmajor(gpu, shapes, epis, seed):
     ([(768, 448, 1280)], [3]),                       # 15 tiles (not a multiple of the 8 XCDs), bias
     ([(600, 512, 700), (600, 512, 96), (600, 512, 256), (600, 512, 512)], [1, 0, 3, 2]),  # mixed epilogues
     ([(2304, 4096, 4096)], [0]),                     # the 7B o-projection shape of a mixed step
+    ([(2304, 4096, 128), (2304, 4096, 512)], [4, 5]),  # 7B low-rank inputs (padded w, g): tanh, sigmoid
+    ([(2304, 128, 4096), (2304, 512, 4096)], [3, 2]),  # 7B low-rank outputs: bias, value residual
 ])
 def test_big_gemm_bitwise_equals_rowmajor_kernel(gpu, shapes, epis):
     big, ref = _big_vs_rowmajor(gpu, shapes, epis, seed=11)
     for i, (x, y) in enumerate(zip(big, ref)):
         assert torch.equal(x, y), (shapes[i], epis[i], float((x.float() - y.float()).abs().max()))
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 256, 200), (2304, 512, 256)])
+def test_tanh_sigmoid_epilogues(gpu, M, K, N):
+    """c = tanh(a b^T) and sigmoid(a b^T), fp32 accumulation, against torch in float64."""
+    from vkwr_amd import capi
+    g = torch.Generator(device=gpu).manual_seed(M + N)
+    a = torch.randn(M, K, device=gpu, generator=g).half()
+    w = (torch.randn(N, K, device=gpu, generator=g) * 0.05).half()
+    ref = a.double() @ w.double().t()
+    for epi, fn in ((capi.EPI_TANH, torch.tanh), (capi.EPI_SIGMOID, torch.sigmoid)):
+        c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+        p = [capi.gemm_problem(a, w, c, epilogue=epi)]
+        ws = torch.empty(max(capi.gemm_workspace_bytes(p), 0), dtype=torch.uint8, device=gpu)
+        capi.gemm(p, ws)
+        torch.cuda.synchronize()
+        # fp16 output rounding (2^-11 relative, |y| <= 1) plus the fp32 sum's rounding
+        assert (c.double() - fn(ref)).abs().max().item() <= 2e-3
 
 
 def test_big_gemm_batch_with_empty_problem_and_oracle(gpu):

@@ -26,7 +26,7 @@ _f = ctypes.c_float
 GEMM_B_NK, GEMM_B_KN = 0, 1
 ACT_NONE, ACT_TANH, ACT_SIGMOID, ACT_RELU_SQUARE = 0, 1, 2, 3
 EPI_NONE, EPI_RELU_SQUARE, EPI_VALUE_RESIDUAL, EPI_BIAS = 0, 1, 2, 3
-EPI_TANH, EPI_SIGMOID = 4, 5  # frag GEMM only
+EPI_TANH, EPI_SIGMOID = 4, 5
 MAX_GEMM_PROBLEMS = 8
 FRAG_PAD = 128
 

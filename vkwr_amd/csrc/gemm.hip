@@ -83,6 +83,8 @@ __device__ __forceinline__ float epilogue(const Prob& P, float acc, int row, int
     return __builtin_fmaf((float)P.vf[i] - vv, gate, vv);
   }
   if (P.epi == VKWR_GEMM_EPI_BIAS) return acc + (float)P.v0[col];
+  if (P.epi == VKWR_GEMM_EPI_TANH) return tanhf(acc);
+  if (P.epi == VKWR_GEMM_EPI_SIGMOID) return sigmoidf(acc);
   return acc;
 }
 
@@ -360,8 +362,43 @@ __device__ __forceinline__ float big_epilogue(const Prob& P, float y, int row, i
     return y + (float)P.v0[col];
   } else if constexpr (kEpi == VKWR_GEMM_EPI_NONE) {
     return y;
+  } else if constexpr (kEpi == VKWR_GEMM_EPI_TANH) {
+    return tanhf(y);
+  } else if constexpr (kEpi == VKWR_GEMM_EPI_SIGMOID) {
+    return sigmoidf(y);
+  } else if constexpr (kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+    const int64_t i = (int64_t)row * P.n + col;
+    const float vv = (float)P.v[i];
+    const float gate = sigmoidf((float)P.v0[col] + y);
+    return __builtin_fmaf((float)P.vf[i] - vv, gate, vv);
   } else {
     return epilogue(P, y, row, col);
+  }
+}
+
+// Stores a 256x256 accumulator tile through epilogue kEpi (fp16, clipped to M x N).
+template <int kEpi>
+__device__ __forceinline__ void big_store(const Prob& P, const fv16 (&acc)[4][4], int m0, int n0, int wm, int wn,
+                                          int lr, int lh) {
+  const int M = P.m, N = P.n;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // one 32x32 block at a time: an epilogue that reads memory (value residual) would
+      // otherwise have every block's loads hoisted and the tile spilled
+      if constexpr (kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL) asm volatile("" ::: "memory");
+      const int col = n0 + wn * 128 + j * 32 + lr;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (row >= M) continue;
+        float y = big_epilogue<kEpi>(P, acc[i][j][r], row, col);
+        asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+        P.c[(int64_t)row * N + col] = (_Float16)y;
+      }
+    }
   }
 }
 
@@ -459,22 +496,20 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) part[((4 * i + j) * 16 + r) * 256 + tid] = acc[i][j][r];
+  } else if constexpr (kEpi >= 0) {
+    big_store<kEpi>(P, acc, m0, n0, wm, wn, lr, lh);
   } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = n0 + wn * 128 + j * 32 + lr;
-        if (col >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (row >= M) continue;
-          float y = big_epilogue<kEpi>(P, acc[i][j][r], row, col);
-          asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
-          P.c[(int64_t)row * N + col] = (_Float16)y;
-        }
-      }
+    // a batch of mixed epilogues: one branch per tile to a specialized store loop
+    // (a per-element switch would not keep the accumulator tile in registers)
+    switch (P.epi) {
+      case VKWR_GEMM_EPI_RELU_SQUARE: big_store<VKWR_GEMM_EPI_RELU_SQUARE>(P, acc, m0, n0, wm, wn, lr, lh); break;
+      case VKWR_GEMM_EPI_VALUE_RESIDUAL:
+        big_store<VKWR_GEMM_EPI_VALUE_RESIDUAL>(P, acc, m0, n0, wm, wn, lr, lh);
+        break;
+      case VKWR_GEMM_EPI_BIAS: big_store<VKWR_GEMM_EPI_BIAS>(P, acc, m0, n0, wm, wn, lr, lh); break;
+      case VKWR_GEMM_EPI_TANH: big_store<VKWR_GEMM_EPI_TANH>(P, acc, m0, n0, wm, wn, lr, lh); break;
+      case VKWR_GEMM_EPI_SIGMOID: big_store<VKWR_GEMM_EPI_SIGMOID>(P, acc, m0, n0, wm, wn, lr, lh); break;
+      default: big_store<VKWR_GEMM_EPI_NONE>(P, acc, m0, n0, wm, wn, lr, lh); break;
     }
   }
 }
@@ -660,7 +695,7 @@ int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, C
                "%s: problem %d too large", fn, i);
     VK_REQUIRE(q.b_layout == VKWR_GEMM_B_NK || q.b_layout == VKWR_GEMM_B_KN, "%s: bad b_layout", fn);
     VK_REQUIRE(q.a_act >= VKWR_GEMM_ACT_NONE && q.a_act <= VKWR_GEMM_ACT_RELU_SQUARE, "%s: bad a_act", fn);
-    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_GEMM_EPI_BIAS,
+    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_GEMM_EPI_SIGMOID,
                "%s: bad epilogue", fn);
     const bool empty = q.m == 0 || q.n == 0;
     VK_REQUIRE(empty || (q.a && q.b && q.c), "%s: null pointer in problem %d", fn, i);
