@@ -16,12 +16,13 @@
 //  * Parallelism without a K-split workspace.  A workgroup owns one
 //    (32 TM) x (32 TN) output tile over the whole of K; its NW waves take the
 //    16 KS-wide k blocks w, w + NW, ... with a two-deep register pipeline
-//    (loads are issued unconditionally -- the last block's index is clamped --
-//    so the compiler's wait counts stay exact), and the NW partial tiles are
+//    (loads are issued unconditionally inside the loop and the last blocks are
+//    peeled, so the compiler's wait counts stay exact), and the NW partial tiles are
 //    added through LDS in wave order after one barrier.  Deterministic, no
 //    second kernel, no fp32 partials in HBM.
 //
-// When a problem has several row tiles, the row tiles of one column tile are
+// A launch runs up to 8 problems, one per grid row (blockIdx.y).  When a
+// problem has several row tiles, the row tiles of one column tile are
 // given workgroup ids that differ by multiples of 8: gfx950 dispatches
 // workgroups round-robin over its 8 XCDs, so they share an L2 and the second
 // read of the weight tile hits it.
@@ -49,7 +50,6 @@ struct FProb {
   int m, n, npad, kpad;
   int epi, c_frag;
   int ncol, nmb;            // column tiles, row tiles
-  int wg_begin;             // first workgroup id (multiple of 8)
   int xcd_map;              // row tiles of a column tile share an XCD
 };
 
@@ -68,38 +68,52 @@ __device__ __forceinline__ float apply_act(int epi, float x) {
   return x;
 }
 
-template <int TM, int TN, int NW, int KS>
+// Store paths.  kStoreAny branches per tile on the problem's epilogue and
+// layout; the two specialised ones hold only their own code, which the decode
+// step's single-epilogue launches (FFN key, FFN value, o projection, head)
+// take: the generic path costs them about 0.8 us per launch.
+constexpr int kStoreAny = 0, kStorePlain = 1, kStoreReluSqFrag = 2;
+
+template <int TM, int TN, int NW, int KS, int kStore>
 __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
   constexpr int kTiles = TM * TN;
-  __shared__ float red[NW * kTiles * 1024];
+  __shared__ __attribute__((aligned(16))) float red[NW * kTiles * 1024];
 
-  // ---- problem and tile of this workgroup (uniform)
-  const int wg = blockIdx.x;
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxFragProblems; ++i)
-    if (i < bt.n && wg >= bt.p[i].wg_begin) pi = i;
-  const FProb& P = bt.p[pi];
-  const int lt = wg - P.wg_begin;
-  if (lt >= P.ncol * P.nmb) return;  // round-up workgroup
+  // ---- problem and tile of this workgroup (uniform).  The problem is
+  // blockIdx.y, and every field the workgroup uses is read into a register
+  // here, before the first branch (the empty asm pins the loads above it): the
+  // compiler otherwise sinks each field load below the branch that precedes
+  // its first use, and the dependent kernel-argument round trips delayed the
+  // first operand load by microseconds.
+  const FProb& Pr = bt.p[blockIdx.y];
+  const _Float16* const pa = Pr.a;
+  const _Float16* const pb = Pr.b;
+  _Float16* const pc = Pr.c;
+  const _Float16 *const pv = Pr.v, *const pvf = Pr.vf, *const pv0 = Pr.v0;
+  const int m = Pr.m, n = Pr.n, npad = Pr.npad, kpad = Pr.kpad, epi = Pr.epi, c_frag = Pr.c_frag;
+  const int ncol = Pr.ncol, nmb = Pr.nmb, xcd_map = Pr.xcd_map;
+  asm volatile("" ::"s"(pa), "s"(pb), "s"(pc), "s"(pv), "s"(pvf), "s"(pv0), "s"(m), "s"(n), "s"(npad), "s"(kpad),
+               "s"(epi), "s"(c_frag), "s"(ncol), "s"(nmb), "s"(xcd_map));
+  const int lt = blockIdx.x;
+  if (lt >= ncol * nmb) return;  // round-up workgroup
   int cb, mb;
-  if (P.xcd_map) {
+  if (xcd_map) {
     const int x = lt & 7, t = lt >> 3;
-    cb = (t / P.nmb) * 8 + x;
-    mb = t % P.nmb;
+    cb = (t / nmb) * 8 + x;
+    mb = t % nmb;
   } else {
-    cb = lt / P.nmb;
-    mb = lt % P.nmb;
+    cb = lt / nmb;
+    mb = lt % nmb;
   }
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t kstep = P.kpad >> 4;  // 16-k steps per 32-row block
+  const int64_t kstep = kpad >> 4;  // 16-k steps per 32-row block
   const _Float16* ap[TM];
   const _Float16* bp[TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) ap[i] = P.a + ((int64_t)(mb * TM + i) * kstep * 64 + lane) * 8;
+  for (int i = 0; i < TM; ++i) ap[i] = pa + ((int64_t)(mb * TM + i) * kstep * 64 + lane) * 8;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) bp[j] = P.b + ((int64_t)(cb * TN + j) * kstep * 64 + lane) * 8;
+  for (int j = 0; j < TN; ++j) bp[j] = pb + ((int64_t)(cb * TN + j) * kstep * 64 + lane) * 8;
 
   fv16 acc[TM][TN];
 #pragma unroll
@@ -109,10 +123,9 @@ __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int nper = P.kpad / (16 * KS * NW);  // k blocks per wave (host guarantees >= 1, exact)
+  const int nper = kpad / (16 * KS * NW);  // k blocks per wave (host guarantees >= 1, exact)
   hv8 fa[2][KS][TM], fb[2][KS][TN];
   auto load = [&](int buf, int j) {
-    j = j < nper ? j : nper - 1;
     const int64_t o = (int64_t)(wave + NW * j) * KS * 512;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -133,18 +146,30 @@ __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
   };
   // The scheduling barriers keep each prefetch ahead of the MFMAs that do not
   // need it (left alone, the scheduler sinks the loads below them).
+  // Every load inside the loop is unconditional (a conditional prefetch makes
+  // the compiler wait for all outstanding loads); the last one or two blocks
+  // are peeled after it, so no block is loaded twice.
   load(0, 0);
-  for (int j = 0; j + 1 < nper; j += 2) {
-    load(1, j + 1);
+  int jb = 0;
+  for (; jb + 2 < nper; jb += 2) {
+    load(1, jb + 1);
     __builtin_amdgcn_sched_barrier(0);
     compute(0);
     __builtin_amdgcn_sched_barrier(0);
-    load(0, j + 2);
+    load(0, jb + 2);
     __builtin_amdgcn_sched_barrier(0);
     compute(1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (nper & 1) compute(0);
+  if (jb + 1 < nper) {
+    load(1, jb + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+  } else {
+    compute(0);
+  }
 
   // ---- reduce the NW partial tiles in wave order, then 8 columns per thread
 #pragma unroll
@@ -155,43 +180,63 @@ __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
   constexpr int kGroups = kTiles * 16 * 8;
   for (int g = threadIdx.x; g < kGroups; g += NW * 64) {
     const int t = g >> 7, r = (g >> 3) & 15, l0 = (g & 7) * 8;
-    float s[8];
+    // Two 16-byte LDS reads per wave partial, all issued before the adds (read
+    // element by element, the compiler split them into dependent 4- and
+    // 12-byte reads).
+    f4 s0 = *reinterpret_cast<const f4*>(&red[(t * 16 + r) * 64 + l0]);
+    f4 s1 = *reinterpret_cast<const f4*>(&red[(t * 16 + r) * 64 + l0 + 4]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s[e] = red[(t * 16 + r) * 64 + l0 + e];
-#pragma unroll
-    for (int w = 1; w < NW; ++w)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[e] += red[((w * kTiles + t) * 16 + r) * 64 + l0 + e];
+    for (int w = 1; w < NW; ++w) {
+      s0 += *reinterpret_cast<const f4*>(&red[((w * kTiles + t) * 16 + r) * 64 + l0]);
+      s1 += *reinterpret_cast<const f4*>(&red[((w * kTiles + t) * 16 + r) * 64 + l0 + 4]);
+    }
+    const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int i = t / TN, j = t % TN;
     const int row = (mb * TM + i) * 32 + 8 * (r >> 2) + 4 * (l0 >> 5) + (r & 3);
     const int col = (cb * TN + j) * 32 + (l0 & 31);
-    if (row >= P.m) continue;
+    if (row >= m) continue;
     h8 o;
-    if (P.c_frag) {
+    if constexpr (kStore == kStoreReluSqFrag) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(P.epi, s[e]);
-      st8(P.c + frag_index(row, col, P.npad), o);
+      for (int e = 0; e < 8; ++e) {
+        const float x = fmaxf(s[e], 0.0f);
+        o.v[e] = (_Float16)(x * x);
+      }
+      st8(pc + frag_index(row, col, npad), o);
       continue;
     }
-    if (col >= P.n) continue;
-    const int64_t idx = (int64_t)row * P.n + col;
-    if (P.epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
-      const h8 vv = ld8(P.v + idx), vf = ld8(P.vf + idx), v0 = ld8(P.v0 + col);
+    if constexpr (kStore == kStorePlain) {
+      if (col >= n) continue;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)s[e];
+      st8(pc + (int64_t)row * n + col, o);
+      continue;
+    }
+    if (c_frag) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
+      st8(pc + frag_index(row, col, npad), o);
+      continue;
+    }
+    if (col >= n) continue;
+    const int64_t idx = (int64_t)row * n + col;
+    if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+      const h8 vv = ld8(pv + idx), vf = ld8(pvf + idx), v0 = ld8(pv0 + col);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = (float)vv.v[e];
         const float gate = sigmoidf((float)v0.v[e] + s[e]);
         o.v[e] = (_Float16)__builtin_fmaf((float)vf.v[e] - x, gate, x);
       }
-    } else if (P.epi == VKWR_GEMM_EPI_BIAS) {
-      const h8 v0 = ld8(P.v0 + col);
+    } else if (epi == VKWR_GEMM_EPI_BIAS) {
+      const h8 v0 = ld8(pv0 + col);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)(s[e] + (float)v0.v[e]);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(P.epi, s[e]);
+      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
     }
-    st8(P.c + idx, o);
+    st8(pc + idx, o);
   }
 }
 
@@ -276,9 +321,22 @@ FragConfig pick_frag_config(const FBatch& bt) {
   return {1, 1, 8, ks_for(8, 4)};
 }
 
+// Grid: x = workgroups of the largest problem (a multiple of 8, so x mod 8 is
+// the XCD), y = problem.
 template <int TM, int TN, int NW, int KS>
 void launch_cfg(const FBatch& bt, int wgs, hipStream_t s) {
-  hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS>), dim3(wgs), dim3(NW * 64), 0, s, bt);
+  bool relu_sq_frag = true, plain = true;
+  for (int i = 0; i < bt.n; ++i) {
+    relu_sq_frag = relu_sq_frag && bt.p[i].c_frag && bt.p[i].epi == VKWR_GEMM_EPI_RELU_SQUARE;
+    plain = plain && !bt.p[i].c_frag && bt.p[i].epi == VKWR_GEMM_EPI_NONE;
+  }
+  const dim3 grid(wgs, bt.n), block(NW * 64);
+  if (relu_sq_frag)
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreReluSqFrag>), grid, block, 0, s, bt);
+  else if (plain)
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStorePlain>), grid, block, 0, s, bt);
+  else
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreAny>), grid, block, 0, s, bt);
 }
 
 int launch_frag(const FBatch& bt, FragConfig c, int wgs, hipStream_t s) {
@@ -384,17 +442,15 @@ extern "C" int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* 
   if (bt.n == 0) return VKWR_OK;
   const FragConfig cfg = pick_frag_config(bt);
   const int bm = 32 * cfg.tm, bn = 32 * cfg.tn;
-  int begin = 0;
+  int wgs = 0;
   for (int i = 0; i < bt.n; ++i) {
     FProb& P = bt.p[i];
     VK_REQUIRE(P.kpad % (16 * cfg.ks * cfg.nw) == 0, "%s: internal: K split", fn);
     P.ncol = P.npad / bn;
     P.nmb = (P.m + bm - 1) / bm;
-    P.wg_begin = begin;
     P.xcd_map = P.nmb > 1 && P.ncol % 8 == 0;
-    const int wgs = P.ncol * P.nmb;
-    begin += (wgs + 7) / 8 * 8;
+    wgs = std::max(wgs, (P.ncol * P.nmb + 7) / 8 * 8);
   }
-  if (int e = launch_frag(bt, cfg, begin, (hipStream_t)stream)) return e;
+  if (int e = launch_frag(bt, cfg, wgs, (hipStream_t)stream)) return e;
   return check_launch(fn);
 }

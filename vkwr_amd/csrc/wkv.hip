@@ -592,9 +592,13 @@ __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
   int lane2 = lane;
   asm volatile("" : "+s"(S2), "+v"(lane2));
   if constexpr (kIlv) {
+    // Non-temporal stores: written as ordinary stores, 64 MiB of dirty state
+    // per layer sit in the memory-side cache and are written back while the
+    // next kernels stream their weights, which slows those reads.
 #pragma unroll
     for (int q = 0; q < 16; ++q)
-      *reinterpret_cast<f4*>(S2 + (q * kHead + lane2) * 4) = f4{s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]};
+      __builtin_nontemporal_store(f4{s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]},
+                                  reinterpret_cast<f4*>(S2 + (q * kHead + lane2) * 4));
   } else {
     store_state_fp32(S2, st, s, lane2);
   }
