@@ -21,7 +21,7 @@
 //    added through LDS in wave order after one barrier.  Deterministic, no
 //    second kernel, no fp32 partials in HBM.
 //
-// A launch runs up to 8 problems, one per grid row (blockIdx.y).  When a
+// A launch runs up to 8 problems, each on its own range of workgroups.  When a
 // problem has several row tiles, the row tiles of one column tile are
 // given workgroup ids that differ by multiples of 8: gfx950 dispatches
 // workgroups round-robin over its 8 XCDs, so they share an L2 and the second
@@ -50,6 +50,7 @@ struct FProb {
   int m, n, npad, kpad;
   int epi, c_frag;
   int ncol, nmb;            // column tiles, row tiles
+  int wg_begin;             // first workgroup id (multiple of 8)
   int xcd_map;              // row tiles of a column tile share an XCD
 };
 
@@ -70,31 +71,41 @@ __device__ __forceinline__ float apply_act(int epi, float x) {
 
 // Store paths.  kStoreAny branches per tile on the problem's epilogue and
 // layout; the two specialised ones hold only their own code, which the decode
-// step's single-epilogue launches (FFN key, FFN value, o projection, head)
+// step's single-problem launches (FFN key, FFN value, o projection, head)
 // take: the generic path costs them about 0.8 us per launch.
 constexpr int kStoreAny = 0, kStorePlain = 1, kStoreReluSqFrag = 2;
 
-template <int TM, int TN, int NW, int KS, int kStore>
+template <int TM, int TN, int NW, int KS, int kStore, bool kMulti>
 __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
   constexpr int kTiles = TM * TN;
   __shared__ __attribute__((aligned(16))) float red[NW * kTiles * 1024];
 
-  // ---- problem and tile of this workgroup (uniform).  The problem is
-  // blockIdx.y, and every field the workgroup uses is read into a register
-  // here, before the first branch (the empty asm pins the loads above it): the
-  // compiler otherwise sinks each field load below the branch that precedes
-  // its first use, and the dependent kernel-argument round trips delayed the
-  // first operand load by microseconds.
-  const FProb& Pr = bt.p[blockIdx.y];
+  // ---- problem and tile of this workgroup (uniform).  Every field the
+  // workgroup uses is read into a register here, before the first branch (the
+  // empty asm pins the loads above it): the compiler otherwise sinks each field
+  // load below the branch that precedes its first use, and each dependent
+  // kernel-argument round trip delays the first operand load by ~0.3 us.  A
+  // single-problem launch needs that one round; a batch first finds its
+  // problem among the first-workgroup ids (one more round).  The problems of a
+  // batch own consecutive workgroup ranges: with one grid row per problem
+  // instead, the small problems' empty slots queue behind the large ones'
+  // one-workgroup-per-CU tiles.
+  int pi = 0;
+  if constexpr (kMulti) {
+#pragma unroll
+    for (int i = 1; i < kMaxFragProblems; ++i)
+      if (i < bt.n && (int)blockIdx.x >= bt.p[i].wg_begin) pi = i;
+  }
+  const FProb& Pr = bt.p[pi];
   const _Float16* const pa = Pr.a;
   const _Float16* const pb = Pr.b;
   _Float16* const pc = Pr.c;
   const _Float16 *const pv = Pr.v, *const pvf = Pr.vf, *const pv0 = Pr.v0;
   const int m = Pr.m, n = Pr.n, npad = Pr.npad, kpad = Pr.kpad, epi = Pr.epi, c_frag = Pr.c_frag;
-  const int ncol = Pr.ncol, nmb = Pr.nmb, xcd_map = Pr.xcd_map;
+  const int ncol = Pr.ncol, nmb = Pr.nmb, xcd_map = Pr.xcd_map, wg_begin = Pr.wg_begin;
   asm volatile("" ::"s"(pa), "s"(pb), "s"(pc), "s"(pv), "s"(pvf), "s"(pv0), "s"(m), "s"(n), "s"(npad), "s"(kpad),
-               "s"(epi), "s"(c_frag), "s"(ncol), "s"(nmb), "s"(xcd_map));
-  const int lt = blockIdx.x;
+               "s"(epi), "s"(c_frag), "s"(ncol), "s"(nmb), "s"(xcd_map), "s"(wg_begin));
+  const int lt = (int)blockIdx.x - wg_begin;
   if (lt >= ncol * nmb) return;  // round-up workgroup
   int cb, mb;
   if (xcd_map) {
@@ -321,8 +332,8 @@ FragConfig pick_frag_config(const FBatch& bt) {
   return {1, 1, 8, ks_for(8, 4)};
 }
 
-// Grid: x = workgroups of the largest problem (a multiple of 8, so x mod 8 is
-// the XCD), y = problem.
+// One workgroup range per problem, each a multiple of 8 long (so a tile's id
+// mod 8 is its XCD).
 template <int TM, int TN, int NW, int KS>
 void launch_cfg(const FBatch& bt, int wgs, hipStream_t s) {
   bool relu_sq_frag = true, plain = true;
@@ -330,13 +341,15 @@ void launch_cfg(const FBatch& bt, int wgs, hipStream_t s) {
     relu_sq_frag = relu_sq_frag && bt.p[i].c_frag && bt.p[i].epi == VKWR_GEMM_EPI_RELU_SQUARE;
     plain = plain && !bt.p[i].c_frag && bt.p[i].epi == VKWR_GEMM_EPI_NONE;
   }
-  const dim3 grid(wgs, bt.n), block(NW * 64);
-  if (relu_sq_frag)
-    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreReluSqFrag>), grid, block, 0, s, bt);
+  const dim3 grid(wgs), block(NW * 64);
+  if (bt.n > 1)
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreAny, true>), grid, block, 0, s, bt);
+  else if (relu_sq_frag)
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreReluSqFrag, false>), grid, block, 0, s, bt);
   else if (plain)
-    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStorePlain>), grid, block, 0, s, bt);
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStorePlain, false>), grid, block, 0, s, bt);
   else
-    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreAny>), grid, block, 0, s, bt);
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreAny, false>), grid, block, 0, s, bt);
 }
 
 int launch_frag(const FBatch& bt, FragConfig c, int wgs, hipStream_t s) {
@@ -449,7 +462,8 @@ extern "C" int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* 
     P.ncol = P.npad / bn;
     P.nmb = (P.m + bm - 1) / bm;
     P.xcd_map = P.nmb > 1 && P.ncol % 8 == 0;
-    wgs = std::max(wgs, (P.ncol * P.nmb + 7) / 8 * 8);
+    P.wg_begin = wgs;
+    wgs += (P.ncol * P.nmb + 7) / 8 * 8;
   }
   if (int e = launch_frag(bt, cfg, wgs, (hipStream_t)stream)) return e;
   return check_launch(fn);
