@@ -419,6 +419,19 @@ typedef struct vkwr_frag_gemm_problem {
 VKWR_EXPORT int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* problems,
                                    void* stream);
 
+/* One frag GEMM with K split over `splits` workgroups per 64 x 64 output
+ * tile: the parts write fp32 partial tiles to `workspace`, and a second
+ * kernel adds them in increasing K order and applies the epilogue (same
+ * epilogues and layouts as vkwr_frag_gemm_f16).  For long-K decode GEMMs
+ * (the FFN value, K = 4 F) whose untiled form reads the activations once per
+ * 32-column tile.  Deterministic.  frag_pad(k) must be a multiple of
+ * 256 * splits; splits in 1..16; workspace 16-byte aligned, at least
+ * vkwr_frag_gemm_splitk_workspace_bytes(m, n, splits) bytes.  Calls that share
+ * a workspace must not overlap.  No counterpart in the reference (see above). */
+VKWR_EXPORT int64_t vkwr_frag_gemm_splitk_workspace_bytes(int64_t m, int64_t n, int splits);
+VKWR_EXPORT int vkwr_frag_gemm_splitk_f16(const vkwr_frag_gemm_problem* problem, int splits,
+                                          void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- token sampling (reference csrc/sampling/, ops vkwr_sampling::*) ----
  *
  * Per batch row b, on the logits of its last token (logits [B,T,V] fp32, row

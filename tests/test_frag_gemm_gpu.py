@@ -205,6 +205,74 @@ def test_frag_gemm_rank_out_chain(gpu):
     check(out, ref, ACC * abs_sum + hid_err, "rank chain")
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(128, 2048, 8192, 4), (100, 2048, 8192, 8), (128, 512, 2048, 2),
+                                          (1, 128, 1024, 4), (64, 256, 256, 1)])
+def test_frag_gemm_splitk_vs_oracle(gpu, M, N, K, splits):
+    """vkwr_frag_gemm_splitk_f16: K parts added in order by the reduce kernel;
+    same bar as the unsplit kernel, run-to-run identical, and the workspace
+    size formula."""
+    from vkwr_amd import capi
+    a, w = h(M, K), h(N, K, scale=0.05)
+    pa, pw = pack(a, gpu, M, K), pack(w, gpu, N, K)
+    need = capi.frag_splitk_workspace_bytes(M, N, splits)
+    assert need == splits * ((M + 63) // 64 * 64) * capi.frag_pad(N) * 4
+    ws = torch.full((need // 4,), float("nan"), dtype=torch.float32, device=gpu)
+    c = torch.full((M, N), float("nan"), dtype=torch.float16, device=gpu)
+    capi.frag_gemm_splitk(capi.frag_problem(pa, pw, c, M, N, K), splits, ws)
+    ref, abs_sum = R.gemm(a, w, "nk")
+    check(c, ref, ACC * abs_sum, f"split {M}x{N}x{K}/{splits}")
+    first = c.clone()
+    capi.frag_gemm_splitk(capi.frag_problem(pa, pw, c, M, N, K), splits, ws)
+    assert torch.equal(c, first)
+
+
+@pytest.mark.parametrize("epi", ["relu2_frag", "tanh_frag", "vres", "bias"])
+def test_frag_gemm_splitk_epilogues(gpu, epi):
+    from vkwr_amd import capi
+    M, N, K, splits = 128, 512, 4096, 4
+    a, w = h(M, K), h(N, K, scale=0.02)
+    v, vf, v0 = h(M, N), h(M, N), h(N)
+    pa, pw = pack(a, gpu, M, K), pack(w, gpu, N, K)
+    ws = torch.empty(capi.frag_splitk_workspace_bytes(M, N, splits) // 4, dtype=torch.float32, device=gpu)
+    y64 = a.astype(np.float64) @ w.astype(np.float64).T
+    _, abs_sum = R.gemm(a, w, "nk")
+    if epi.endswith("_frag"):
+        name = epi[:-5]
+        code = {"relu2": capi.EPI_RELU_SQUARE, "tanh": capi.EPI_TANH}[name]
+        cf = capi.frag_empty(M, N, gpu)
+        capi.frag_gemm_splitk(capi.frag_problem(pa, pw, cf, M, N, K, epilogue=code, c_frag=True), splits, ws)
+        got = torch.from_numpy(frag_to_dense(cf, M, N)[:M, :N].copy())
+        deriv = 2 * np.abs(y64) + 1e-3 if name == "relu2" else np.ones_like(y64)
+        check(got, R._act(y64, name).astype(np.float16), deriv * ACC * abs_sum + 2e-6, epi)
+        return
+    out = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    if epi == "vres":
+        capi.frag_gemm_splitk(capi.frag_problem(pa, pw, out, M, N, K, epilogue=capi.EPI_VALUE_RESIDUAL,
+                                                v=dev(v, gpu), v_first=dev(vf, gpu), v0=dev(v0, gpu)), splits, ws)
+        ref, _ = R.gemm(a, w, "nk", epi="vres", v=v, v_first=vf, v0=v0)
+        d = np.abs(vf.astype(np.float64) - v.astype(np.float64)) * 0.25
+        check(out, ref, d * ACC * abs_sum + 2e-6, epi)
+    else:
+        capi.frag_gemm_splitk(capi.frag_problem(pa, pw, out, M, N, K, epilogue=capi.EPI_BIAS, v0=dev(v0, gpu)),
+                              splits, ws)
+        check(out, (y64 + v0.astype(np.float64)).astype(np.float16), ACC * abs_sum, epi)
+
+
+def test_frag_gemm_splitk_rejects_bad_arguments(gpu):
+    from vkwr_amd import capi
+    a = capi.frag_empty(128, 1024, gpu)
+    b = capi.frag_empty(128, 1024, gpu)
+    c = torch.empty(128 * 128, dtype=torch.float16, device=gpu)
+    ws = torch.empty(capi.frag_splitk_workspace_bytes(128, 128, 4) // 4, dtype=torch.float32, device=gpu)
+    p = capi.frag_problem(a, b, c, 128, 128, 1024)
+    with pytest.raises(RuntimeError, match="multiple of 256"):
+        capi.frag_gemm_splitk(p, 8, ws)  # 1024 / 8 < 256
+    with pytest.raises(RuntimeError, match="workspace of"):
+        capi.frag_gemm_splitk(p, 4, ws[:-4])
+    with pytest.raises(RuntimeError, match="splits"):
+        capi.frag_gemm_splitk(p, 0, ws)
+
+
 def test_frag_gemm_rejects_bad_arguments(gpu):
     from vkwr_amd import capi
     a = capi.frag_empty(128, 128, gpu)

@@ -73,6 +73,8 @@ _gn = _sig("vkwr_tmix_groupnorm_bonus_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p
 _wkv_slots = _sig("vkwr_wkv7_fp32_forward_slots",
                   [_i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _frag_gemm = _sig("vkwr_frag_gemm_f16", [_i, ctypes.POINTER(FragProblem), _p])
+_frag_splitk = _sig("vkwr_frag_gemm_splitk_f16", [ctypes.POINTER(FragProblem), _i, _p, _i64, _p])
+_frag_splitk_ws = _sig("vkwr_frag_gemm_splitk_workspace_bytes", [_i64, _i64, _i], _i64)
 _frag_pack = _sig("vkwr_frag_pack_f16", [_i64, _i64, _p, _i, _p, _p])
 _frag_unpack = _sig("vkwr_frag_unpack_f16", [_i64, _i64, _p, _p, _p])
 _ln_mix_frag = _sig("vkwr_add_layer_norm_mix_frag_f16",
@@ -199,6 +201,20 @@ def frag_gemm(problems):
     """Runs 1..8 frag GEMMs in one launch."""
     arr = _arr_frag(problems)
     _check(_frag_gemm(len(problems), arr, _stream()), "vkwr_frag_gemm_f16")
+
+
+def frag_splitk_workspace_bytes(m, n, splits):
+    """Workspace bytes vkwr_frag_gemm_splitk_f16 needs for an [m, n] output in `splits` K parts."""
+    return _frag_splitk_ws(m, n, splits)
+
+
+def frag_gemm_splitk(problem, splits, workspace):
+    """One frag GEMM with K split over `splits` workgroups per 64x64 tile (fp32 partials in
+    `workspace`, a CUDA tensor of at least frag_splitk_workspace_bytes bytes, then an ordered reduce
+    that applies the epilogue)."""
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(_frag_splitk(ctypes.byref(problem), splits, workspace.data_ptr(), nbytes, _stream()),
+           "vkwr_frag_gemm_splitk_f16")
 
 
 def _arr_frag(problems):

@@ -51,6 +51,8 @@ struct FProb {
   int epi, c_frag;
   int ncol, nmb;            // column tiles, row tiles
   int wg_begin;             // first workgroup id (multiple of 8)
+  float* ws;                // K split: fp32 partial tiles [ksplit][nmb * 32 * TM][npad]
+  int ksplit;               // K parts (1: no split)
   int xcd_map;              // row tiles of a column tile share an XCD
 };
 
@@ -73,7 +75,68 @@ __device__ __forceinline__ float apply_act(int epi, float x) {
 // layout; the two specialised ones hold only their own code, which the decode
 // step's single-problem launches (FFN key, FFN value, o projection, head)
 // take: the generic path costs them about 0.8 us per launch.
-constexpr int kStoreAny = 0, kStorePlain = 1, kStoreReluSqFrag = 2;
+// kStorePartial writes the workgroup's fp32 tile of one K part to the split
+// workspace; frag_splitk_reduce_kernel adds the parts and applies the epilogue.
+constexpr int kStoreAny = 0, kStorePlain = 1, kStoreReluSqFrag = 2, kStorePartial = 3;
+
+// W consecutive fp16 values, stored or loaded as one access.
+template <int W>
+struct alignas(2 * W) HW {
+  _Float16 v[W];
+};
+
+// Epilogue and store of W consecutive output columns (col % W == 0, W = 4 or
+// 8: a group never straddles a frag chunk or the row end, n being a multiple
+// of 8) of one row.
+template <int kStore, int W>
+__device__ __forceinline__ void store_cols(const float (&s)[W], int row, int col, int n, int npad, int epi,
+                                           int c_frag, _Float16* pc, const _Float16* pv, const _Float16* pvf,
+                                           const _Float16* pv0) {
+  typedef HW<W> hw;
+  hw o;
+  if constexpr (kStore == kStoreReluSqFrag) {
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      const float x = fmaxf(s[e], 0.0f);
+      o.v[e] = (_Float16)(x * x);
+    }
+    *reinterpret_cast<hw*>(pc + frag_index(row, col, npad)) = o;
+    return;
+  }
+  if constexpr (kStore == kStorePlain) {
+    if (col >= n) return;
+#pragma unroll
+    for (int e = 0; e < W; ++e) o.v[e] = (_Float16)s[e];
+    *reinterpret_cast<hw*>(pc + (int64_t)row * n + col) = o;
+    return;
+  }
+  if (c_frag) {
+#pragma unroll
+    for (int e = 0; e < W; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
+    *reinterpret_cast<hw*>(pc + frag_index(row, col, npad)) = o;
+    return;
+  }
+  if (col >= n) return;
+  const int64_t idx = (int64_t)row * n + col;
+  if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+    const hw vv = *reinterpret_cast<const hw*>(pv + idx), vf = *reinterpret_cast<const hw*>(pvf + idx),
+             v0 = *reinterpret_cast<const hw*>(pv0 + col);
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      const float x = (float)vv.v[e];
+      const float gate = sigmoidf((float)v0.v[e] + s[e]);
+      o.v[e] = (_Float16)__builtin_fmaf((float)vf.v[e] - x, gate, x);
+    }
+  } else if (epi == VKWR_GEMM_EPI_BIAS) {
+    const hw v0 = *reinterpret_cast<const hw*>(pv0 + col);
+#pragma unroll
+    for (int e = 0; e < W; ++e) o.v[e] = (_Float16)(s[e] + (float)v0.v[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < W; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
+  }
+  *reinterpret_cast<hw*>(pc + idx) = o;
+}
 
 template <int TM, int TN, int NW, int KS, int kStore, bool kMulti>
 __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
@@ -103,28 +166,37 @@ __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
   const _Float16 *const pv = Pr.v, *const pvf = Pr.vf, *const pv0 = Pr.v0;
   const int m = Pr.m, n = Pr.n, npad = Pr.npad, kpad = Pr.kpad, epi = Pr.epi, c_frag = Pr.c_frag;
   const int ncol = Pr.ncol, nmb = Pr.nmb, xcd_map = Pr.xcd_map, wg_begin = Pr.wg_begin;
+  float* const ws = Pr.ws;
+  const int ksplit = kStore == kStorePartial ? Pr.ksplit : 1;
   asm volatile("" ::"s"(pa), "s"(pb), "s"(pc), "s"(pv), "s"(pvf), "s"(pv0), "s"(m), "s"(n), "s"(npad), "s"(kpad),
-               "s"(epi), "s"(c_frag), "s"(ncol), "s"(nmb), "s"(xcd_map), "s"(wg_begin));
+               "s"(epi), "s"(c_frag), "s"(ncol), "s"(nmb), "s"(xcd_map), "s"(wg_begin), "s"(ws), "s"(ksplit));
   const int lt = (int)blockIdx.x - wg_begin;
-  if (lt >= ncol * nmb) return;  // round-up workgroup
-  int cb, mb;
+  if (lt >= ncol * nmb * ksplit) return;  // round-up workgroup
+  // Tile and K part.  With the XCD map, the K parts and row tiles of a column
+  // tile get ids that differ by multiples of 8 (one L2).
+  int cb, mb, part;
   if (xcd_map) {
     const int x = lt & 7, t = lt >> 3;
-    cb = (t / nmb) * 8 + x;
-    mb = t % nmb;
+    part = t % ksplit;
+    const int u = t / ksplit;
+    cb = (u / nmb) * 8 + x;
+    mb = u % nmb;
   } else {
-    cb = lt / nmb;
-    mb = lt % nmb;
+    part = lt % ksplit;
+    const int u = lt / ksplit;
+    cb = u / nmb;
+    mb = u % nmb;
   }
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t kstep = kpad >> 4;  // 16-k steps per 32-row block
+  const int64_t kstep = kpad >> 4;             // 16-k steps per 32-row block
+  const int64_t k0 = part * (kstep / ksplit);  // first 16-k step of this K part
   const _Float16* ap[TM];
   const _Float16* bp[TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) ap[i] = pa + ((int64_t)(mb * TM + i) * kstep * 64 + lane) * 8;
+  for (int i = 0; i < TM; ++i) ap[i] = pa + (((int64_t)(mb * TM + i) * kstep + k0) * 64 + lane) * 8;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) bp[j] = pb + ((int64_t)(cb * TN + j) * kstep * 64 + lane) * 8;
+  for (int j = 0; j < TN; ++j) bp[j] = pb + (((int64_t)(cb * TN + j) * kstep + k0) * 64 + lane) * 8;
 
   fv16 acc[TM][TN];
 #pragma unroll
@@ -134,7 +206,7 @@ __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int nper = kpad / (16 * KS * NW);  // k blocks per wave (host guarantees >= 1, exact)
+  const int nper = kpad / ksplit / (16 * KS * NW);  // k blocks per wave (host guarantees >= 1, exact)
   hv8 fa[2][KS][TM], fb[2][KS][TN];
   auto load = [&](int buf, int j) {
     const int64_t o = (int64_t)(wave + NW * j) * KS * 512;
@@ -201,54 +273,35 @@ __global__ __launch_bounds__(NW * 64) void frag_gemm_kernel(FBatch bt) {
       s0 += *reinterpret_cast<const f4*>(&red[((w * kTiles + t) * 16 + r) * 64 + l0]);
       s1 += *reinterpret_cast<const f4*>(&red[((w * kTiles + t) * 16 + r) * 64 + l0 + 4]);
     }
-    const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int i = t / TN, j = t % TN;
     const int row = (mb * TM + i) * 32 + 8 * (r >> 2) + 4 * (l0 >> 5) + (r & 3);
     const int col = (cb * TN + j) * 32 + (l0 & 31);
+    if constexpr (kStore == kStorePartial) {
+      float* const o = ws + ((int64_t)part * nmb * (32 * TM) + row) * npad + col;
+      *reinterpret_cast<f4*>(o) = s0;
+      *reinterpret_cast<f4*>(o + 4) = s1;
+      continue;
+    }
     if (row >= m) continue;
-    h8 o;
-    if constexpr (kStore == kStoreReluSqFrag) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = fmaxf(s[e], 0.0f);
-        o.v[e] = (_Float16)(x * x);
-      }
-      st8(pc + frag_index(row, col, npad), o);
-      continue;
-    }
-    if constexpr (kStore == kStorePlain) {
-      if (col >= n) continue;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)s[e];
-      st8(pc + (int64_t)row * n + col, o);
-      continue;
-    }
-    if (c_frag) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
-      st8(pc + frag_index(row, col, npad), o);
-      continue;
-    }
-    if (col >= n) continue;
-    const int64_t idx = (int64_t)row * n + col;
-    if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
-      const h8 vv = ld8(pv + idx), vf = ld8(pvf + idx), v0 = ld8(pv0 + col);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = (float)vv.v[e];
-        const float gate = sigmoidf((float)v0.v[e] + s[e]);
-        o.v[e] = (_Float16)__builtin_fmaf((float)vf.v[e] - x, gate, x);
-      }
-    } else if (epi == VKWR_GEMM_EPI_BIAS) {
-      const h8 v0 = ld8(pv0 + col);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)(s[e] + (float)v0.v[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
-    }
-    st8(pc + idx, o);
+    const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    store_cols<kStore, 8>(s, row, col, n, npad, epi, c_frag, pc, pv, pvf, pv0);
   }
+}
+
+// Adds the ksplit fp32 partial planes of a K-split GEMM in increasing K order
+// and applies the epilogue: one thread per 4 consecutive columns of a row (a
+// 128-row decode batch fills 256 workgroups).
+__global__ __launch_bounds__(256) void frag_splitk_reduce_kernel(FProb P, int mrows) {
+  const int groups = P.npad >> 2;
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= P.m * groups) return;
+  const int row = g / groups, col = (g - row * groups) * 4;
+  const int64_t plane = (int64_t)mrows * P.npad;
+  const float* p = P.ws + (int64_t)row * P.npad + col;
+  f4 a = *reinterpret_cast<const f4*>(p);
+  for (int q = 1; q < P.ksplit; ++q) a += *reinterpret_cast<const f4*>(p + q * plane);
+  const float s[4] = {a.x, a.y, a.z, a.w};
+  store_cols<kStoreAny, 4>(s, row, col, P.n, P.npad, P.epi, P.c_frag, P.c, P.v, P.vf, P.v0);
 }
 
 // ---------------------------------------------------------------- packing
@@ -406,6 +459,55 @@ extern "C" int vkwr_frag_unpack_f16(int64_t rows, int64_t k, const uint16_t* src
   return check_launch(fn);
 }
 
+namespace {
+
+// Validates one problem and fills its kernel descriptor (sizes, pointers,
+// epilogue); tiling fields are set by the caller.
+int fill_problem(const char* fn, int i, const vkwr_frag_gemm_problem& q, FProb& P, bool& empty) {
+  VK_REQUIRE(q.m >= 0 && q.n >= 0 && q.k >= 0, "%s: negative size in problem %d", fn, i);
+  VK_REQUIRE(q.m <= (1 << 20) && q.n <= (1 << 24) && q.k <= (1 << 20), "%s: problem %d too large", fn, i);
+  VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_FRAG_EPI_SIGMOID, "%s: bad epilogue", fn);
+  VK_REQUIRE(q.c_frag == 0 || q.c_frag == 1, "%s: bad c_frag", fn);
+  empty = q.m == 0 || q.n == 0;
+  if (empty) return VKWR_OK;
+  VK_REQUIRE(q.k > 0, "%s: k == 0 in problem %d", fn, i);
+  VK_REQUIRE(q.a && q.b && q.c, "%s: null pointer in problem %d", fn, i);
+  VK_REQUIRE(aligned16(q.a) && aligned16(q.b) && aligned16(q.c), "%s: operands must be 16-byte aligned", fn);
+  if (q.c_frag) {
+    VK_REQUIRE(q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL && q.epilogue != VKWR_GEMM_EPI_BIAS,
+               "%s: value-residual / bias epilogues need a row-major output", fn);
+  } else {
+    VK_REQUIRE(q.n % 8 == 0, "%s: row-major output needs n %% 8 == 0 (problem %d)", fn, i);
+  }
+  if (q.epilogue == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+    VK_REQUIRE(q.v && q.v_first && q.v0, "%s: value-residual epilogue needs v, v_first, v0", fn);
+    VK_REQUIRE(aligned16(q.v) && aligned16(q.v_first) && aligned16(q.v0), "%s: epilogue operands alignment", fn);
+  }
+  if (q.epilogue == VKWR_GEMM_EPI_BIAS) {
+    VK_REQUIRE(q.v0 && aligned16(q.v0), "%s: bias epilogue needs an aligned v0", fn);
+  }
+  P = FProb{};
+  P.a = reinterpret_cast<const _Float16*>(q.a);
+  P.b = reinterpret_cast<const _Float16*>(q.b);
+  P.c = reinterpret_cast<_Float16*>(q.c);
+  P.v = reinterpret_cast<const _Float16*>(q.v);
+  P.vf = reinterpret_cast<const _Float16*>(q.v_first);
+  P.v0 = reinterpret_cast<const _Float16*>(q.v0);
+  P.m = (int)q.m;
+  P.n = (int)q.n;
+  P.npad = (int)frag_pad(q.n);
+  P.kpad = (int)frag_pad(q.k);
+  P.epi = q.epilogue;
+  P.c_frag = q.c_frag;
+  P.ksplit = 1;
+  return VKWR_OK;
+}
+
+// The K-split GEMM runs on 64 x 64 tiles, 8 waves, two 16-k steps per load.
+constexpr int kSplitTile = 64, kSplitKRound = 16 * 2 * 8;
+
+}  // namespace
+
 extern "C" int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* problems, void* stream) {
   clear_error();
   const char* fn = "vkwr_frag_gemm_f16";
@@ -415,42 +517,9 @@ extern "C" int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* 
   FBatch bt;
   bt.n = 0;
   for (int i = 0; i < n_problems; ++i) {
-    const vkwr_frag_gemm_problem& q = problems[i];
-    VK_REQUIRE(q.m >= 0 && q.n >= 0 && q.k >= 0, "%s: negative size in problem %d", fn, i);
-    VK_REQUIRE(q.m <= (1 << 20) && q.n <= (1 << 24) && q.k <= (1 << 20), "%s: problem %d too large", fn, i);
-    VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_FRAG_EPI_SIGMOID, "%s: bad epilogue", fn);
-    VK_REQUIRE(q.c_frag == 0 || q.c_frag == 1, "%s: bad c_frag", fn);
-    if (q.m == 0 || q.n == 0) continue;
-    VK_REQUIRE(q.k > 0, "%s: k == 0 in problem %d", fn, i);
-    VK_REQUIRE(q.a && q.b && q.c, "%s: null pointer in problem %d", fn, i);
-    VK_REQUIRE(aligned16(q.a) && aligned16(q.b) && aligned16(q.c), "%s: operands must be 16-byte aligned", fn);
-    if (q.c_frag) {
-      VK_REQUIRE(q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL && q.epilogue != VKWR_GEMM_EPI_BIAS,
-                 "%s: value-residual / bias epilogues need a row-major output", fn);
-    } else {
-      VK_REQUIRE(q.n % 8 == 0, "%s: row-major output needs n %% 8 == 0 (problem %d)", fn, i);
-    }
-    if (q.epilogue == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
-      VK_REQUIRE(q.v && q.v_first && q.v0, "%s: value-residual epilogue needs v, v_first, v0", fn);
-      VK_REQUIRE(aligned16(q.v) && aligned16(q.v_first) && aligned16(q.v0), "%s: epilogue operands alignment", fn);
-    }
-    if (q.epilogue == VKWR_GEMM_EPI_BIAS) {
-      VK_REQUIRE(q.v0 && aligned16(q.v0), "%s: bias epilogue needs an aligned v0", fn);
-    }
-    FProb& P = bt.p[bt.n++];
-    P = FProb{};
-    P.a = reinterpret_cast<const _Float16*>(q.a);
-    P.b = reinterpret_cast<const _Float16*>(q.b);
-    P.c = reinterpret_cast<_Float16*>(q.c);
-    P.v = reinterpret_cast<const _Float16*>(q.v);
-    P.vf = reinterpret_cast<const _Float16*>(q.v_first);
-    P.v0 = reinterpret_cast<const _Float16*>(q.v0);
-    P.m = (int)q.m;
-    P.n = (int)q.n;
-    P.npad = (int)frag_pad(q.n);
-    P.kpad = (int)frag_pad(q.k);
-    P.epi = q.epilogue;
-    P.c_frag = q.c_frag;
+    bool empty = false;
+    if (int e = fill_problem(fn, i, problems[i], bt.p[bt.n], empty)) return e;
+    if (!empty) ++bt.n;
   }
   if (bt.n == 0) return VKWR_OK;
   const FragConfig cfg = pick_frag_config(bt);
@@ -466,5 +535,43 @@ extern "C" int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem* 
     wgs += (P.ncol * P.nmb + 7) / 8 * 8;
   }
   if (int e = launch_frag(bt, cfg, wgs, (hipStream_t)stream)) return e;
+  return check_launch(fn);
+}
+
+extern "C" int64_t vkwr_frag_gemm_splitk_workspace_bytes(int64_t m, int64_t n, int splits) {
+  if (m <= 0 || n <= 0 || splits < 1) return 0;
+  return (int64_t)splits * ((m + kSplitTile - 1) / kSplitTile * kSplitTile) * frag_pad(n) * (int64_t)sizeof(float);
+}
+
+extern "C" int vkwr_frag_gemm_splitk_f16(const vkwr_frag_gemm_problem* problem, int splits, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_frag_gemm_splitk_f16";
+  VK_REQUIRE(problem != nullptr, "%s: null problem", fn);
+  VK_REQUIRE(splits >= 1 && splits <= 16, "%s: splits must be in 1..16 (got %d)", fn, splits);
+  FBatch bt;
+  bt.n = 1;
+  bool empty = false;
+  if (int e = fill_problem(fn, 0, *problem, bt.p[0], empty)) return e;
+  if (empty) return VKWR_OK;
+  FProb& P = bt.p[0];
+  VK_REQUIRE(P.kpad % (kSplitKRound * splits) == 0, "%s: padded k (%d) must be a multiple of %d * splits", fn,
+             P.kpad, kSplitKRound);
+  const int64_t need = vkwr_frag_gemm_splitk_workspace_bytes(P.m, P.n, splits);
+  VK_REQUIRE(workspace != nullptr && aligned16(workspace), "%s: workspace must be non-null and 16-byte aligned", fn);
+  VK_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes, %lld needed", fn, (long long)workspace_bytes,
+             (long long)need);
+  P.ncol = P.npad / kSplitTile;
+  P.nmb = (P.m + kSplitTile - 1) / kSplitTile;
+  P.xcd_map = P.ncol % 8 == 0;
+  P.wg_begin = 0;
+  P.ws = static_cast<float*>(workspace);
+  P.ksplit = splits;
+  const int wgs = (P.ncol * P.nmb * splits + 7) / 8 * 8;
+  hipLaunchKernelGGL((frag_gemm_kernel<2, 2, 8, 2, kStorePartial, false>), dim3(wgs), dim3(512), 0,
+                     (hipStream_t)stream, bt);
+  const int64_t threads = (int64_t)P.m * (P.npad / 4);
+  hipLaunchKernelGGL(frag_splitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, P, P.nmb * kSplitTile);
   return check_launch(fn);
 }

@@ -227,6 +227,20 @@ class DecodeEngine:
         self.o_in_f, self.xk_f, self.act_f, self.h_f = fr(C), fr(C), fr(F), fr(C)
         self.ffn = buf(B, C)
         self.logits = buf(B, cfg.vocab)
+        # FFN value (K = F): K split over workgroups, fp32 partials in a workspace
+        # sized for the largest batch.
+        nbytes = max(capi.frag_splitk_workspace_bytes(b, C, self._value_splits(b)) for b in range(1, B + 1))
+        self.value_ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=dev)
+
+    def _value_splits(self, B):
+        """K parts of the FFN value GEMM at batch B: enough 64x64-tile parts to give
+        the 256 CUs one workgroup each, each part at least 256 deep in K."""
+        C, F = self.cfg.n_embd, self.cfg.dim_ffn
+        tiles = -(-B // 64) * (capi.frag_pad(C) // 64)
+        splits = max(1, min(16, 256 // max(tiles, 1)))
+        while splits > 1 and capi.frag_pad(F) % (256 * splits):
+            splits //= 2
+        return splits
 
     def _step_frag(self, state, tokens, slots):
         cfg, m, s = self.cfg, self.model, self
@@ -277,7 +291,11 @@ class DecodeEngine:
             capi.add_layer_norm_mix(s.o[:B], res, state.ffn_shift[l], L["ln2_w"], L["ln2_b"], [L["x_k_ffn"]],
                                     res2, [s.xk_f], shift_slots=slots, frag=True)
             capi.frag_gemm([fp(s.xk_f, P["key"], s.act_f, B, F, C, epilogue=capi.EPI_RELU_SQUARE, c_frag=True)])
-            capi.frag_gemm([fp(s.act_f, P["value"], s.ffn, B, C, F)])
+            splits = self._value_splits(B)
+            if splits > 1:
+                capi.frag_gemm_splitk(fp(s.act_f, P["value"], s.ffn, B, C, F), splits, s.value_ws)
+            else:
+                capi.frag_gemm([fp(s.act_f, P["value"], s.ffn, B, C, F)])
             x, res_in = s.ffn[:B], res2
         capi.add_last_layer_norm(B, 1, C, x, res_in, m.ln_out_w, m.ln_out_b, s.h_f, frag=True)
         capi.frag_gemm([fp(s.h_f, s.p_head, s.logits, B, cfg.vocab, C)])
