@@ -351,6 +351,22 @@ VKWR_EXPORT int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint
                                                  uint16_t* x_out, uint16_t* const* out,
                                                  const int32_t* x_rows, const int32_t* shift_slots,
                                                  void* stream);
+
+/* vkwr_add_layer_norm_mix_frag_f16 whose x is the unreduced output of
+ * vkwr_frag_gemm_splitk_parts_f16: x[r, c] = fp16(sum over q < n_parts of
+ * x_parts[q * part_stride + r * C + c]), the parts added in q order -- the
+ * same values vkwr_frag_gemm_splitk_f16 would have stored, so the result is
+ * bit-identical to reducing first.  n_parts 2, 4 or 8; C % 128 == 0,
+ * C <= 4096; no x_rows gather.  No counterpart in the reference: it removes
+ * the reduce launch between the decode step's FFN value GEMM and the next
+ * layer's LayerNorm. */
+VKWR_EXPORT int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, const float* x_parts,
+                                                       int n_parts, int64_t part_stride,
+                                                       const uint16_t* residual, uint16_t* shift_state,
+                                                       const uint16_t* weight, const uint16_t* bias,
+                                                       int n_mix, const uint16_t* const* mix, float eps,
+                                                       uint16_t* x_out, uint16_t* const* out,
+                                                       const int32_t* shift_slots, void* stream);
 VKWR_EXPORT int vkwr_add_last_layer_norm_frag_f16(int B, int T, int C, const uint16_t* x,
                                                   const uint16_t* residual, const uint16_t* weight,
                                                   const uint16_t* bias, float eps, uint16_t* y,
@@ -431,6 +447,14 @@ VKWR_EXPORT int vkwr_frag_gemm_f16(int n_problems, const vkwr_frag_gemm_problem*
 VKWR_EXPORT int64_t vkwr_frag_gemm_splitk_workspace_bytes(int64_t m, int64_t n, int splits);
 VKWR_EXPORT int vkwr_frag_gemm_splitk_f16(const vkwr_frag_gemm_problem* problem, int splits,
                                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The first half of vkwr_frag_gemm_splitk_f16 alone: writes the `splits` fp32
+ * partial planes to workspace (plane q at q * roundup(m, 64) * frag_pad(n)
+ * floats, row stride frag_pad(n)) and leaves the reduction to a consumer that
+ * reads them (vkwr_add_layer_norm_mix_parts_frag_f16).  epilogue must be NONE,
+ * c_frag 0; c is not used.  No counterpart in the reference (see above). */
+VKWR_EXPORT int vkwr_frag_gemm_splitk_parts_f16(const vkwr_frag_gemm_problem* problem, int splits,
+                                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- token sampling (reference csrc/sampling/, ops vkwr_sampling::*) ----
  *

@@ -307,6 +307,36 @@ def test_ln_mix_frag_equals_packed_row_major(gpu):
         assert np.array_equal(frag_to_dense(f, rows, C)[:rows].view(np.uint16), o.cpu().numpy().view(np.uint16))
 
 
+@pytest.mark.parametrize("rows,C,K,splits,n_mix", [(128, 2048, 8192, 4, 6), (100, 2048, 4096, 8, 6),
+                                                   (64, 4096, 2048, 2, 1)])
+def test_ln_mix_parts_equals_reduce_then_ln(gpu, rows, C, K, splits, n_mix):
+    """vkwr_add_layer_norm_mix_parts_frag_f16 on the unreduced planes of
+    vkwr_frag_gemm_splitk_parts_f16 is bit-identical to
+    vkwr_frag_gemm_splitk_f16 followed by vkwr_add_layer_norm_mix_frag_f16."""
+    from vkwr_amd import capi
+    a, w = h(rows, K), h(C, K, scale=0.05)
+    pa, pw = pack(a, gpu, rows, K), pack(w, gpu, C, K)
+    res = dev(h(rows, C), gpu)
+    wt, bs = dev(h(C), gpu), dev(h(C), gpu)
+    mixes = [dev(rng.random(C).astype(np.float16), gpu) for _ in range(n_mix)]
+    shift0 = dev(h(rows, C), gpu)
+    s1, s2 = shift0.clone(), shift0.clone()
+    xo1, xo2 = torch.empty(rows, C, dtype=torch.float16, device=gpu), torch.empty(rows, C, dtype=torch.float16,
+                                                                                 device=gpu)
+    o1 = [capi.frag_empty(rows, C, gpu) for _ in range(n_mix)]
+    o2 = [capi.frag_empty(rows, C, gpu) for _ in range(n_mix)]
+    ws = torch.empty(capi.frag_splitk_workspace_bytes(rows, C, splits) // 4, dtype=torch.float32, device=gpu)
+    y = torch.empty(rows, C, dtype=torch.float16, device=gpu)
+    capi.frag_gemm_splitk(capi.frag_problem(pa, pw, y, rows, C, K), splits, ws)
+    capi.add_layer_norm_mix(y, res, s1, wt, bs, mixes, xo1, o1, frag=True)
+    ws.fill_(float("nan"))
+    capi.frag_gemm_splitk_parts(capi.frag_problem(pa, pw, y, rows, C, K), splits, ws)
+    capi.add_layer_norm_mix_parts(ws, splits, capi.splitk_plane_floats(rows, C), res, s2, wt, bs, mixes, xo2, o2)
+    assert torch.equal(xo1, xo2) and torch.equal(s1, s2)
+    for f1, f2 in zip(o1, o2):
+        assert torch.equal(f1, f2)
+
+
 def test_last_ln_and_groupnorm_frag_equal_packed_row_major(gpu):
     from vkwr_amd import capi
     B, T, C, H = 7, 3, 256, 4

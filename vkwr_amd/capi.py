@@ -74,6 +74,10 @@ _wkv_slots = _sig("vkwr_wkv7_fp32_forward_slots",
                   [_i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _frag_gemm = _sig("vkwr_frag_gemm_f16", [_i, ctypes.POINTER(FragProblem), _p])
 _frag_splitk = _sig("vkwr_frag_gemm_splitk_f16", [ctypes.POINTER(FragProblem), _i, _p, _i64, _p])
+_frag_splitk_parts = _sig("vkwr_frag_gemm_splitk_parts_f16", [ctypes.POINTER(FragProblem), _i, _p, _i64, _p])
+_ln_mix_parts = _sig("vkwr_add_layer_norm_mix_parts_frag_f16",
+                     [_i64, _i, _p, _i, _i64, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p,
+                      _p])
 _frag_splitk_ws = _sig("vkwr_frag_gemm_splitk_workspace_bytes", [_i64, _i64, _i], _i64)
 _frag_pack = _sig("vkwr_frag_pack_f16", [_i64, _i64, _p, _i, _p, _p])
 _frag_unpack = _sig("vkwr_frag_unpack_f16", [_i64, _i64, _p, _p, _p])
@@ -215,6 +219,32 @@ def frag_gemm_splitk(problem, splits, workspace):
     nbytes = workspace.numel() * workspace.element_size()
     _check(_frag_splitk(ctypes.byref(problem), splits, workspace.data_ptr(), nbytes, _stream()),
            "vkwr_frag_gemm_splitk_f16")
+
+
+def frag_gemm_splitk_parts(problem, splits, workspace):
+    """The partial planes of frag_gemm_splitk alone (epilogue NONE, row-major, c unused): plane q
+    starts at float q * splitk_plane_floats(m, n), row stride frag_pad(n)."""
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(_frag_splitk_parts(ctypes.byref(problem), splits, workspace.data_ptr(), nbytes, _stream()),
+           "vkwr_frag_gemm_splitk_parts_f16")
+
+
+def splitk_plane_floats(m, n):
+    """Floats between consecutive partial planes of a K-split frag GEMM."""
+    return (m + 63) // 64 * 64 * frag_pad(n)
+
+
+def add_layer_norm_mix_parts(x_parts, n_parts, part_stride, residual, shift_state, weight, bias, mixes, x_out,
+                             outs, eps=1e-5, shift_slots=None):
+    """add_layer_norm_mix(frag=True) whose x is n_parts fp32 K-part planes (x_parts, a CUDA float
+    tensor; plane stride part_stride floats, row stride C)."""
+    rows = x_out.shape[0]
+    C = x_out.shape[-1]
+    mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
+    op = (_p * len(outs))(*[o.data_ptr() for o in outs])
+    _check(_ln_mix_parts(rows, C, _ptr(x_parts), n_parts, part_stride, _ptr(residual), _ptr(shift_state),
+                         _ptr(weight), _ptr(bias), len(mixes), mp, eps, _ptr(x_out), op, _ptr(shift_slots),
+                         _stream()), "vkwr_add_layer_norm_mix_parts_frag_f16")
 
 
 def _arr_frag(problems):

@@ -463,7 +463,8 @@ namespace {
 
 // Validates one problem and fills its kernel descriptor (sizes, pointers,
 // epilogue); tiling fields are set by the caller.
-int fill_problem(const char* fn, int i, const vkwr_frag_gemm_problem& q, FProb& P, bool& empty) {
+int fill_problem(const char* fn, int i, const vkwr_frag_gemm_problem& q, FProb& P, bool& empty,
+                 bool need_c = true) {
   VK_REQUIRE(q.m >= 0 && q.n >= 0 && q.k >= 0, "%s: negative size in problem %d", fn, i);
   VK_REQUIRE(q.m <= (1 << 20) && q.n <= (1 << 24) && q.k <= (1 << 20), "%s: problem %d too large", fn, i);
   VK_REQUIRE(q.epilogue >= VKWR_GEMM_EPI_NONE && q.epilogue <= VKWR_FRAG_EPI_SIGMOID, "%s: bad epilogue", fn);
@@ -471,7 +472,7 @@ int fill_problem(const char* fn, int i, const vkwr_frag_gemm_problem& q, FProb& 
   empty = q.m == 0 || q.n == 0;
   if (empty) return VKWR_OK;
   VK_REQUIRE(q.k > 0, "%s: k == 0 in problem %d", fn, i);
-  VK_REQUIRE(q.a && q.b && q.c, "%s: null pointer in problem %d", fn, i);
+  VK_REQUIRE(q.a && q.b && (q.c || !need_c), "%s: null pointer in problem %d", fn, i);
   VK_REQUIRE(aligned16(q.a) && aligned16(q.b) && aligned16(q.c), "%s: operands must be 16-byte aligned", fn);
   if (q.c_frag) {
     VK_REQUIRE(q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL && q.epilogue != VKWR_GEMM_EPI_BIAS,
@@ -543,16 +544,15 @@ extern "C" int64_t vkwr_frag_gemm_splitk_workspace_bytes(int64_t m, int64_t n, i
   return (int64_t)splits * ((m + kSplitTile - 1) / kSplitTile * kSplitTile) * frag_pad(n) * (int64_t)sizeof(float);
 }
 
-extern "C" int vkwr_frag_gemm_splitk_f16(const vkwr_frag_gemm_problem* problem, int splits, void* workspace,
-                                         int64_t workspace_bytes, void* stream) {
-  clear_error();
-  const char* fn = "vkwr_frag_gemm_splitk_f16";
+namespace {
+
+// Validates a K-split problem and launches its partial-tile kernel.
+int splitk_partials(const char* fn, const vkwr_frag_gemm_problem* problem, int splits, void* workspace,
+                    int64_t workspace_bytes, bool need_c, FBatch& bt, bool& empty, hipStream_t stream) {
   VK_REQUIRE(problem != nullptr, "%s: null problem", fn);
   VK_REQUIRE(splits >= 1 && splits <= 16, "%s: splits must be in 1..16 (got %d)", fn, splits);
-  FBatch bt;
   bt.n = 1;
-  bool empty = false;
-  if (int e = fill_problem(fn, 0, *problem, bt.p[0], empty)) return e;
+  if (int e = fill_problem(fn, 0, *problem, bt.p[0], empty, need_c)) return e;
   if (empty) return VKWR_OK;
   FProb& P = bt.p[0];
   VK_REQUIRE(P.kpad % (kSplitKRound * splits) == 0, "%s: padded k (%d) must be a multiple of %d * splits", fn,
@@ -568,10 +568,38 @@ extern "C" int vkwr_frag_gemm_splitk_f16(const vkwr_frag_gemm_problem* problem, 
   P.ws = static_cast<float*>(workspace);
   P.ksplit = splits;
   const int wgs = (P.ncol * P.nmb * splits + 7) / 8 * 8;
-  hipLaunchKernelGGL((frag_gemm_kernel<2, 2, 8, 2, kStorePartial, false>), dim3(wgs), dim3(512), 0,
-                     (hipStream_t)stream, bt);
+  hipLaunchKernelGGL((frag_gemm_kernel<2, 2, 8, 2, kStorePartial, false>), dim3(wgs), dim3(512), 0, stream, bt);
+  return VKWR_OK;
+}
+
+}  // namespace
+
+extern "C" int vkwr_frag_gemm_splitk_f16(const vkwr_frag_gemm_problem* problem, int splits, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_frag_gemm_splitk_f16";
+  FBatch bt;
+  bool empty = false;
+  if (int e = splitk_partials(fn, problem, splits, workspace, workspace_bytes, true, bt, empty, (hipStream_t)stream))
+    return e;
+  if (empty) return VKWR_OK;
+  const FProb& P = bt.p[0];
   const int64_t threads = (int64_t)P.m * (P.npad / 4);
   hipLaunchKernelGGL(frag_splitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, P, P.nmb * kSplitTile);
   return check_launch(fn);
+}
+
+extern "C" int vkwr_frag_gemm_splitk_parts_f16(const vkwr_frag_gemm_problem* problem, int splits, void* workspace,
+                                               int64_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_frag_gemm_splitk_parts_f16";
+  VK_REQUIRE(problem != nullptr, "%s: null problem", fn);
+  VK_REQUIRE(problem->epilogue == VKWR_GEMM_EPI_NONE && problem->c_frag == 0,
+             "%s: the parts carry no epilogue (epilogue NONE, c_frag 0)", fn);
+  FBatch bt;
+  bool empty = false;
+  if (int e = splitk_partials(fn, problem, splits, workspace, workspace_bytes, false, bt, empty, (hipStream_t)stream))
+    return e;
+  return empty ? VKWR_OK : check_launch(fn);
 }

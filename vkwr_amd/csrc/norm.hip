@@ -43,6 +43,11 @@ struct LnArgs {
   const _Float16* mix[6];
   _Float16* out[6];
   int out_frag;  // y / out[] in frag layout (row blocks of 32, K = C; needs VW == 8)
+  // x given as the fp32 K-part planes of a split GEMM (vkwr_frag_gemm_splitk_parts_f16):
+  // x[row, c] = fp16(sum over q of x_parts[q * part_stride + row * C + c]), added in q order
+  const float* x_parts;
+  int64_t part_stride;
+  int n_parts;
 };
 
 template <bool kBf16>
@@ -57,7 +62,8 @@ __device__ __forceinline__ float ld_in(const void* p, int64_t i) {
 // VW: elements per lane access (8 = one 16-byte load, 1 = scalar); NV: accesses
 // per lane (VW * NV * 256 >= C); NMIX: 0 = plain LN output, 1 or 6 = decode
 // fusion with that many token-shift mix vectors.
-template <int VW, int NV, int NMIX, bool kBf16>
+// NP > 0: x comes as NP fp32 K-part planes (vector path only).
+template <int VW, int NV, int NMIX, bool kBf16, int NP = 0>
 __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
   __shared__ float red[kWaves];
   const int64_t row = blockIdx.x;
@@ -98,7 +104,24 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
   for (int n = 0; n < NV; ++n) {
     const int c0 = (tid + n * kThreads) * VW;
     if (c0 < C) {
-      if constexpr (kVec) {
+      if constexpr (kVec && NP > 0) {
+        // the split GEMM's epilogue: parts added in K order, rounded to fp16
+        const float* xp = p.x_parts + dst + c0;
+        f4 a0 = *reinterpret_cast<const f4*>(xp), a1 = *reinterpret_cast<const f4*>(xp + 4);
+#pragma unroll
+        for (int q = 1; q < NP; ++q) {
+          a0 += *reinterpret_cast<const f4*>(xp + q * p.part_stride);
+          a1 += *reinterpret_cast<const f4*>(xp + q * p.part_stride + 4);
+        }
+        const float xs[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[n][e] = (float)(_Float16)xs[e];
+        if (p.residual) {
+          const h8 rv = ld8(p.residual + rsrc + c0);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)rv.v[e];
+        }
+      } else if constexpr (kVec) {
         const h8 xv = ld8(reinterpret_cast<const _Float16*>(p.x) + src + c0);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[n][e] = (float)xv.v[e];
@@ -220,6 +243,24 @@ int launch_ln(const char* fn, const LnArgs& p, bool vec_ok, hipStream_t stream) 
   VK_REQUIRE(!p.out_frag || (vec_ok && p.C % kFragPad == 0),
              "%s: frag output needs C %% %d == 0 and 16-byte aligned rows", fn, kFragPad);
   const dim3 grid((unsigned)p.rows), block(kThreads);
+  if constexpr (NMIX > 0 && !kBf16) {
+    if (p.x_parts) {
+      VK_REQUIRE(vec_ok && p.C % kFragPad == 0 && p.C <= 4096,
+                 "%s: K-part input needs C %% %d == 0, C <= 4096 and 16-byte aligned rows", fn, kFragPad);
+      const bool one = p.C <= 8 * kThreads;
+#define VK_LN_PARTS(np)                                                                                  \
+  if (p.n_parts == np) {                                                                                 \
+    if (one) hipLaunchKernelGGL((layer_norm_kernel<8, 1, NMIX, false, np>), grid, block, 0, stream, p);  \
+    else hipLaunchKernelGGL((layer_norm_kernel<8, 2, NMIX, false, np>), grid, block, 0, stream, p);      \
+    return check_launch(fn);                                                                             \
+  }
+      VK_LN_PARTS(2)
+      VK_LN_PARTS(4)
+      VK_LN_PARTS(8)
+#undef VK_LN_PARTS
+      VK_REQUIRE(false, "%s: n_parts must be 2, 4 or 8 (got %d)", fn, p.n_parts);
+    }
+  }
   if (vec_ok && p.C % 8 == 0) {
     const int per = (p.C / 8 + kThreads - 1) / kThreads;  // 1..4
     if (per == 1) hipLaunchKernelGGL((layer_norm_kernel<8, 1, NMIX, kBf16>), grid, block, 0, stream, p);
@@ -322,7 +363,8 @@ namespace {
 int add_ln_mix(const char* fn, int64_t rows, int C, const uint16_t* x, const uint16_t* residual,
                uint16_t* shift_state, const uint16_t* weight, const uint16_t* bias, int n_mix,
                const uint16_t* const* mix, float eps, uint16_t* x_out, uint16_t* const* out,
-               const int32_t* x_rows, const int32_t* shift_slots, int frag, void* stream) {
+               const int32_t* x_rows, const int32_t* shift_slots, int frag, void* stream,
+               const float* x_parts = nullptr, int n_parts = 0, int64_t part_stride = 0) {
   VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
   VK_REQUIRE(mix && out, "%s: null pointer", fn);
   LnArgs p{};
@@ -339,15 +381,18 @@ int add_ln_mix(const char* fn, int64_t rows, int C, const uint16_t* x, const uin
   p.x_rows = x_rows;
   p.shift_slots = shift_slots;
   p.out_frag = frag;
-  bool vec = aligned16(x) && (!residual || aligned16(residual)) && aligned16(shift_state) &&
-             aligned16(x_out);
+  p.x_parts = x_parts;
+  p.n_parts = n_parts;
+  p.part_stride = part_stride;
+  bool vec = aligned16(x_parts ? (const void*)x_parts : (const void*)x) && (!residual || aligned16(residual)) &&
+             aligned16(shift_state) && aligned16(x_out);
   for (int i = 0; i < n_mix; ++i) {
     VK_REQUIRE(rows == 0 || (mix[i] && out[i]), "%s: null pointer", fn);
     p.mix[i] = reinterpret_cast<const _Float16*>(mix[i]);
     p.out[i] = reinterpret_cast<_Float16*>(out[i]);
     vec = vec && aligned16(out[i]);
   }
-  VK_REQUIRE(rows == 0 || (x && shift_state && weight && bias && x_out), "%s: null pointer", fn);
+  VK_REQUIRE(rows == 0 || ((x || x_parts) && shift_state && weight && bias && x_out), "%s: null pointer", fn);
   if (n_mix == 1) return launch_ln<1, false>(fn, p, vec, (hipStream_t)stream);
   return launch_ln<6, false>(fn, p, vec, (hipStream_t)stream);
 }
@@ -374,6 +419,20 @@ extern "C" int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint1
   clear_error();
   return add_ln_mix("vkwr_add_layer_norm_mix_frag_f16", rows, C, x, residual, shift_state, weight, bias,
                     n_mix, mix, eps, x_out, out, x_rows, shift_slots, 1, stream);
+}
+
+extern "C" int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, const float* x_parts, int n_parts,
+                                                      int64_t part_stride, const uint16_t* residual,
+                                                      uint16_t* shift_state, const uint16_t* weight,
+                                                      const uint16_t* bias, int n_mix, const uint16_t* const* mix,
+                                                      float eps, uint16_t* x_out, uint16_t* const* out,
+                                                      const int32_t* shift_slots, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_add_layer_norm_mix_parts_frag_f16";
+  VK_REQUIRE(rows == 0 || x_parts, "%s: null x_parts", fn);
+  VK_REQUIRE(part_stride >= rows * (int64_t)C, "%s: part_stride below rows * C", fn);
+  return add_ln_mix(fn, rows, C, nullptr, residual, shift_state, weight, bias, n_mix, mix, eps, x_out, out, nullptr,
+                    shift_slots, 1, stream, x_parts, n_parts, part_stride);
 }
 
 extern "C" int vkwr_add_f16(int64_t n, const uint16_t* x, const uint16_t* y, uint16_t* out,

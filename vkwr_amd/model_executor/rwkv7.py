@@ -247,16 +247,24 @@ class DecodeEngine:
         B = tokens.shape[0]
         C, H, F = cfg.n_embd, cfg.n_head, cfg.dim_ffn
         fp = capi.frag_problem
-        x, res_in = None, None
+        x, res_in, parts = None, None, 0
+        splits = self._value_splits(B)
+        # FFN value K parts reduced inside the next layer's LayerNorm (2, 4 or 8 parts)
+        parts_ok = splits in (2, 4, 8) and C % 128 == 0 and C <= 4096
         for l, L in enumerate(m.layers):
             first = l == 0
             P = s.pw[l]
             res = s.res[l % 2][:B]
             # ---- time mix
-            capi.add_layer_norm_mix(
-                m.emb if first else x, None if first else res_in, state.att_shift[l], L["ln1_w"], L["ln1_b"],
-                [L["x_r"], L["x_w"], L["x_k"], L["x_v"], L["x_a"], L["x_g"]], res, s.mixf,
-                x_rows=tokens if first else None, shift_slots=slots, frag=True)
+            mixes = [L["x_r"], L["x_w"], L["x_k"], L["x_v"], L["x_a"], L["x_g"]]
+            if parts:  # the previous layer's FFN value, still as K parts: reduced here
+                capi.add_layer_norm_mix_parts(s.value_ws, parts, capi.splitk_plane_floats(B, C), res_in,
+                                              state.att_shift[l], L["ln1_w"], L["ln1_b"], mixes, res, s.mixf,
+                                              shift_slots=slots)
+            else:
+                capi.add_layer_norm_mix(
+                    m.emb if first else x, None if first else res_in, state.att_shift[l], L["ln1_w"], L["ln1_b"],
+                    mixes, res, s.mixf, x_rows=tokens if first else None, shift_slots=slots, frag=True)
             xr, xw, xk, xv, xa, xg = s.mixf
             v_out = (s.v_first if first else s.v)[:B]
             probs = [fp(xr, P["Wr"], s.r, B, C, C), fp(xk, P["Wk"], s.k, B, C, C), fp(xv, P["Wv"], v_out, B, C, C),
@@ -291,8 +299,11 @@ class DecodeEngine:
             capi.add_layer_norm_mix(s.o[:B], res, state.ffn_shift[l], L["ln2_w"], L["ln2_b"], [L["x_k_ffn"]],
                                     res2, [s.xk_f], shift_slots=slots, frag=True)
             capi.frag_gemm([fp(s.xk_f, P["key"], s.act_f, B, F, C, epilogue=capi.EPI_RELU_SQUARE, c_frag=True)])
-            splits = self._value_splits(B)
-            if splits > 1:
+            parts = 0
+            if parts_ok and l + 1 < len(m.layers):
+                capi.frag_gemm_splitk_parts(fp(s.act_f, P["value"], s.ffn, B, C, F), splits, s.value_ws)
+                parts = splits
+            elif splits > 1:
                 capi.frag_gemm_splitk(fp(s.act_f, P["value"], s.ffn, B, C, F), splits, s.value_ws)
             else:
                 capi.frag_gemm([fp(s.act_f, P["value"], s.ffn, B, C, F)])
