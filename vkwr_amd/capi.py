@@ -73,6 +73,8 @@ _gn = _sig("vkwr_tmix_groupnorm_bonus_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p
 _wkv_slots = _sig("vkwr_wkv7_fp32_forward_slots",
                   [_i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _frag_gemm = _sig("vkwr_frag_gemm_f16", [_i, ctypes.POINTER(FragProblem), _p])
+_act = _sig("vkwr_activation_f16", [_i, _i64, _p, _p, _p])
+ACT_EW_TANH, ACT_EW_SIGMOID = 1, 2  # vkwr_activation_f16 codes
 _frag_splitk = _sig("vkwr_frag_gemm_splitk_f16", [ctypes.POINTER(FragProblem), _i, _p, _i64, _p])
 _frag_splitk_parts = _sig("vkwr_frag_gemm_splitk_parts_f16", [ctypes.POINTER(FragProblem), _i, _p, _i64, _p])
 _ln_mix_parts = _sig("vkwr_add_layer_norm_mix_parts_frag_f16",
@@ -205,6 +207,11 @@ def frag_gemm(problems):
     """Runs 1..8 frag GEMMs in one launch."""
     arr = _arr_frag(problems)
     _check(_frag_gemm(len(problems), arr, _stream()), "vkwr_frag_gemm_f16")
+
+
+def activation(act, x, out):
+    """out = act(x) elementwise (ACT_EW_TANH / ACT_EW_SIGMOID); out may be x."""
+    _check(_act(act, x.numel(), _ptr(x), _ptr(out), _stream()), "vkwr_activation_f16")
 
 
 def frag_splitk_workspace_bytes(m, n, splits):

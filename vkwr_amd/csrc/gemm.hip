@@ -52,6 +52,7 @@ struct Prob {
   int a_act;  // VKWR_GEMM_ACT_*
   int epi;    // VKWR_GEMM_EPI_*
   int vec;    // 16-byte accesses allowed (aligned rows, K and N multiples of 8)
+  int vec_out;  // 16-byte epilogue: c (and v, v_first, v0, ws when used) aligned, N a multiple of 8
   int tiles_m, tiles_n, splits, k_per_split;
   int tile_begin;
 };
@@ -116,8 +117,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(Batch bt) {
   constexpr int CA = (NA + 255) / 256;  // per lane
   constexpr int CB = (NB + 255) / 256;
   static_assert(TM >= 1 && TN >= 1 && CA >= 1 && CB >= 1, "tile shape");
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * kLdsK];
+  // One LDS block: the A and B stages during the K loop, then the fp32 output
+  // tile (half of it at a time) for the vector epilogue.
+  __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (BM + BN) * kLdsK];
+  auto& As = *reinterpret_cast<_Float16(*)[2][BM * kLdsK]>(smem);
+  auto& Bs = *reinterpret_cast<_Float16(*)[2][BN * kLdsK]>(smem + 2 * BM * kLdsK);
+  static_assert(BM / WM * BN * 4 <= 2 * (BM + BN) * kLdsK * 2, "epilogue staging must fit the stage buffers");
 
   // ---- locate problem / tile / split (workgroup-uniform)
   const int t = blockIdx.x;
@@ -236,7 +241,75 @@ __global__ __launch_bounds__(256) void gemm_kernel(Batch bt) {
     __syncthreads();
   }
 
-  // ---- epilogue
+  // ---- epilogue.  With 16-byte rows (P.vec_out) the accumulators go through LDS,
+  // one half of the tile (the waves of one wm) at a time, and each thread
+  // finishes 8 consecutive columns of a row with 16-byte loads and stores;
+  // written straight from the MFMA layout, every store would be 2 bytes per
+  // lane.  Same per-element arithmetic either way.
+  if (P.vec_out) {
+    constexpr int HR = BM / WM;  // rows per half
+    float* const stage = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int half = 0; half < WM; ++half) {
+      if (wm == half) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int rl = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+              stage[rl * BN + wn * (BN / WN) + j * 32 + (lane & 31)] = acc[i][j][r];
+            }
+      }
+      __syncthreads();
+      for (int g = tid; g < HR * BN / 8; g += 256) {
+        const int rl = g / (BN / 8), c8 = (g % (BN / 8)) * 8;
+        const int row = m0 + half * HR + rl, col = n0 + c8;
+        if (row >= P.m || col >= P.n) continue;
+        const float* sp = stage + rl * BN + c8;
+        const f4 lo = *reinterpret_cast<const f4*>(sp), hi = *reinterpret_cast<const f4*>(sp + 4);
+        const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const int64_t idx = (int64_t)row * P.n + col;
+        if (P.splits > 1) {
+          float* w = P.ws + (int64_t)split * P.m * P.n + idx;
+          *reinterpret_cast<f4*>(w) = lo;
+          *reinterpret_cast<f4*>(w + 4) = hi;
+          continue;
+        }
+        hv8 o;
+        if (P.epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+          const hv8 vv = *reinterpret_cast<const hv8*>(P.v + idx), vf = *reinterpret_cast<const hv8*>(P.vf + idx),
+                    v0 = *reinterpret_cast<const hv8*>(P.v0 + col);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = (float)vv[e];
+            float y = __builtin_fmaf((float)vf[e] - x, sigmoidf((float)v0[e] + s8[e]), x);
+            asm volatile("" : "+v"(y));
+            o[e] = (_Float16)y;
+          }
+        } else if (P.epi == VKWR_GEMM_EPI_BIAS) {
+          const hv8 v0 = *reinterpret_cast<const hv8*>(P.v0 + col);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float y = s8[e] + (float)v0[e];
+            asm volatile("" : "+v"(y));
+            o[e] = (_Float16)y;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float y = epilogue(P, s8[e], row, col + e);
+            asm volatile("" : "+v"(y));
+            o[e] = (_Float16)y;
+          }
+        }
+        *reinterpret_cast<hv8*>(P.c + idx) = o;
+      }
+      __syncthreads();
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -717,6 +790,10 @@ int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, C
     P.a_act = q.a_act;
     P.epi = q.epilogue;
     P.vec = aligned16(q.a) && aligned16(q.b) && q.k % 8 == 0 && (!P.b_kn || q.n % 8 == 0);
+    P.vec_out = aligned16(q.c) && q.n % 8 == 0 &&
+                (q.epilogue != VKWR_GEMM_EPI_VALUE_RESIDUAL ||
+                 (aligned16(q.v) && aligned16(q.v_first) && aligned16(q.v0))) &&
+                (q.epilogue != VKWR_GEMM_EPI_BIAS || aligned16(q.v0));
     if (!empty) {
       max_m = std::max(max_m, P.m);
       min_n = std::min(min_n, P.n);
@@ -763,6 +840,7 @@ extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, 
     if (P.splits > 1) {
       P.ws = ws;
       ws += (int64_t)P.splits * P.m * P.n;
+      if (!aligned16(P.ws)) P.vec_out = 0;
     }
   }
   int begin = 0;

@@ -81,14 +81,22 @@ class MixedEngine:
         return ps
 
     def _rank_out(self, L, R, first):
+        """The low-rank output GEMMs; tanh(w1) and sigmoid(g1) are applied by
+        _rank_act first (once per element: as an A-operand activation every
+        column tile of the GEMM recomputed them, 56 of the 103 us of g2 at the 7B
+        shape).  Same fp16 values as the A-operand form."""
         s, gp = self, capi.gemm_problem
-        ps = [gp(s.w1[:R], L["w2"], s.w[:R], a_act=capi.ACT_TANH, epilogue=capi.EPI_BIAS, v0=L["w0"]),
+        ps = [gp(s.w1[:R], L["w2"], s.w[:R], epilogue=capi.EPI_BIAS, v0=L["w0"]),
               gp(s.a1[:R], L["a2"], s.a12[:R]),
-              gp(s.g1[:R], L["g2"], s.g[:R], a_act=capi.ACT_SIGMOID)]
+              gp(s.g1[:R], L["g2"], s.g[:R])]
         if not first:
             ps.append(gp(s.v1[:R], L["v2"], s.v_new[:R], epilogue=capi.EPI_VALUE_RESIDUAL, v=s.v[:R],
                          v_first=s.v_first[:R], v0=L["v0"]))
         return ps
+
+    def _rank_act(self, R):
+        capi.activation(capi.ACT_EW_TANH, self.w1[:R], self.w1[:R])
+        capi.activation(capi.ACT_EW_SIGMOID, self.g1[:R], self.g1[:R])
 
     def _gemm_batches(self, R, nl):
         m, s, gp = self.model, self, capi.gemm_problem
@@ -143,6 +151,7 @@ class MixedEngine:
                 capi.token_shift(B, T, C, s.xx[r0:r0 + n], state.att_shift[l], mixes,
                                  [t[r0:r0 + n] for t in s.mix], shift_slots=slots)
             capi.gemm(self._proj(L, R, first), ws)
+            self._rank_act(R)
             capi.gemm(self._rank_out(L, R, first), ws)
             v = (s.v_first if first else s.v_new)[:R]
             capi.kk_a_gate(R, 1, C, H, s.k[:R], L["k_k"], L["a0"], s.a12[:R], L["k_a"], s.new_k[:R],
