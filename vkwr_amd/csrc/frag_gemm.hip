@@ -77,7 +77,12 @@ __device__ __forceinline__ float apply_act(int epi, float x) {
 // take: the generic path costs them about 0.8 us per launch.
 // kStorePartial writes the workgroup's fp32 tile of one K part to the split
 // workspace; frag_splitk_reduce_kernel adds the parts and applies the epilogue.
-constexpr int kStoreAny = 0, kStorePlain = 1, kStoreReluSqFrag = 2, kStorePartial = 3;
+// kStoreActFrag and kStoreRowMajor cover the decode step's two mixed batches
+// (projections: plain row-major or frag with none / tanh / sigmoid; low-rank
+// outputs: row-major with none / bias / value residual) without the other
+// paths' code.
+constexpr int kStoreAny = 0, kStorePlain = 1, kStoreReluSqFrag = 2, kStorePartial = 3, kStoreActFrag = 4,
+              kStoreRowMajor = 5;
 
 // W consecutive fp16 values, stored or loaded as one access.
 template <int W>
@@ -110,7 +115,7 @@ __device__ __forceinline__ void store_cols(const float (&s)[W], int row, int col
     *reinterpret_cast<hw*>(pc + (int64_t)row * n + col) = o;
     return;
   }
-  if (c_frag) {
+  if (kStore != kStoreRowMajor && c_frag) {
 #pragma unroll
     for (int e = 0; e < W; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
     *reinterpret_cast<hw*>(pc + frag_index(row, col, npad)) = o;
@@ -118,6 +123,12 @@ __device__ __forceinline__ void store_cols(const float (&s)[W], int row, int col
   }
   if (col >= n) return;
   const int64_t idx = (int64_t)row * n + col;
+  if constexpr (kStore == kStoreActFrag) {  // row-major outputs of this batch are plain
+#pragma unroll
+    for (int e = 0; e < W; ++e) o.v[e] = (_Float16)s[e];
+    *reinterpret_cast<hw*>(pc + idx) = o;
+    return;
+  }
   if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
     const hw vv = *reinterpret_cast<const hw*>(pv + idx), vf = *reinterpret_cast<const hw*>(pvf + idx),
              v0 = *reinterpret_cast<const hw*>(pv0 + col);
@@ -131,6 +142,9 @@ __device__ __forceinline__ void store_cols(const float (&s)[W], int row, int col
     const hw v0 = *reinterpret_cast<const hw*>(pv0 + col);
 #pragma unroll
     for (int e = 0; e < W; ++e) o.v[e] = (_Float16)(s[e] + (float)v0.v[e]);
+  } else if (kStore == kStoreRowMajor) {  // none (activations only come with frag outputs here)
+#pragma unroll
+    for (int e = 0; e < W; ++e) o.v[e] = (_Float16)s[e];
   } else {
 #pragma unroll
     for (int e = 0; e < W; ++e) o.v[e] = (_Float16)apply_act(epi, s[e]);
@@ -389,13 +403,23 @@ FragConfig pick_frag_config(const FBatch& bt) {
 // mod 8 is its XCD).
 template <int TM, int TN, int NW, int KS>
 void launch_cfg(const FBatch& bt, int wgs, hipStream_t s) {
-  bool relu_sq_frag = true, plain = true;
+  bool relu_sq_frag = true, plain = true, act_frag = true, row_major = true;
   for (int i = 0; i < bt.n; ++i) {
-    relu_sq_frag = relu_sq_frag && bt.p[i].c_frag && bt.p[i].epi == VKWR_GEMM_EPI_RELU_SQUARE;
-    plain = plain && !bt.p[i].c_frag && bt.p[i].epi == VKWR_GEMM_EPI_NONE;
+    const FProb& P = bt.p[i];
+    relu_sq_frag = relu_sq_frag && P.c_frag && P.epi == VKWR_GEMM_EPI_RELU_SQUARE;
+    plain = plain && !P.c_frag && P.epi == VKWR_GEMM_EPI_NONE;
+    act_frag = act_frag && (P.c_frag ? (P.epi == VKWR_GEMM_EPI_NONE || P.epi == VKWR_FRAG_EPI_TANH ||
+                                        P.epi == VKWR_FRAG_EPI_SIGMOID)
+                                     : P.epi == VKWR_GEMM_EPI_NONE);
+    row_major = row_major && !P.c_frag &&
+                (P.epi == VKWR_GEMM_EPI_NONE || P.epi == VKWR_GEMM_EPI_BIAS || P.epi == VKWR_GEMM_EPI_VALUE_RESIDUAL);
   }
   const dim3 grid(wgs), block(NW * 64);
-  if (bt.n > 1)
+  if (bt.n > 1 && act_frag)
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreActFrag, true>), grid, block, 0, s, bt);
+  else if (bt.n > 1 && row_major)
+    hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreRowMajor, true>), grid, block, 0, s, bt);
+  else if (bt.n > 1)
     hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreAny, true>), grid, block, 0, s, bt);
   else if (relu_sq_frag)
     hipLaunchKernelGGL((frag_gemm_kernel<TM, TN, NW, KS, kStoreReluSqFrag, false>), grid, block, 0, s, bt);
