@@ -575,7 +575,8 @@ __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
   if constexpr (kIlv) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      const f4 x = *reinterpret_cast<const f4*>(S + (q * kHead + lane) * 4);
+      // non-temporal: the state is not read again before the next decode step
+      const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4*>(S + (q * kHead + lane) * 4));
       s[4 * q + 0] = x.x;
       s[4 * q + 1] = x.y;
       s[4 * q + 2] = x.z;
