@@ -345,7 +345,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the WKV path shards by sequence with no communication; see DESIGN.md)", file=sys.stderr)
+              "(the WKV path shards by sequence with no communication between GPUs)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "no GPU visible"
     import vkwr_amd  # noqa: F401
