@@ -17,9 +17,15 @@
 //    (32 TM) x (32 TN) output tile over the whole of K; its NW waves take the
 //    16 KS-wide k blocks w, w + NW, ... with a two-deep register pipeline
 //    (loads are issued unconditionally inside the loop and the last blocks are
-//    peeled, so the compiler's wait counts stay exact), and the NW partial tiles are
-//    added through LDS in wave order after one barrier.  Deterministic, no
-//    second kernel, no fp32 partials in HBM.
+//    peeled, so the compiler's wait counts stay exact), and the NW partial
+//    tiles are added through LDS in wave order after one barrier.
+//    Deterministic, no second kernel, no fp32 partials in HBM.
+//
+//  * For long K (the FFN value, K = 4 C) the same kernel can instead give
+//    each workgroup one K part of a 64 x 64 tile and write its fp32 partial
+//    tile to a caller workspace (vkwr_frag_gemm_splitk_f16): each workgroup
+//    then reads half the activation bytes of the unsplit 32 x 32 form, and
+//    frag_splitk_reduce_kernel (or the consumer) adds the parts in K order.
 //
 // A launch runs up to 8 problems, each on its own range of workgroups.  When a
 // problem has several row tiles, the row tiles of one column tile are
