@@ -120,14 +120,14 @@ __global__ __launch_bounds__(256) void kk_a_gate_kernel(GateArgs p) {
   const int64_t idx = head * kHead + lane;
   const float kv = (float)p.k[idx];
   const float u = kv * (float)p.k_k[c];
-  const float total = wave_sum(u * u);
+  const float total = wave_sum_prod(u, u);
   const float inv = 1.0f / fmaxf(sqrtf(total), kKkEps);
   const float kk = u * inv;
   const float a = sigmoidf((float)p.a0[c] + (float)p.a12[idx]);
   const float ka = (float)p.k_a[c];
-  p.new_k[idx] = (_Float16)(kv * __builtin_fmaf(a, ka, 1.0f - ka));
+  p.new_k[idx] = f16_of(kv * __builtin_fmaf(a, ka, 1.0f - ka));
   p.neg_kk[idx] = (_Float16)(-kk);
-  p.kka[idx] = (_Float16)(kk * a);
+  p.kka[idx] = f16_of(kk * a);
   if (p.shift) p.shift[idx] = p.x[idx];  // T == 1: row (b,0) == b
 }
 
@@ -149,13 +149,110 @@ __global__ __launch_bounds__(256) void groupnorm_bonus_gate_kernel(GnArgs p) {
   const float xv = (float)p.x[idx];
   const float mean = wave_sum(xv) * (1.0f / 64.0f);
   const float d = xv - mean;
-  const float var = wave_sum(d * d) * (1.0f / 64.0f);
+  const float var = wave_sum_prod(d, d) * (1.0f / 64.0f);
   const float rstd = rsqrtf(var + kGroupNormEps);
-  const float rkv = wave_sum((float)p.r[idx] * (float)p.k[idx] * (float)p.r_k[c]);
+  const float rkv = wave_sum_prod((float)p.r[idx] * (float)p.k[idx], (float)p.r_k[c]);
   float y = __builtin_fmaf(d * rstd, (float)p.w[c], (float)p.b[c]);
   y = __builtin_fmaf(rkv, (float)p.v[idx], y);
   const int64_t o = p.out_frag ? frag_index(head / p.H, c, (int64_t)p.H * kHead) : idx;
-  p.out[o] = (_Float16)(y * (float)p.g[idx]);
+  p.out[o] = f16_of(y * (float)p.g[idx]);
+}
+
+// ---- 16-byte forms of the two kernels above: 8 lanes per (b, t, h), lane g of
+// the group holding channels 8g .. 8g + 7 (one 16-byte access per vector), 8
+// heads per wave.  head_sum8 adds the 64 channel values in exactly the
+// pairwise tree of wave_sum (xor 32, 16, 8, 4, 2, 1 over the channel index):
+// channel 8g + e pairs with lane g ^ 4, g ^ 2, g ^ 1 (same e), then with e ^ 4,
+// e ^ 2, e ^ 1 inside the lane, so the results are bit-identical to the
+// one-channel-per-lane kernels (and to the fused decode kernel).
+// The result is the group's lane 0 value, broadcast: with a fused first stage
+// the lanes' trees differ (each keeps its own products exact), and wave_sum
+// takes lane 0's.
+__device__ __forceinline__ float head_sum8_tail(float (&x)[8], int first_m) {
+#pragma unroll
+  for (int m = 4; m >= 1; m >>= 1)
+    if (m <= first_m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] += __shfl_xor(x[e], m, 64);
+  const float t = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
+  return __shfl(t, (int)(threadIdx.x & 56), 64);
+}
+__device__ __forceinline__ float head_sum8(float (&x)[8]) { return head_sum8_tail(x, 4); }
+// head_sum8 of a[e] * b[e] with the first stage fused as in wave_sum_prod
+__device__ __forceinline__ float head_sum8_prod(const float (&a)[8], const float (&b)[8]) {
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = __builtin_fmaf(a[e], b[e], __shfl_xor(a[e] * b[e], 4, 64));
+  return head_sum8_tail(x, 2);
+}
+
+__global__ __launch_bounds__(256) void kk_a_gate_vec_kernel(GateArgs p) {
+  const int64_t head = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const bool live = head < p.heads;
+  const int64_t hd = live ? head : p.heads - 1;  // dead lanes join the shuffles on a valid head
+  const int g = threadIdx.x & 7;
+  const int c0 = (int)(hd % p.H) * kHead + 8 * g;
+  const int64_t i0 = hd * kHead + 8 * g;
+  const h8 k8 = ld8(p.k + i0), kk8 = ld8(p.k_k + c0), a08 = ld8(p.a0 + c0), a128 = ld8(p.a12 + i0),
+           ka8 = ld8(p.k_a + c0);
+  float u[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) u[e] = (float)k8.v[e] * (float)kk8.v[e];
+  const float total = head_sum8_prod(u, u);
+  const float inv = 1.0f / fmaxf(sqrtf(total), kKkEps);
+  h8 nk, nkk, kka;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float kv = (float)k8.v[e];
+    const float kk = u[e] * inv;
+    const float a = sigmoidf((float)a08.v[e] + (float)a128.v[e]);
+    const float ka = (float)ka8.v[e];
+    nk.v[e] = f16_of(kv * __builtin_fmaf(a, ka, 1.0f - ka));
+    nkk.v[e] = (_Float16)(-kk);
+    kka.v[e] = f16_of(kk * a);
+  }
+  if (!live) return;
+  st8(p.new_k + i0, nk);
+  st8(p.neg_kk + i0, nkk);
+  st8(p.kka + i0, kka);
+  if (p.shift) st8(p.shift + i0, ld8(p.x + i0));  // T == 1: row (b,0) == b
+}
+
+__global__ __launch_bounds__(256) void groupnorm_bonus_gate_vec_kernel(GnArgs p) {
+  const int64_t head = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const bool live = head < p.heads;
+  const int64_t hd = live ? head : p.heads - 1;
+  const int g = threadIdx.x & 7;
+  const int c0 = (int)(hd % p.H) * kHead + 8 * g;
+  const int64_t i0 = hd * kHead + 8 * g;
+  const h8 x8 = ld8(p.x + i0), r8 = ld8(p.r + i0), k8 = ld8(p.k + i0), rk8 = ld8(p.r_k + c0);
+  float t[8], xv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) t[e] = xv[e] = (float)x8.v[e];
+  const float mean = head_sum8(t) * (1.0f / 64.0f);
+  float d[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) d[e] = xv[e] - mean;
+  const float var = head_sum8_prod(d, d) * (1.0f / 64.0f);
+  const float rstd = rsqrtf(var + kGroupNormEps);
+  float rk[8], rkc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    rk[e] = (float)r8.v[e] * (float)k8.v[e];
+    rkc[e] = (float)rk8.v[e];
+  }
+  const float rkv = head_sum8_prod(rk, rkc);
+  const h8 w8 = ld8(p.w + c0), b8 = ld8(p.b + c0), v8 = ld8(p.v + i0), g8 = ld8(p.g + i0);
+  h8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float y = __builtin_fmaf(d[e] * rstd, (float)w8.v[e], (float)b8.v[e]);
+    y = __builtin_fmaf(rkv, (float)v8.v[e], y);
+    o.v[e] = f16_of(y * (float)g8.v[e]);
+  }
+  if (!live) return;
+  const int64_t o0 = p.out_frag ? frag_index(hd / p.H, c0, (int64_t)p.H * kHead) : i0;
+  st8(p.out + o0, o);
 }
 
 __global__ __launch_bounds__(256) void vres_gate_kernel(int64_t n, int C, const _Float16* v,
@@ -305,9 +402,15 @@ extern "C" int vkwr_tmix_kk_a_gate_f16(int B, int T, int C, int H, const uint16_
              reinterpret_cast<const _Float16*>(k_a), reinterpret_cast<const _Float16*>(x),
              reinterpret_cast<_Float16*>(shift_state), reinterpret_cast<_Float16*>(new_k),
              reinterpret_cast<_Float16*>(neg_kk), reinterpret_cast<_Float16*>(kka)};
-  const int64_t blocks = (heads + 3) / 4;
+  const bool vec = aligned16(k) && aligned16(k_k) && aligned16(a0) && aligned16(a12) && aligned16(k_a) &&
+                   aligned16(new_k) && aligned16(neg_kk) && aligned16(kka) &&
+                   (!shift_state || (aligned16(shift_state) && aligned16(x)));
+  const int64_t blocks = vec ? (heads + 31) / 32 : (heads + 3) / 4;
   VK_REQUIRE(blocks <= 0x7fffffff, "%s: too many heads", fn);
-  hipLaunchKernelGGL(kk_a_gate_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
+  if (vec)
+    hipLaunchKernelGGL(kk_a_gate_vec_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(kk_a_gate_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
   return check_launch(fn);
 }
 
@@ -327,10 +430,16 @@ int groupnorm_bonus_gate(const char* fn, int B, int T, int C, int H, const uint1
            reinterpret_cast<const _Float16*>(bias), reinterpret_cast<const _Float16*>(g),
            reinterpret_cast<_Float16*>(out), frag};
   VK_REQUIRE(!frag || C % kFragPad == 0, "%s: frag output needs C %% %d == 0", fn, kFragPad);
-  const int64_t blocks = (heads + 3) / 4;
+  const bool vec = aligned16(x) && aligned16(r) && aligned16(k) && aligned16(v) && aligned16(r_k) &&
+                   aligned16(weight) && aligned16(bias) && aligned16(g) && aligned16(out);
+  const int64_t blocks = vec ? (heads + 31) / 32 : (heads + 3) / 4;
   VK_REQUIRE(blocks <= 0x7fffffff, "%s: too many heads", fn);
-  hipLaunchKernelGGL(groupnorm_bonus_gate_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, p);
+  if (vec)
+    hipLaunchKernelGGL(groupnorm_bonus_gate_vec_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(groupnorm_bonus_gate_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, p);
   return check_launch(fn);
 }
 }  // namespace

@@ -94,6 +94,26 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
+// fp16 of an fp32 value computed by a product: the value is first rounded to
+// fp32, then to fp16 (as a float -> half conversion of the product does), not
+// folded with the product into one mixed-precision FMA that rounds once.
+__device__ __forceinline__ _Float16 f16_of(float x) {
+  asm volatile("" : "+v"(x));
+  return (_Float16)x;
+}
+
+// wave_sum(a * b) with the first butterfly stage fused: each lane adds its
+// exact product to its xor-32 partner's rounded product, fma(a, b, partner).
+// Written out because that is what the compiler makes of wave_sum(a * b)
+// under fp contraction, and every kernel that reduces the same quantity (the
+// per-head kk norm, GroupNorm variance, the r.k bonus) must agree bit for bit.
+__device__ __forceinline__ float wave_sum_prod(float a, float b) {
+  float v = __builtin_fmaf(a, b, __shfl_xor(a * b, 32, 64));
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
 // Sum over a workgroup of NW waves (NW * 64 threads); `red` is NW floats of LDS.
 // Wave totals are added in wave order.  Contains two barriers: every thread of
 // the workgroup must call it.

@@ -557,16 +557,16 @@ __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
   const float kv = (float)p.k[tok], a12 = (float)p.a12[tok];
   // kk / a gate
   const float u = kv * (float)p.k_k[c];
-  const float inv = 1.0f / fmaxf(sqrtf(wave_sum(u * u)), kKkEps);
+  const float inv = 1.0f / fmaxf(sqrtf(wave_sum_prod(u, u)), kKkEps);
   const float kk = u * inv;
   const float a = sigmoidf((float)p.a0[c] + a12);
   const float ka = (float)p.k_a[c];
-  const _Float16 new_k = (_Float16)(kv * __builtin_fmaf(a, ka, 1.0f - ka));
+  const _Float16 new_k = f16_of(kv * __builtin_fmaf(a, ka, 1.0f - ka));
   const _Float16 neg_kk = (_Float16)(-kk);
-  const _Float16 kka = (_Float16)(kk * a);
+  const _Float16 kka = f16_of(kk * a);
   // The r.k bonus does not depend on the WKV output: reduce it now (a
   // wave-uniform scalar) so r and new_k need not stay live across the state phase.
-  const float rkv = wave_sum((float)xr * (float)new_k * (float)p.r_k[c]);
+  const float rkv = wave_sum_prod((float)xr * (float)new_k, (float)p.r_k[c]);
   // WKV-7 (the channel vectors go to LDS first: only v stays in a register
   // across the state load)
   token_stage(vb, lane, xr, xw, new_k, neg_kk, kka);
@@ -609,11 +609,11 @@ __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
   const float gv = (float)p.g[tok], lw = (float)p.ln_w[c], lb = (float)p.ln_b[c];
   const float mean = wave_sum(y) * (1.0f / 64.0f);
   const float d = y - mean;
-  const float var = wave_sum(d * d) * (1.0f / 64.0f);
+  const float var = wave_sum_prod(d, d) * (1.0f / 64.0f);
   const float rstd = rsqrtf(var + kGroupNormEps);
   float z = __builtin_fmaf(d * rstd, lw, lb);
   z = __builtin_fmaf(rkv, vi, z);
-  p.out[out_index()] = (_Float16)(z * gv);
+  p.out[out_index()] = f16_of(z * gv);
 }
 
 struct Fp16Args {
