@@ -621,14 +621,25 @@ __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan p
   const int i = blk >> 2, j = blk & 3;
   const int col = n0 + wn * 128 + j * 32 + lr;
   if (col >= P.n) return;
-  const float* base = pl.ws + (size_t)t * pl.parts * kBigTileElems;
+  // The 16 values of a part are loaded together (the workspace holds whole
+  // tiles, so rows past M are in bounds), then the parts are added in order.
+  const float* base = pl.ws + (size_t)t * pl.parts * kBigTileElems + (size_t)blk * 16 * 256 + tid;
+  float acc[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = base[r * 256];
+  for (int q = 1; q < pl.parts; ++q) {
+    const float* bq = base + (size_t)q * kBigTileElems;
+    float nx[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) nx[r] = bq[r * 256];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += nx[r];
+  }
+#pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
     if (row >= P.m) continue;
-    const size_t e = (size_t)(blk * 16 + r) * 256 + tid;
-    float acc = base[e];
-    for (int q = 1; q < pl.parts; ++q) acc += base[(size_t)q * kBigTileElems + e];
-    float y = big_epilogue<kEpi>(P, acc, row, col);
+    float y = big_epilogue<kEpi>(P, acc[r], row, col);
     asm volatile("" : "+v"(y));
     P.c[(int64_t)row * P.n + col] = (_Float16)y;
   }
