@@ -23,7 +23,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-import torch  # noqa: E402  (before vkwr_amd: shared HIP runtime)
+import torch  # noqa: E402  (before vkwr: shared HIP runtime)
 
 P_SLOTS, B_ACTIVE, H, HEAD = 512, 128, 32, 64
 C = H * HEAD
@@ -117,8 +117,8 @@ def model_decode(dev, steps, warmup=3, frag=True):
     weights) for 128 sequences at T=1 from a 160-slot state pool.  One step is captured
     into a HIP graph and replayed `steps` times (the recurrent state advances every
     replay); HIP events on the replay stream time it."""
-    from vkwr_amd.model_executor import DecodeEngine, RWKV7Config, RWKV7Model, RWKV7State
-    from vkwr_amd.model_executor.rwkv7 import flops_per_step, gbytes_per_step
+    from vkwr.model_executor import DecodeEngine, RWKV7Config, RWKV7Model, RWKV7State
+    from vkwr.model_executor.rwkv7 import flops_per_step, gbytes_per_step
 
     cfg = RWKV7Config.preset("1.5b")
     B = 128
@@ -171,7 +171,7 @@ def prefill_c2(dev, steps, warmup=2):
     (vkwr_v1_wkv::wkv_forward_slots_fp32 -> the row-split prefill kernel).  Inputs drawn as
     in config 0, resident in HBM; eager calls (each is hundreds of microseconds) bracketed
     by HIP events on the current stream."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     Bp, Tp = 8, 1024
     g = torch.Generator(device=dev).manual_seed(2)
@@ -218,7 +218,7 @@ def sampling_bs128(dev, calls, warmup=3):
     """Token sampling after the config-3 decode step: 128 rows of fp32 logits over the
     65536-token vocabulary, resident in HBM (vkwr_sampling ops, one 1024-lane workgroup
     per row).  Eager calls bracketed by HIP events on the current stream."""
-    from vkwr_amd._ops import sampling_ops as ops
+    from vkwr._ops import sampling_ops as ops
 
     Bs, Vs = 128, 65536
     g = torch.Generator(device=dev).manual_seed(5)
@@ -266,8 +266,8 @@ def serve_mixed_7b(dev, steps, warmup=1):
     (2304 GEMM rows) on a 2048-slot fp32 state pool.  Eager launches (shapes vary per
     step in serving); HIP events on the current stream."""
     from vkwr_amd import capi
-    from vkwr_amd.model_executor import MixedEngine, RWKV7Config, RWKV7Model, RWKV7State
-    from vkwr_amd.model_executor.mixed import gemm_flops
+    from vkwr.model_executor import MixedEngine, RWKV7Config, RWKV7Model, RWKV7State
+    from vkwr.model_executor.mixed import gemm_flops
 
     cfg = RWKV7Config.preset("7b")
     Bd, Bp, T, P = 256, 4, 512, 2048
@@ -348,8 +348,8 @@ def main():
               "(the WKV path shards by sequence with no communication between GPUs)", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "no GPU visible"
-    import vkwr_amd  # noqa: F401
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    import vkwr  # noqa: F401
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     dev = torch.device("cuda:0")
     K, W = args.steps, args.warmup

@@ -1,5 +1,5 @@
 """CPU oracle for the RWKV-7 hot path -- test infrastructure only.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
-may import this package.  The product (``vkwr_amd``) never does.
+may import this package.  The product (``vkwr``, ``vkwr_amd``) never does.
 """

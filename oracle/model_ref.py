@@ -1,7 +1,7 @@
 """End-to-end oracle of the RWKV-7 decode step -- test infrastructure only.
 
 A plain torch float32 restatement of the layer composition that
-vkwr_amd.model_executor.rwkv7 runs on the HIP kernels (the reference ships no
+vkwr.model_executor.rwkv7 runs on the HIP kernels (the reference ships no
 model code; the composition follows its op contracts, see that module's
 docstring).  Runs on any torch device.  With round_fp16=True every op output
 is rounded to fp16 where the GPU path stores fp16, so the comparison isolates
@@ -26,7 +26,7 @@ def _ln(x, w, b, eps=1e-5):
 
 
 def decode_step(model, wkv, att_shift, ffn_shift, tokens, slots, round_fp16=True):
-    """model: vkwr_amd.model_executor.rwkv7.RWKV7Model (fp16 weights, converted here);
+    """model: vkwr.model_executor.rwkv7.RWKV7Model (fp16 weights, converted here);
     tokens, slots: int tensors [B].  Returns float32 logits [B, V]."""
     cfg = model.cfg
     dev = wkv.device

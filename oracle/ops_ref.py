@@ -2,7 +2,7 @@
 gate / activation ops of the RWKV-7 hot path -- test infrastructure only.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
-may use this module; the product (``vkwr_amd``) never does.
+may use this module; the product (``vkwr``, ``vkwr_amd``) never does.
 
 Each function restates the arithmetic of the reference kernel it names (paths
 relative to the reference root) in float64 and rounds to fp16 at the points

@@ -1,7 +1,7 @@
 """CPU oracle (numpy) for token sampling -- test infrastructure only.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
-may use this module; the product (``vkwr_amd``) never does.
+may use this module; the product (``vkwr``, ``vkwr_amd``) never does.
 
 Restates the reference's sampling kernels (csrc/sampling/sampling.cu; paths
 relative to the reference root) one batch row at a time:

@@ -4,7 +4,7 @@
  * This file restates, on the CPU, the arithmetic of the reference's WKV-7
  * kernels (szxysdt/VKWR).  It is the checker that the HIP kernels of this
  * repository are compared against, and the "reference CPU path" that bench.py
- * times as a baseline.  Nothing in the product (vkwr_amd/) links, imports or
+ * times as a baseline.  Nothing in the product (vkwr/, vkwr_amd/) links, imports or
  * calls it; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
  * load it.
  *

@@ -18,5 +18,5 @@ def pytest_configure(config):
 def gpu():
     """GPU tests fail (not skip) without a GPU: they are run only on the GPU box."""
     assert torch.cuda.is_available(), "GPU test run without a visible GPU"
-    import vkwr_amd  # noqa: F401  (loads the extension modules; raises if absent)
+    import vkwr  # noqa: F401  (loads the extension modules; raises if absent)
     return torch.device("cuda:0")

@@ -47,7 +47,7 @@ GEMM_SHAPES = [  # (M, K, N)
 @pytest.mark.parametrize("M,K,N", GEMM_SHAPES)
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_gemm_vs_oracle(gpu, M, K, N, layout):
-    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    from vkwr._ops.v1 import v1_linear_ops as L
     a = h(M, K)
     w = h(N, K, scale=0.05) if layout == "nk" else h(K, N, scale=0.05)
     y = (L.linear_f16_orig if layout == "nk" else L.linear_f16)(dev(a, gpu), dev(w, gpu))
@@ -58,7 +58,7 @@ def test_gemm_vs_oracle(gpu, M, K, N, layout):
 
 def test_gemm_deterministic_and_split_k(gpu):
     """Small-M shapes take the K-split path; results are run-to-run identical."""
-    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    from vkwr._ops.v1 import v1_linear_ops as L
     a, w = dev(h(128, 8192), gpu), dev(h(2048, 8192, scale=0.02), gpu)
     y1 = L.linear_f16_orig(a, w)
     y2 = L.linear_f16_orig(a, w)
@@ -68,7 +68,7 @@ def test_gemm_deterministic_and_split_k(gpu):
 
 
 def test_all_linear_ops_compute_the_same_function(gpu):
-    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    from vkwr._ops.v1 import v1_linear_ops as L
     B, T, K, N = 2, 3, 256, 512
     x = dev(h(B, T, K), gpu)
     w_kn = dev(h(K, N, scale=0.05), gpu)
@@ -94,7 +94,7 @@ def test_all_linear_ops_compute_the_same_function(gpu):
 
 
 def test_linear_validation_errors(gpu):
-    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    from vkwr._ops.v1 import v1_linear_ops as L
     K, N = 128, 256
     x = dev(h(2, 4, K), gpu)
     w = dev(h(K, N), gpu)
@@ -128,7 +128,7 @@ def test_linear_validation_errors(gpu):
 
 @pytest.mark.parametrize("act", [1, 2])
 def test_linear_t_act_and_vres(gpu, act):
-    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    from vkwr._ops.v1 import v1_linear_ops as L
     M, K, N = 4, 96, 2048
     x, w = h(M, K), h(N, K, scale=0.1)
     y = L.linear_t_act_f16(dev(x, gpu), dev(w, gpu), act)
@@ -142,7 +142,7 @@ def test_linear_t_act_and_vres(gpu, act):
 
 def test_linear_reference_unit_tests(gpu):
     """reference tests/ops/test_v1_linear_ops.py: shapes, NaN, zero input, vs torch.matmul."""
-    from vkwr_amd._ops.v1 import v1_linear_ops as L
+    from vkwr._ops.v1 import v1_linear_ops as L
     for B, T, K, N in [(1, 1, 64, 128), (2, 4, 128, 256), (1, 16, 256, 512), (4, 8, 512, 1024)]:
         x = torch.randn(B, T, K, dtype=torch.float16, device=gpu)
         w = torch.randn(K, N, dtype=torch.float16, device=gpu)
@@ -167,7 +167,7 @@ def test_linear_reference_unit_tests(gpu):
 @pytest.mark.parametrize("M,C,ranks", [(128, 2048, (96, 96, 256, 64)), (3, 256, (32, 16, 64, 8)),
                                        (1, 4096, (128, 128, 480, 96))])
 def test_rank_in_out(gpu, M, C, ranks):
-    from vkwr_amd._ops.v1 import v1_rank_ops as K
+    from vkwr._ops.v1 import v1_rank_ops as K
     Rw, Ra, Rg, Rv = ranks
     xs = [h(M, C) for _ in range(4)]
     w1s = [h(r, C, scale=0.02) for r in ranks]
@@ -196,7 +196,7 @@ def test_rank_in_out(gpu, M, C, ranks):
 
 
 def test_rank_validation_errors(gpu):
-    from vkwr_amd._ops.v1 import v1_rank_ops as K
+    from vkwr._ops.v1 import v1_rank_ops as K
     M, C = 2, 128
     x = dev(h(M, C), gpu)
     w = dev(h(16, C), gpu)
@@ -210,7 +210,7 @@ def test_rank_validation_errors(gpu):
 
 @pytest.mark.parametrize("B,T,C,F", [(1, 1, 256, 256), (2, 8, 256, 512), (128, 1, 2048, 8192), (1, 4, 512, 1024)])
 def test_cmix_sparse(gpu, B, T, C, F):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     x, shift0 = h(B, T, C), h(B, C)
     x_k = rng.random(C).astype(np.float16)
     key, value = h(F, C, scale=0.05), h(F, C, scale=0.05)
@@ -229,7 +229,7 @@ def test_cmix_sparse(gpu, B, T, C, F):
 
 
 def test_cmix_down_ops(gpu):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     B, T, C, F = 2, 3, 512, 1024
     pre = h(B, T, F)
     value = h(F, C, scale=0.05)

@@ -1,4 +1,4 @@
-"""End-to-end RWKV-7 decode step (vkwr_amd.model_executor) against the
+"""End-to-end RWKV-7 decode step (vkwr.model_executor) against the
 float32 composition oracle (oracle/model_ref.py).
 
 Bar (north_star): end-to-end logits within max-abs 5e-2 of the float32 model;
@@ -27,7 +27,7 @@ STATE_TOL = 1e-3
 
 def _setup(gpu, preset, B, P, seed=0, frag=True):
     from vkwr_amd import capi
-    from vkwr_amd.model_executor import RWKV7Config, RWKV7Model, RWKV7State, DecodeEngine
+    from vkwr.model_executor import RWKV7Config, RWKV7Model, RWKV7State, DecodeEngine
     cfg = RWKV7Config.preset(preset)
     model = RWKV7Model(cfg, gpu, seed=seed)
     layout = capi.WKV_STATE_ILV if frag else capi.WKV_STATE_STD

@@ -51,14 +51,14 @@ def close_ulp(got, ref, ulps=1, min_equal=0.99, what="", atol=ATOL):
 
 @pytest.mark.parametrize("rows,C", [(1, 64), (16, 2048), (128, 2048), (7, 4096), (3, 8192), (5, 77), (4, 1000)])
 def test_layer_norm(gpu, rows, C):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     x, w, b = h(rows, C, scale=2.0), h(C), h(C)
     y = N.layer_norm_f16(dev(x, gpu), dev(w, gpu), dev(b, gpu))
     close_ulp(y, R.layer_norm(x, w, b)[1], what=f"ln {rows}x{C}")
 
 
 def test_layer_norm_misaligned_view_uses_scalar_path(gpu):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     C = 256
     big = h(4 * C + 1)
     x = dev(big, gpu)[1:].view(4, C)  # 2-byte offset: not 16-byte aligned
@@ -69,7 +69,7 @@ def test_layer_norm_misaligned_view_uses_scalar_path(gpu):
 
 @pytest.mark.parametrize("shape", [(2, 8, 512), (128, 1, 2048), (3, 5, 130)])
 def test_add_layer_norm(gpu, shape):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     C = shape[-1]
     x, r, w, b = h(*shape, scale=3.0), h(*shape, scale=3.0), h(C), h(C)
     x_out, y = N.add_layer_norm_f16(dev(x, gpu), dev(r, gpu), dev(w, gpu), dev(b, gpu))
@@ -80,7 +80,7 @@ def test_add_layer_norm(gpu, shape):
 
 @pytest.mark.parametrize("B,T,C", [(1, 1, 2048), (4, 3, 4096), (2, 5, 66)])
 def test_add_last_layer_norm(gpu, B, T, C):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     x, r, w, b = h(B, T, C), h(B, T, C), h(C), h(C)
     y = N.add_last_layer_norm_f16(dev(x, gpu), dev(r, gpu), dev(w, gpu), dev(b, gpu))
     assert y.shape == (B, C)
@@ -88,7 +88,7 @@ def test_add_last_layer_norm(gpu, B, T, C):
 
 
 def test_emb_ln0(gpu):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     V, C = 64, 2048
     e = torch.randn(V, C).to(torch.bfloat16)
     w = torch.randn(C).to(torch.bfloat16)
@@ -99,7 +99,7 @@ def test_emb_ln0(gpu):
 
 
 def test_add_f16(gpu):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     for shape in [(4, 1024), (3, 7, 2)]:
         x, y = h(*shape), h(*shape)
         close_ulp(N.add_f16(dev(x, gpu), dev(y, gpu)), R.add16(x, y), ulps=0.5, min_equal=1.0, atol=0)
@@ -109,7 +109,7 @@ def test_add_f16(gpu):
 
 @pytest.mark.parametrize("n_mix,B,C", [(6, 128, 2048), (1, 128, 2048), (6, 4, 4096), (1, 3, 4096), (6, 2, 130)])
 def test_add_layer_norm_mix(gpu, n_mix, B, C):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     x, r, w, b = h(B, 1, C, scale=2.0), h(B, 1, C, scale=2.0), h(C), h(C)
     shift0 = h(B, C)
     mixes = [(rng.random(C)).astype(np.float16) for _ in range(n_mix)]
@@ -131,7 +131,7 @@ def test_add_layer_norm_mix(gpu, n_mix, B, C):
 
 def test_add_layer_norm_mix_variants_agree(gpu):
     """_cfg and _scalar_stats (C=4096 only) compute the same function."""
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     B, C = 3, 4096
     x, r, w, b = (dev(a, gpu) for a in (h(B, 1, C), h(B, 1, C), h(C), h(C)))
     mixes = [dev(rng.random(C).astype(np.float16), gpu) for _ in range(6)]
@@ -153,7 +153,7 @@ def test_add_layer_norm_mix_variants_agree(gpu):
 
 
 def test_norm_validation_errors(gpu):
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     C = 10000
     x = torch.randn(1, 1, C, dtype=torch.float16, device=gpu)
     with pytest.raises(RuntimeError):
@@ -178,7 +178,7 @@ def test_norm_validation_errors(gpu):
 
 def test_norm_reference_unit_tests(gpu):
     """reference tests/ops/test_v1_norm_ops.py: shapes, dtype, 1-D input, NaN."""
-    from vkwr_amd._ops.v1 import v1_norm_ops as N
+    from vkwr._ops.v1 import v1_norm_ops as N
     for B, T, C in [(1, 1, 64), (2, 8, 256), (1, 16, 1024), (4, 4, 4096)]:
         x = torch.randn(B, T, C, dtype=torch.float16, device=gpu)
         w, b = torch.randn(C, dtype=torch.float16, device=gpu), torch.randn(C, dtype=torch.float16, device=gpu)
@@ -198,7 +198,7 @@ def test_norm_reference_unit_tests(gpu):
 
 @pytest.mark.parametrize("n_mix,B,T,C", [(6, 128, 1, 2048), (6, 2, 40, 256), (1, 3, 17, 4096), (1, 2, 3, 70), (6, 1, 1, 4096)])
 def test_token_shift(gpu, n_mix, B, T, C):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     x, shift0 = h(B, T, C), h(B, C)
     mixes = [rng.random(C).astype(np.float16) for _ in range(n_mix)]
     shift = dev(shift0, gpu)
@@ -215,7 +215,7 @@ def test_token_shift(gpu, n_mix, B, T, C):
 
 def test_token_shift_prev_is_entry_value_for_long_prefill(gpu):
     """T > 1: every sequence's t = 0 output uses shift_state as it was at entry."""
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     B, T, C = 64, 300, 512
 
     def unit_range(*shape):  # |values| in [0.5, 2): prev - cur is exact in fp32
@@ -233,7 +233,7 @@ def test_token_shift_prev_is_entry_value_for_long_prefill(gpu):
 
 @pytest.mark.parametrize("half_math", [False, True])
 def test_tmix_mix6_t1_c4096(gpu, half_math):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     B, C = 5, 4096
     x, shift0 = h(B, 1, C), h(B, C)
     mixes = [rng.random(C).astype(np.float16) for _ in range(6)]
@@ -247,7 +247,7 @@ def test_tmix_mix6_t1_c4096(gpu, half_math):
 
 
 def test_mix_validation_errors(gpu):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     B, T, C = 1, 2, 63
     x = torch.randn(B, T, C, dtype=torch.float16, device=gpu)
     s = torch.zeros(B, C, dtype=torch.float16, device=gpu)
@@ -284,7 +284,7 @@ def test_mix_validation_errors(gpu):
 
 @pytest.mark.parametrize("B,T,H", [(128, 1, 32), (2, 4, 4), (1, 1, 1)])
 def test_kk_a_gate(gpu, B, T, H):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     C = 64 * H
     k, a12 = h(B, T, C), h(B, T, C)
     k_k, a0, k_a = h(C), h(C), h(C)
@@ -294,7 +294,7 @@ def test_kk_a_gate(gpu, B, T, H):
 
 
 def test_kk_a_gate_update_shift(gpu):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     B, H = 4, 2
     C = 64 * H
     k, a12, x = h(B, 1, C), h(B, 1, C), h(B, 1, C)
@@ -308,7 +308,7 @@ def test_kk_a_gate_update_shift(gpu):
 
 @pytest.mark.parametrize("B,T,H", [(128, 1, 32), (2, 4, 4), (1, 1, 1)])
 def test_groupnorm_bonus_gate(gpu, B, T, H):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     C = 64 * H
     x, r, k, v, g = (h(B, T, C) for _ in range(5))
     r_k, w, b = h(C), h(C), h(C)
@@ -320,7 +320,7 @@ def test_groupnorm_bonus_gate(gpu, B, T, H):
 
 
 def test_vres_gate_and_elementwise(gpu):
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     B, T, C = 3, 5, 256
     v, vf, v12, v0 = h(B, T, C), h(B, T, C), h(B, T, C), h(C)
     close_ulp(M.tmix_vres_gate(B, T, C, *(dev(a, gpu) for a in (v, vf, v0, v12))), R.vres_gate(v, vf, v0, v12),
@@ -340,7 +340,7 @@ def test_vres_gate_and_elementwise(gpu):
 
 def test_mix_reference_unit_tests(gpu):
     """reference tests/ops/test_v1_mix_ops.py: shapes, return counts, NaN, mutation."""
-    from vkwr_amd._ops.v1 import v1_mix_ops as M
+    from vkwr._ops.v1 import v1_mix_ops as M
     for B, T, C in [(1, 1, 64), (2, 8, 256), (1, 16, 4096)]:
         x = torch.randn(B, T, C, dtype=torch.float16, device=gpu)
         s = torch.randn(B, C, dtype=torch.float16, device=gpu)

@@ -12,9 +12,9 @@ import os
 import pytest
 import torch
 
-import vkwr_amd  # noqa: F401
-from vkwr_amd._ops import rwkv7_ops
-from vkwr_amd._ops.v1 import v1_wkv_ops
+import vkwr  # noqa: F401
+from vkwr._ops import rwkv7_ops
+from vkwr._ops.v1 import v1_wkv_ops
 
 # Reference interface data for the other namespaces (see tests/golden/README.md).
 _IFACE = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "ref_interface.json")))
@@ -109,7 +109,7 @@ def _iface_wrappers():
 def test_wrapper_signature_iface(modname, name, params):
     if name in PENDING:
         pytest.skip(f"{name} not built yet")
-    mod = importlib.import_module(f"vkwr_amd._ops.v1.{modname}")
+    mod = importlib.import_module(f"vkwr._ops.v1.{modname}")
     assert ", ".join(inspect.signature(getattr(mod, name)).parameters) == params
 
 
@@ -136,7 +136,7 @@ def test_cpu_tensors_rejected_by_dispatcher():
 
 
 def test_sampling_wrappers():
-    from vkwr_amd._ops import sampling_ops
+    from vkwr._ops import sampling_ops
 
     assert sampling_ops.STATE_BYTES == 32
     for name, params in {"setup_rand": "seed, B",

@@ -23,7 +23,7 @@ MARGIN = 1e-5
 
 
 def _ops():
-    from vkwr_amd._ops import sampling_ops
+    from vkwr._ops import sampling_ops
     return sampling_ops
 
 

@@ -1,4 +1,4 @@
-"""GPU tests of the mixed prefill + decode step (vkwr_amd.model_executor.mixed)
+"""GPU tests of the mixed prefill + decode step (vkwr.model_executor.mixed)
 and the continuous-batching scheduler (scheduler.py) on the tiny RWKV-7 shape.
 
 Bar: a prefill chunk of T tokens gives the last-token logits and recurrent
@@ -21,7 +21,7 @@ TOL = 5e-2
 
 def _tiny(gpu, n_slots, seed=0):
     from vkwr_amd import capi
-    from vkwr_amd.model_executor import RWKV7Config, RWKV7Model, RWKV7State
+    from vkwr.model_executor import RWKV7Config, RWKV7Model, RWKV7State
     cfg = RWKV7Config.preset("tiny")
     model = RWKV7Model(cfg, gpu, seed=seed)
     state = RWKV7State(cfg, n_slots, gpu, std=0.1, seed=seed + 1, layout=capi.WKV_STATE_STD)
@@ -40,7 +40,7 @@ def _i32(x, gpu):
 
 
 def test_decode_rows_match_decode_engine(gpu):
-    from vkwr_amd.model_executor import DecodeEngine, MixedEngine
+    from vkwr.model_executor import DecodeEngine, MixedEngine
     cfg, model, state = _tiny(gpu, 12)
     s2 = _clone(state)
     g = torch.Generator().manual_seed(3)
@@ -55,7 +55,7 @@ def test_decode_rows_match_decode_engine(gpu):
 
 @pytest.mark.parametrize("T", [1, 5, 16])
 def test_prefill_chunk_equals_decode_steps(gpu, T):
-    from vkwr_amd.model_executor import DecodeEngine, MixedEngine
+    from vkwr.model_executor import DecodeEngine, MixedEngine
     cfg, model, state = _tiny(gpu, 6)
     s2 = _clone(state)
     g = torch.Generator().manual_seed(T)
@@ -73,7 +73,7 @@ def test_prefill_chunk_equals_decode_steps(gpu, T):
 
 
 def test_mixed_groups_equal_separate_steps(gpu):
-    from vkwr_amd.model_executor import MixedEngine
+    from vkwr.model_executor import MixedEngine
     cfg, model, state = _tiny(gpu, 16)
     g = torch.Generator().manual_seed(9)
     dec = (torch.randint(0, cfg.vocab, (4,), generator=g).to(torch.int32).to(gpu), _i32([0, 1, 2, 3], gpu))
@@ -92,7 +92,7 @@ def test_mixed_groups_equal_separate_steps(gpu):
 def test_scheduler_matches_teacher_forced_replay(gpu):
     """12 requests, prompts 1..23 tokens (chunk 8, so up to three chunks), budgets 1..6 tokens,
     only 5 slots: admission waits for slots, slots are recycled and reset."""
-    from vkwr_amd.model_executor import ContinuousBatcher, DecodeEngine, MixedEngine
+    from vkwr.model_executor import ContinuousBatcher, DecodeEngine, MixedEngine
     cfg, model, state = _tiny(gpu, 5)
     g = torch.Generator().manual_seed(11)
     eng = MixedEngine(model, 48, max_seqs=16)
@@ -107,7 +107,7 @@ def test_scheduler_matches_teacher_forced_replay(gpu):
     assert sched.slots.available == 5
     # replay each request alone on a fresh slot, teacher-forced with the scheduler's tokens
     from vkwr_amd import capi
-    from vkwr_amd.model_executor import RWKV7State
+    from vkwr.model_executor import RWKV7State
     ref_state = RWKV7State(cfg, 1, gpu, std=0.0, layout=capi.WKV_STATE_STD)
     dec = DecodeEngine(model, 1, frag=False)
     slot = _i32([0], gpu)
@@ -124,7 +124,7 @@ def test_scheduler_matches_teacher_forced_replay(gpu):
 def test_scheduler_with_gpu_sampler(gpu):
     """The scheduler with the GPU sampler: top_k = 1 reproduces the greedy run token for
     token; temperature sampling with one seed is reproducible and stays in the vocabulary."""
-    from vkwr_amd.model_executor import ContinuousBatcher, GpuSampler, MixedEngine
+    from vkwr.model_executor import ContinuousBatcher, GpuSampler, MixedEngine
 
     def run(sample):
         cfg, model, state = _tiny(gpu, 4)

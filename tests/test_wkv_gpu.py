@@ -74,7 +74,7 @@ def _order(mode, T):
 def test_fp32_dense_matches_oracle(gpu, mode, B, T, H, dist, std):
     if mode != "wkv_forward_fp32" and T > 16:
         pytest.skip("large case runs once, under the default mode")
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     C = H * 64
     ins = make_wkv_inputs(B, T, H, seed=B * 100 + T, dist=dist)
@@ -93,7 +93,7 @@ def test_fp32_dense_matches_oracle(gpu, mode, B, T, H, dist, std):
 
 def test_slots_config1_steps_match_oracle(gpu):
     """BASELINE config 1 at full size: pool 512 x H=32, 128 distinct slots, 3 decode steps."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     P, B, H = 512, 128, 32
     C = H * 64
@@ -113,7 +113,7 @@ def test_slots_config1_steps_match_oracle(gpu):
 
 def test_slots_equal_gather_dense_scatter(gpu):
     """Fused slot op == index_select -> wkv_forward_fp32 -> index_copy_, bitwise, T=3."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     P, B, T, H = 40, 9, 3, 4
     C = H * 64
@@ -145,7 +145,7 @@ def test_slots_out_of_range_is_skipped(gpu):
     untouched = [0, 2, 3, 5, 6, 7]
     assert torch.equal(pool[untouched], before[untouched])
     with pytest.raises(RuntimeError):
-        from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+        from vkwr._ops.v1 import v1_wkv_ops as ops
         ops.wkv_forward_slots_fp32(B, 1, C, H, pool, slots, *ins, validate=True)
 
 
@@ -213,7 +213,7 @@ def test_state_layout_round_trip_and_definition(gpu):
 
 def test_prefill_config2_reduced_matches_oracle(gpu):
     """BASELINE config 2 shape (T=1024, H=32) at B=2, slots gathered from a pool."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     P, B, T, H = 16, 2, 1024, 32
     C = H * 64
@@ -243,7 +243,7 @@ def _config2_inputs(gpu, B, T, H, seed=5):
 def test_prefill_config2_full_equals_decode_steps(gpu):
     """BASELINE config 2 at full size (B=8,T=1024,H=32): one row-per-lane prefill call (mode 1)
     == 1024 decode calls, bitwise (size-independent property; the oracle covers B=2 above)."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, H = 8, 1024, 32
     C = H * 64
@@ -263,7 +263,7 @@ def test_prefill_config2_full_rows_chunking_and_tolerance(gpu):
     T=256 calls == 512 calls of T=2, bitwise -- the per-token arithmetic does not depend on
     where a call or a staged chunk starts -- and within the stated
     tolerances of the row-per-lane kernel (y max-abs 2e-2 / mean-rel 5e-3, state 1e-3)."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, H = 8, 1024, 32
     C = H * 64
@@ -294,7 +294,7 @@ def test_rows_kernel_split_forms_are_identical(gpu):
     workgroups of 32 rows; above, one workgroup of 64.  Both keep every row's lane
     mapping and reduction order: a B=16, H=32 call (512 pairs, one workgroup each) equals
     the same work as two B=8 calls (256 pairs, two workgroups each), bitwise."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, H = 16, 37, 32
     C = H * 64
@@ -315,7 +315,7 @@ def test_rows_kernel_split_forms_are_identical(gpu):
 def test_rows_kernel_unaligned_inputs_match_oracle(gpu):
     """r..b and y starting 2 bytes past a 16-byte boundary take the kernel's scalar load/store
     path; results are the same bits as the oracle's row-split order."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, H = 2, 21, 2
     C = H * 64
@@ -389,7 +389,7 @@ def test_fp16_family_matches_oracle(gpu, variant, B, T, H):
 
 def test_fp16_w0_one_token_state_shape_from_reference_tests(gpu):
     """The reference tests pass w0 as [B,T,C]; only the first C values are used."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, C = 2, 8, 128
     H = C // 64
@@ -404,7 +404,7 @@ def test_fp16_w0_one_token_state_shape_from_reference_tests(gpu):
 
 def test_legacy_state_as_1_c_64(gpu):
     """The legacy golden test reshapes the state to [1,C,64] (reference test_monkey_patch.py:39-43)."""
-    from vkwr_amd._ops import rwkv7_ops
+    from vkwr._ops import rwkv7_ops
 
     C = 128
     ins = _dev(make_wkv_inputs(1, 3, 2, seed=10, dist="realistic"), gpu)
@@ -425,7 +425,7 @@ def _fp16_inputs(B, T, C, device):
 
 @pytest.mark.parametrize("B,T,C", [(1, 1, 64), (1, 4, 64), (2, 8, 128), (4, 4, 256), (1, 16, 128)])
 def test_ref_wkv_seq_fp16_basic(gpu, B, T, C):
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     H = C // 64
     state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
@@ -435,7 +435,7 @@ def test_ref_wkv_seq_fp16_basic(gpu, B, T, C):
 
 
 def test_ref_fp16_not_nan_mutation_zero_determinism(gpu):
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, C = 2, 8, 256
     H = C // 64
@@ -459,7 +459,7 @@ def test_ref_fp16_not_nan_mutation_zero_determinism(gpu):
 
 @pytest.mark.parametrize("fn", ["wkv_forward_fp32", "wkv_forward_seq_fp32", "wkv_forward_small_fp32", "wkv_forward_block_fp32"])
 def test_ref_fp32_basic_mutation_zero(gpu, fn):
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, C = 2, 8, 256
     H = C // 64
@@ -473,7 +473,7 @@ def test_ref_fp32_basic_mutation_zero(gpu, fn):
 
 
 def test_ref_validation_errors(gpu):
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, C, H = 1, 4, 100, 2
     state = torch.zeros(B, H, 64, 64, dtype=torch.float16, device=gpu)
@@ -498,7 +498,7 @@ def test_ref_validation_errors(gpu):
 
 
 def test_ref_advance_i32(gpu):
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     x = torch.zeros(4, dtype=torch.int32, device=gpu)
     assert ops.advance_i32(x, 5) is None
@@ -523,7 +523,7 @@ def test_ref_advance_i32(gpu):
 
 def test_ref_wkv_seq_fp16_performance(gpu):
     """Liveness bound of the reference (tests/ops/test_v1_wkv_ops.py:454-466): < 200 ms/call."""
-    from vkwr_amd._ops.v1 import v1_wkv_ops as ops
+    from vkwr._ops.v1 import v1_wkv_ops as ops
 
     B, T, C = 2, 64, 1024
     H = C // 64

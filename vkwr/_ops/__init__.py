@@ -6,7 +6,7 @@ The reference also imports ``sampling_ops``, a module it does not ship (so
 
 
 def import_all_ops():
-    from vkwr_amd._ops import rwkv7_ops, sampling_ops  # noqa: F401
-    from vkwr_amd._ops.v1 import import_all_v1_ops
+    from vkwr._ops import rwkv7_ops, sampling_ops  # noqa: F401
+    from vkwr._ops.v1 import import_all_v1_ops
 
     import_all_v1_ops()

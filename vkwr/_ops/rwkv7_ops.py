@@ -5,9 +5,7 @@ Same names, signatures and output allocation as the reference.
 import torch
 import torch.library
 
-from vkwr_amd._ops._load import load_ext
-
-_rwkv7_C = load_ext("_rwkv7_C")
+from vkwr import _rwkv7_C  # noqa: F401  (registers the ops)
 
 HEAD_SIZE = 64
 

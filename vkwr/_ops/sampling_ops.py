@@ -15,9 +15,7 @@ logits: fp32 [B, V] or [B, T, V] (row b samples from its last token); tok: int32
 import torch
 import torch.library
 
-from vkwr_amd._ops._load import load_ext
-
-_sampling_C = load_ext("_sampling_C")
+from vkwr import _sampling_C  # noqa: F401  (registers the ops)
 
 STATE_BYTES = 32  # VKWR_SAMPLING_STATE_BYTES
 

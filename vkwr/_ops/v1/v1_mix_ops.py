@@ -7,9 +7,7 @@ the Python-side ValueError of tmix_mix6_t1_c4096 for C != 4096
 import torch
 import torch.library
 
-from vkwr_amd._ops._load import load_ext
-
-_v1_mix_C = load_ext("_v1_mix_C")
+from vkwr import _v1_mix_C  # noqa: F401  (registers the ops)
 
 
 def _like(x, n):

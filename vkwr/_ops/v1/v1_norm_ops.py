@@ -6,9 +6,7 @@ allocates its outputs in the extension, as there.
 import torch
 import torch.library
 
-from vkwr_amd._ops._load import load_ext
-
-_v1_norm_C = load_ext("_v1_norm_C")
+from vkwr import _v1_norm_C  # noqa: F401  (registers the ops)
 
 
 def _like(x, n=1):

@@ -4,9 +4,7 @@ reference."""
 import torch
 import torch.library
 
-from vkwr_amd._ops._load import load_ext
-
-_v1_rank_C = load_ext("_v1_rank_C")
+from vkwr import _v1_rank_C  # noqa: F401  (registers the ops)
 
 
 @torch.library.register_fake("vkwr_v1_rank::linear_wag_rank_in_f16")

@@ -8,9 +8,7 @@ end are additions: they have no reference counterpart.
 import torch
 import torch.library
 
-from vkwr_amd._ops._load import load_ext
-
-_v1_wkv_C = load_ext("_v1_wkv_C")
+from vkwr import _v1_wkv_C  # noqa: F401  (registers the ops)
 
 HEAD_SIZE = 64
 

@@ -31,7 +31,7 @@ Every buffer is preallocated for `max_rows` rows, so a step allocates nothing.
 import torch
 
 from vkwr_amd import capi
-from vkwr_amd.model_executor.rwkv7 import HEAD
+from vkwr.model_executor.rwkv7 import HEAD
 
 TMIX_MIX = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
 

@@ -1,15 +1,11 @@
-"""vkwr_amd: MI355X-native (gfx950) implementation of VKWR's RWKV-7 hot path.
+"""vkwr_amd: the MI355X-native (gfx950) kernels of VKWR's RWKV-7 hot path.
 
-Importing the package loads the HIP extension modules, which register the
-reference's torch-op namespaces (``torch.ops.vkwr_v1_wkv``, ``vkwr_rwkv7``, ...)
-with the same schemas, and the Python wrappers of ``vkwr_amd._ops`` mirror
-``vkwr._ops`` (reference vkwr/__init__.py:1-3, vkwr/_ops/__init__.py:1-5).
+``libvkwr_amd.so`` holds the hand-written HIP kernels behind the C ABI of
+include/vkwr_amd.h; ``vkwr_amd.capi`` binds that ABI with ctypes for the model
+executor.  The reference-facing package is ``vkwr``: its extension modules
+(``vkwr._v1_wkv_C`` ...) register the reference's torch ops on these kernels.
 
 torch is imported first on purpose: the kernels link libamdhip64.so.7 and must
 bind to the HIP runtime torch already loaded.
 """
-import torch  # noqa: F401  (must precede the extension modules)
-
-from vkwr_amd._ops import import_all_ops
-
-import_all_ops()
+import torch  # noqa: F401  (must precede the kernel library)

@@ -1,8 +1,9 @@
 """Build driver: configures and builds the CMake project (gfx950 only) in-tree.
 
-``build()`` always re-runs CMake (configure + build); the outputs land next to
-this file: ``libvkwr_amd.so`` (HIP kernels, C ABI of include/vkwr_amd.h) and
-the torch extension modules ``_v1_*_C.so`` / ``_rwkv7_C.so``.
+``build()`` always re-runs CMake (configure + build), in-tree:
+``vkwr_amd/libvkwr_amd.so`` (HIP kernels, C ABI of include/vkwr_amd.h) and the
+torch extension modules ``vkwr/_v1_*_C.so``, ``vkwr/_rwkv7_C.so`` and
+``vkwr/_sampling_C.so``.
 """
 import os
 import subprocess

@@ -1,6 +1,6 @@
 """ctypes binding of the C ABI (include/vkwr_amd.h) for the model executor.
 
-The reference-compatible torch ops (vkwr_amd._ops) cover the reference's op
+The reference-compatible torch ops (vkwr._ops) cover the reference's op
 surface; the decode driver additionally needs the fused entry points that
 have no reference op (batched GEMMs with fused epilogues, the slot-indexed
 shift-state fusion).  This module calls them directly with device pointers
@@ -13,10 +13,10 @@ import os
 
 import torch
 
-from vkwr_amd._ops._load import load_ext
-
-load_ext("_v1_wkv_C")  # the extension modules link (and so load) the kernel library
-_LIB = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvkwr_amd.so"))
+_LIBPATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvkwr_amd.so")
+if not os.path.exists(_LIBPATH):
+    raise ImportError(f"vkwr_amd: {_LIBPATH} is not built (gfx950 HIP kernels); there is no CPU fallback.")
+_LIB = ctypes.CDLL(_LIBPATH)
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
