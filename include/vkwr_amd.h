@@ -177,9 +177,13 @@ VKWR_EXPORT int vkwr_emb_ln0_bf16_to_f16(int64_t V, int C, const uint16_t* emb,
  *   fp16(y + (prev - y) * mix[i]), where y = fp16(LN(x + residual)) and prev is
  *   the shift_state row at entry; then that shift_state row = y.
  *   x_rows (may be NULL) gathers x: row r reads x[x_rows[r]] (an embedding
- *   lookup); shift_slots (may be NULL) maps row r to shift_state[shift_slots[r]]
- *   (a per-sequence slot pool).  The caller guarantees both are in range and
- *   shift_slots distinct.
+ *   lookup; x has n_x rows); shift_slots (may be NULL) maps row r to
+ *   shift_state[shift_slots[r]] (a per-sequence slot pool of n_shift rows).
+ *   shift_slots must be distinct.  A row whose x_rows or shift_slots entry
+ *   lies outside [0, n_x) / [0, n_shift) gets NaN in x_out and out[], and no
+ *   shift row is read or written for it (checked on the device; the host does
+ *   not read the index arrays).  n_x / n_shift are ignored when the matching
+ *   index array is NULL.
  * Replaces add_layer_norm_cmix_mix_f16{,_cfg,_scalar_stats}_cuda and
  * add_layer_norm_tmix_mix6_f16{,_cfg,_scalar_stats}_cuda
  * (csrc/v1/norm/norm_ops.cu:1045-1340), reached from the vkwr_v1_norm ops of the
@@ -190,7 +194,7 @@ VKWR_EXPORT int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t*
                                             int n_mix, const uint16_t* const* mix, float eps,
                                             uint16_t* x_out, uint16_t* const* out,
                                             const int32_t* x_rows, const int32_t* shift_slots,
-                                            void* stream);
+                                            int64_t n_x, int64_t n_shift, void* stream);
 
 /* out = x + y elementwise (fp32 add, fp16 round), n elements.
  * Replaces add_f16_cuda (csrc/v1/norm/norm_ops.cu:866-876), reached from
@@ -217,13 +221,14 @@ VKWR_EXPORT int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
                                          int half_math, void* stream);
 
 /* Token-shift lerp of T tokens for B sequences whose shift rows live in a slot
- * pool: sequence b's shift row is shift_pool[shift_slots[b]] (the caller
- * guarantees distinct, in-range slots); otherwise identical to
- * vkwr_token_shift_mix_f16.  No single reference function: replaces gathering
+ * pool of n_slots rows: sequence b's shift row is shift_pool[shift_slots[b]]
+ * (slots distinct); otherwise identical to vkwr_token_shift_mix_f16.  A slot
+ * outside [0, n_slots) gives that sequence NaN outputs and leaves the pool
+ * untouched (checked on the device).  No single reference function: replaces gathering
  * the shift rows, tmix_mix6 / cmix_mix (csrc/v1/mix/mix_ops.cu:42-160,
  * 432-462) and scattering them back, for the mixed prefill + decode step. */
 VKWR_EXPORT int vkwr_token_shift_mix_slots_f16(int B, int T, int C, const uint16_t* x, uint16_t* shift_pool,
-                                               const int32_t* shift_slots, int n_mix,
+                                               int64_t n_slots, const int32_t* shift_slots, int n_mix,
                                                const uint16_t* const* mix, uint16_t* const* out,
                                                int half_math, void* stream);
 
@@ -350,7 +355,7 @@ VKWR_EXPORT int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint
                                                  int n_mix, const uint16_t* const* mix, float eps,
                                                  uint16_t* x_out, uint16_t* const* out,
                                                  const int32_t* x_rows, const int32_t* shift_slots,
-                                                 void* stream);
+                                                 int64_t n_x, int64_t n_shift, void* stream);
 
 /* vkwr_add_layer_norm_mix_frag_f16 whose x is the unreduced output of
  * vkwr_frag_gemm_splitk_parts_f16: x[r, c] = fp16(sum over q < n_parts of
@@ -366,7 +371,8 @@ VKWR_EXPORT int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, cons
                                                        const uint16_t* weight, const uint16_t* bias,
                                                        int n_mix, const uint16_t* const* mix, float eps,
                                                        uint16_t* x_out, uint16_t* const* out,
-                                                       const int32_t* shift_slots, void* stream);
+                                                       const int32_t* shift_slots, int64_t n_shift,
+                                                       void* stream);
 VKWR_EXPORT int vkwr_add_last_layer_norm_frag_f16(int B, int T, int C, const uint16_t* x,
                                                   const uint16_t* residual, const uint16_t* weight,
                                                   const uint16_t* bias, float eps, uint16_t* y,

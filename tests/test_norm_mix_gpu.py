@@ -365,3 +365,83 @@ def test_mix_reference_unit_tests(gpu):
         assert len(outs) == 3 and all(o.shape == k.shape and not torch.isnan(o).any() for o in outs)
         y = M.tmix_lnx_rkvres_xg(B, T, C, H, k, k, k, k, vv[0], torch.ones_like(vv[0]), torch.zeros_like(vv[0]), k)
         assert y.shape == k.shape and not torch.isnan(y).any()
+
+
+# ------------------------------------------------------------------ slot-indexed shift rows
+
+
+@pytest.mark.parametrize("n_mix", [1, 6])
+def test_token_shift_slots_bounds(gpu, n_mix):
+    """vkwr_token_shift_mix_slots_f16: in-range sequences equal the dense form on gathered
+    shift rows (bitwise, pool rows written back); a slot outside [0, n_slots) -- here n_slots
+    and -1, rejected by the kernel's own check before any pool access -- gives NaN outputs and
+    leaves the pool bitwise unchanged."""
+    from vkwr_amd import capi
+    B, T, C, P = 5, 3, 256, 9
+    x = dev(h(B, T, C), gpu)
+    pool = dev(h(P, C), gpu)
+    mixes = [dev(rng.random(C).astype(np.float16), gpu) for _ in range(n_mix)]
+    slots_l = [4, P, 0, -1, 7]
+    slots = torch.tensor(slots_l, dtype=torch.int32, device=gpu)
+    outs = [torch.empty(B, T, C, dtype=torch.float16, device=gpu) for _ in range(n_mix)]
+    before = pool.clone()
+    capi.token_shift(B, T, C, x, pool, mixes, outs, shift_slots=slots)
+    ok = [0, 2, 4]
+    sel = torch.tensor([slots_l[b] for b in ok], device=gpu).long()
+    shift = before.index_select(0, sel).contiguous()
+    xs = x[ok].contiguous()
+    refs = [torch.empty(len(ok), T, C, dtype=torch.float16, device=gpu) for _ in range(n_mix)]
+    capi.token_shift(len(ok), T, C, xs, shift, mixes, refs)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        assert torch.equal(o[ok], r)
+        assert torch.isnan(o[1]).all() and torch.isnan(o[3]).all()
+    want = before.clone()
+    want.index_copy_(0, sel, shift)
+    assert torch.equal(pool, want)
+
+
+@pytest.mark.parametrize("frag", [False, True])
+def test_ln_mix_slots_and_rows_bounds(gpu, frag):
+    """vkwr_add_layer_norm_mix{,_frag}_f16 with x_rows (embedding gather) and shift_slots:
+    in-range rows equal the dense form on gathered rows; a row whose x_rows entry is past the
+    table or whose slot is past the pool gets NaN outputs and no shift row is touched."""
+    from vkwr_amd import capi
+    rows, C, V, P = 6, 256, 40, 10
+    emb = dev(h(V, C), gpu)
+    res = dev(h(rows, C), gpu)
+    pool = dev(h(P, C), gpu)
+    wt, bs = dev(1 + h(C, scale=0.1), gpu), dev(h(C, scale=0.1), gpu)
+    mixes = [dev(rng.random(C).astype(np.float16), gpu) for _ in range(6)]
+    toks_l, slots_l = [3, 39, V, 0, 12, 7], [1, 9, 2, P, -1, 5]
+    toks = torch.tensor(toks_l, dtype=torch.int32, device=gpu)
+    slots = torch.tensor(slots_l, dtype=torch.int32, device=gpu)
+    x_out = torch.empty(rows, C, dtype=torch.float16, device=gpu)
+    mk = (lambda: capi.frag_empty(rows, C, gpu)) if frag else (lambda: torch.empty(rows, C, dtype=torch.float16,
+                                                                                 device=gpu))
+    outs = [mk() for _ in range(6)]
+    before = pool.clone()
+    capi.add_layer_norm_mix(emb, res, pool, wt, bs, mixes, x_out, outs, x_rows=toks, shift_slots=slots, frag=frag)
+    ok, bad = [0, 1, 5], [2, 3, 4]
+    xs = emb.index_select(0, torch.tensor([toks_l[r] for r in ok], device=gpu).long()).contiguous()
+    sel = torch.tensor([slots_l[r] for r in ok], device=gpu).long()
+    shift = before.index_select(0, sel).contiguous()
+    xo_ref = torch.empty(len(ok), C, dtype=torch.float16, device=gpu)
+    refs = [torch.empty(len(ok), C, dtype=torch.float16, device=gpu) for _ in range(6)]
+    capi.add_layer_norm_mix(xs, res[ok].contiguous(), shift, wt, bs, mixes, xo_ref, refs)
+    got = outs
+    if frag:
+        got = []
+        for o in outs:
+            u = torch.empty(rows, C, dtype=torch.float16, device=gpu)
+            capi.frag_unpack(o, rows, C, u)
+            got.append(u)
+    torch.cuda.synchronize()
+    assert torch.equal(x_out[ok], xo_ref)
+    assert torch.isnan(x_out[bad]).all()
+    for o, r in zip(got, refs):
+        assert torch.equal(o[ok], r)
+        assert torch.isnan(o[bad]).all()
+    want = before.clone()
+    want.index_copy_(0, sel, shift)
+    assert torch.equal(pool, want)

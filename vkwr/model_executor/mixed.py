@@ -63,10 +63,10 @@ class MixedEngine:
         self.ffn = buf(R, C)
         self.h = buf(self.max_seqs, C)
         self.logits = buf(self.max_seqs, cfg.vocab)
-        sizes = sorted({max_rows} | {1 << i for i in range(20) if (1 << i) <= max_rows})
-        need = max(capi.gemm_workspace_bytes(ps) for m in sizes for ps in self._gemm_batches(m, 1))
-        need = max(need, max(capi.gemm_workspace_bytes(self._head_problem(s)) for s in
-                             sorted({self.max_seqs} | {1 << i for i in range(20) if (1 << i) <= self.max_seqs})))
+        # GEMM workspace: the largest need of any launch at any row count a step can have
+        # (the plan is not monotone in the row count, so every count is evaluated).
+        need = max(capi.gemm_workspace_bytes_upto(ps) for ps in self._gemm_batches(max_rows, 1))
+        need = max(need, capi.gemm_workspace_bytes_upto(self._head_problem(self.max_seqs)))
         self.ws = torch.empty(max(need, 0), dtype=torch.uint8, device=dev)
 
     # -- GEMM batches (shared by planning and execution)

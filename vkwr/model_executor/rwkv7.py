@@ -195,9 +195,9 @@ class DecodeEngine:
         self.xk_ffn, self.act, self.ffn = buf(B, C), buf(B, F), buf(B, C)
         self.h = buf(B, C)
         self.logits = buf(B, cfg.vocab)
-        # GEMM workspace: the largest K-split need of any launch at any batch size
-        need = max(capi.gemm_workspace_bytes(ps) for b in sorted({B, 128, 64, 32, 16, 8, 4, 2, 1})
-                   if b <= B for ps in self._all_gemms(b))
+        # GEMM workspace: the largest K-split need of any launch at any batch size (every
+        # size is evaluated: the plan is not monotone in the row count)
+        need = max(capi.gemm_workspace_bytes_upto(ps) for ps in self._all_gemms(B))
         self.ws = torch.empty(max(need, 0), dtype=torch.uint8, device=dev)
 
     def _init_frag(self, dev):

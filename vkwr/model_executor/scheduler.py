@@ -64,6 +64,8 @@ class SlotAllocator:
 class ContinuousBatcher:
     def __init__(self, engine, state, max_decode=256, max_prefill_chunks=4, chunk=512, sample=None):
         assert chunk >= 1 and max_decode + chunk <= engine.max_rows
+        # every decode row and every chunk's sequence gets a logits row
+        assert max_decode + max_prefill_chunks <= engine.max_seqs, (max_decode, max_prefill_chunks, engine.max_seqs)
         self.engine, self.state = engine, state
         self.max_decode, self.max_prefill_chunks, self.chunk = max_decode, max_prefill_chunks, chunk
         self.max_rows = engine.max_rows
@@ -73,6 +75,7 @@ class ContinuousBatcher:
         self.sample = sample or (lambda logits: torch.argmax(logits.float(), dim=-1))
         self.device = engine.model.head.device
         self._next_id = 0
+        self._rr = 0  # round-robin start among the decoding sequences
         self.steps = 0
         self.tokens_processed = 0
 
@@ -99,7 +102,14 @@ class ContinuousBatcher:
             req.slot = self.slots.alloc()
             self._reset_slot(req.slot)
             self.running.append(req)
-        dec = [r for r in self.running if not r.prefilling][: self.max_decode]
+        decoding = [r for r in self.running if not r.prefilling]
+        if len(decoding) > self.max_decode:
+            # more generating sequences than decode rows: rotate, so none starves
+            start = self._rr % len(decoding)
+            dec = (decoding[start:] + decoding[:start])[: self.max_decode]
+            self._rr = start + self.max_decode
+        else:
+            dec = decoding
         rows = len(dec)
         groups = {}  # chunk length -> requests
         n_chunks = 0

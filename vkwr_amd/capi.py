@@ -65,7 +65,8 @@ _LIB.vkwr_last_error.restype = ctypes.c_char_p
 _gemm = _sig("vkwr_gemm_f16", [_i, ctypes.POINTER(GemmProblem), _p, _i64, _p])
 _gemm_ws = _sig("vkwr_gemm_f16_workspace_bytes", [_i, ctypes.POINTER(GemmProblem)], _i64)
 _ln_mix = _sig("vkwr_add_layer_norm_mix_f16",
-               [_i64, _i, _p, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p, _p, _p])
+               [_i64, _i, _p, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p, _p, _i64, _i64,
+                _p])
 _ln_last = _sig("vkwr_add_last_layer_norm_f16", [_i, _i, _i, _p, _p, _p, _p, _f, _p, _p])
 _ln = _sig("vkwr_layer_norm_f16", [_i64, _i, _p, _p, _p, _p, _f, _p, _p, _p])
 _gate = _sig("vkwr_tmix_kk_a_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p])
@@ -79,12 +80,13 @@ _frag_splitk = _sig("vkwr_frag_gemm_splitk_f16", [ctypes.POINTER(FragProblem), _
 _frag_splitk_parts = _sig("vkwr_frag_gemm_splitk_parts_f16", [ctypes.POINTER(FragProblem), _i, _p, _i64, _p])
 _ln_mix_parts = _sig("vkwr_add_layer_norm_mix_parts_frag_f16",
                      [_i64, _i, _p, _i, _i64, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p,
-                      _p])
+                      _i64, _p])
 _frag_splitk_ws = _sig("vkwr_frag_gemm_splitk_workspace_bytes", [_i64, _i64, _i], _i64)
 _frag_pack = _sig("vkwr_frag_pack_f16", [_i64, _i64, _p, _i, _p, _p])
 _frag_unpack = _sig("vkwr_frag_unpack_f16", [_i64, _i64, _p, _p, _p])
 _ln_mix_frag = _sig("vkwr_add_layer_norm_mix_frag_f16",
-                    [_i64, _i, _p, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p, _p, _p])
+                    [_i64, _i, _p, _p, _p, _p, _p, _i, ctypes.POINTER(_p), _f, _p, ctypes.POINTER(_p), _p, _p, _i64,
+                     _i64, _p])
 _ln_last_frag = _sig("vkwr_add_last_layer_norm_frag_f16", [_i, _i, _i, _p, _p, _p, _p, _f, _p, _p])
 _gn_frag = _sig("vkwr_tmix_groupnorm_bonus_gate_frag_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _wkv_fused = _sig("vkwr_wkv7_decode_fused_f16", [_i, _i, _i, _p, _i, _i, _p] + [_p] * 13 + [_i, _p])
@@ -92,7 +94,7 @@ _wkv_layout = _sig("vkwr_wkv7_state_layout_f32", [_i64, _p, _p, _i, _p])
 WKV_STATE_STD, WKV_STATE_ILV = 0, 1
 _shift = _sig("vkwr_token_shift_mix_f16", [_i, _i, _i, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 _shift_slots = _sig("vkwr_token_shift_mix_slots_f16",
-                    [_i, _i, _i, _p, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
+                    [_i, _i, _i, _p, _p, _i64, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 _d = ctypes.c_double
 _samp_setup = _sig("vkwr_sampling_setup_rand", [_i64, _i, _p, _p])
 _samp_temp = _sig("vkwr_sampling_temperature_topk_topp", [_i, _i, _i, _p, _p, _p, _p, _d, _i, _d, _p])
@@ -139,6 +141,25 @@ def gemm_workspace_bytes(problems):
     return n
 
 
+def gemm_workspace_bytes_upto(problems):
+    """The largest workspace one launch of `problems` needs when every problem's row count is
+    replaced by the same R, over R = 1 .. the problems' common row count.  The GEMM plan (tile
+    shape, K splits, the large-M kernel's split last round) is not monotone in the row count,
+    so a buffer sized for the largest batch, or for a few row counts, can fall short at others."""
+    arr = _arr(problems)
+    rows = {int(p.m) for p in problems}
+    assert len(rows) == 1, f"problems must share the row count (got {sorted(rows)})"
+    best = 0
+    for m in range(1, rows.pop() + 1):
+        for i in range(len(problems)):
+            arr[i].m = m
+        n = _gemm_ws(len(problems), arr)
+        if n < 0:
+            raise RuntimeError(f"vkwr_gemm_f16_workspace_bytes: {_LIB.vkwr_last_error().decode()}")
+        best = max(best, n)
+    return best
+
+
 def gemm(problems, workspace):
     """Runs 1..8 GEMMs in one launch; workspace is a uint8 CUDA tensor (may be empty)."""
     arr = _arr(problems)
@@ -148,14 +169,17 @@ def gemm(problems, workspace):
 
 def add_layer_norm_mix(x, residual, shift_state, weight, bias, mixes, x_out, outs, eps=1e-5,
                        x_rows=None, shift_slots=None, frag=False):
-    """frag=True: outs are frag matrices [rows, C] (see frag_empty)."""
+    """frag=True: outs are frag matrices [rows, C] (see frag_empty).  x_rows gathers rows of x
+    (bounded by x's row count), shift_slots rows of shift_state (bounded by its row count); an
+    index out of range gives that row NaN outputs and leaves the shift state untouched."""
     rows = x_out.shape[0]
     C = x_out.shape[-1]
     mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
     fn = _ln_mix_frag if frag else _ln_mix
     _check(fn(rows, C, _ptr(x), _ptr(residual), _ptr(shift_state), _ptr(weight), _ptr(bias), len(mixes),
-              mp, eps, _ptr(x_out), op, _ptr(x_rows), _ptr(shift_slots), _stream()),
+              mp, eps, _ptr(x_out), op, _ptr(x_rows), _ptr(shift_slots), x.numel() // C,
+              shift_state.numel() // C, _stream()),
            "vkwr_add_layer_norm_mix%s_f16" % ("_frag" if frag else ""))
 
 
@@ -251,7 +275,7 @@ def add_layer_norm_mix_parts(x_parts, n_parts, part_stride, residual, shift_stat
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
     _check(_ln_mix_parts(rows, C, _ptr(x_parts), n_parts, part_stride, _ptr(residual), _ptr(shift_state),
                          _ptr(weight), _ptr(bias), len(mixes), mp, eps, _ptr(x_out), op, _ptr(shift_slots),
-                         _stream()), "vkwr_add_layer_norm_mix_parts_frag_f16")
+                         shift_state.numel() // C, _stream()), "vkwr_add_layer_norm_mix_parts_frag_f16")
 
 
 def _arr_frag(problems):
@@ -286,8 +310,8 @@ def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False, shift_slo
         _check(_shift(B, T, C, _ptr(x), _ptr(shift_state), len(mixes), mp, op, 1 if half_math else 0, _stream()),
                "vkwr_token_shift_mix_f16")
     else:
-        _check(_shift_slots(B, T, C, _ptr(x), _ptr(shift_state), _ptr(shift_slots), len(mixes), mp, op,
-                            1 if half_math else 0, _stream()), "vkwr_token_shift_mix_slots_f16")
+        _check(_shift_slots(B, T, C, _ptr(x), _ptr(shift_state), shift_state.numel() // C, _ptr(shift_slots),
+                            len(mixes), mp, op, 1 if half_math else 0, _stream()), "vkwr_token_shift_mix_slots_f16")
 
 
 def sampling_setup_rand(seed, states):

@@ -176,7 +176,7 @@ std::vector<at::Tensor> run_mix(const at::Tensor& x, const at::Tensor& residual,
   }
   check_status(vkwr_add_layer_norm_mix_f16(x.size(0), (int)C, h(x), h(residual), h(shift_state),
                                            h(weight), h(bias), n, mp, (float)eps, h(outs[0]), op,
-                                           nullptr, nullptr, stream()),
+                                           nullptr, nullptr, 0, 0, stream()),
                what);
   return outs;
 }

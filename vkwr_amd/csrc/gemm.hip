@@ -694,19 +694,17 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
     Prob& P = bt.p[i];
     const int base = P.tiles_m * P.tiles_n;
     // Split K only when the whole batch leaves CUs idle; keep >= 8 stages per split.
+    // An empty problem (no tiles) or K == 0 (the kernel writes epilogue(0)) is never split.
     int s = 1;
-    if (!cfg.big && tiles < target_wgs && P.m <= 256) {
+    if (!cfg.big && tiles > 0 && base > 0 && P.k > 0 && tiles < target_wgs && P.m <= 256) {
       s = (target_wgs + tiles - 1) / tiles;
       s = std::min(s, std::max(1, P.k / (8 * kBK)));
       s = std::min(s, 16);
     }
-    int kps = (P.k + s - 1) / s;
-    kps = (kps + kBK - 1) / kBK * kBK;
-    s = (P.k + kps - 1) / kps;
-    P.splits = std::max(1, s);
-    P.k_per_split = std::max(kps, kBK);
+    const int kps = std::max(kBK, ((P.k + s - 1) / s + kBK - 1) / kBK * kBK);
+    P.splits = std::max(1, (P.k + kps - 1) / kps);
+    P.k_per_split = kps;
     if (P.splits > 1) ws += (int64_t)P.splits * P.m * P.n * 4;
-    (void)base;
   }
   int begin = 0;
   for (int i = 0; i < bt.n; ++i) {

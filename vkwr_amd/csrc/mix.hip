@@ -28,6 +28,7 @@ struct ShiftArgs {
   const _Float16* x;
   _Float16* shift;
   const int32_t* shift_slots;  // may be null: sequence b uses shift row b
+  int64_t n_slots;             // rows of the shift pool when shift_slots is given
   const _Float16* mix[6];
   _Float16* out[6];
 };
@@ -54,8 +55,18 @@ __global__ __launch_bounds__(256) void token_shift_kernel(ShiftArgs p) {
     for (int e = 0; e < VW; ++e) mu[i][e] = p.mix[i][c0 + e];
 
   _Float16 prev[VW];
-  const int64_t srow = (int64_t)(p.shift_slots ? p.shift_slots[b] : b) * p.C + c0;
+  const int64_t slot = p.shift_slots ? (int64_t)p.shift_slots[b] : b;
+  const int64_t srow = slot * p.C + c0;
   const _Float16* xs = p.x + ((int64_t)b * p.T) * p.C + c0;
+  if (p.shift_slots && (slot < 0 || slot >= p.n_slots)) {
+    // A slot outside the pool: this sequence's outputs are NaN and no shift row is touched.
+    for (int t = t0; t < t1; ++t)
+#pragma unroll
+      for (int i = 0; i < NMIX; ++i)
+#pragma unroll
+        for (int e = 0; e < VW; ++e) p.out[i][((int64_t)b * p.T + t) * p.C + c0 + e] = (_Float16)__builtin_nanf("");
+    return;
+  }
   if (t0 == 0) {
 #pragma unroll
     for (int e = 0; e < VW; ++e) prev[e] = p.shift[srow + e];
@@ -325,8 +336,8 @@ using namespace vk;
 
 namespace {
 int token_shift_mix(const char* fn, int B, int T, int C, const uint16_t* x, uint16_t* shift_state,
-                    const int32_t* shift_slots, int n_mix, const uint16_t* const* mix, uint16_t* const* out,
-                    int half_math, void* stream) {
+                    const int32_t* shift_slots, int64_t n_slots, int n_mix, const uint16_t* const* mix,
+                    uint16_t* const* out, int half_math, void* stream) {
   VK_REQUIRE(B >= 0 && T >= 0 && C >= 0, "%s: negative size", fn);
   VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
   if ((int64_t)B * T * C == 0) return VKWR_OK;
@@ -338,6 +349,7 @@ int token_shift_mix(const char* fn, int B, int T, int C, const uint16_t* x, uint
   p.x = reinterpret_cast<const _Float16*>(x);
   p.shift = reinterpret_cast<_Float16*>(shift_state);
   p.shift_slots = shift_slots;
+  p.n_slots = n_slots;
   bool vec = (C % 8 == 0) && aligned16(x) && aligned16(shift_state);
   for (int i = 0; i < n_mix; ++i) {
     VK_REQUIRE(mix[i] && out[i], "%s: null pointer", fn);
@@ -367,18 +379,19 @@ extern "C" int vkwr_token_shift_mix_f16(int B, int T, int C, const uint16_t* x,
                                         const uint16_t* const* mix, uint16_t* const* out,
                                         int half_math, void* stream) {
   clear_error();
-  return token_shift_mix("vkwr_token_shift_mix_f16", B, T, C, x, shift_state, nullptr, n_mix, mix, out, half_math,
-                         stream);
+  return token_shift_mix("vkwr_token_shift_mix_f16", B, T, C, x, shift_state, nullptr, 0, n_mix, mix, out,
+                         half_math, stream);
 }
 
 extern "C" int vkwr_token_shift_mix_slots_f16(int B, int T, int C, const uint16_t* x, uint16_t* shift_pool,
-                                              const int32_t* shift_slots, int n_mix,
+                                              int64_t n_slots, const int32_t* shift_slots, int n_mix,
                                               const uint16_t* const* mix, uint16_t* const* out,
                                               int half_math, void* stream) {
   clear_error();
   const char* fn = "vkwr_token_shift_mix_slots_f16";
   VK_REQUIRE((int64_t)B * T * C == 0 || shift_slots, "%s: null shift_slots", fn);
-  return token_shift_mix(fn, B, T, C, x, shift_pool, shift_slots, n_mix, mix, out, half_math, stream);
+  VK_REQUIRE(n_slots >= 0, "%s: negative n_slots", fn);
+  return token_shift_mix(fn, B, T, C, x, shift_pool, shift_slots, n_slots, n_mix, mix, out, half_math, stream);
 }
 
 extern "C" int vkwr_tmix_kk_a_gate_f16(int B, int T, int C, int H, const uint16_t* k,

@@ -38,6 +38,7 @@ struct LnArgs {
   _Float16* y;      // plain mode output
   const int32_t* x_rows;       // may be null: x row = row
   const int32_t* shift_slots;  // may be null: shift row = row
+  int64_t n_x, n_shift;        // rows of x / shift when x_rows / shift_slots index them
   // mix mode
   _Float16* shift;
   const _Float16* mix[6];
@@ -74,7 +75,22 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
   const int64_t rrow = row * p.src_mul + p.src_add;  // residual row
   const int64_t rsrc = rrow * (int64_t)C;
   const int64_t dst = row * (int64_t)C;
-  const int64_t sdst = (p.shift_slots ? (int64_t)p.shift_slots[row] : row) * (int64_t)C;
+  const int64_t srow = p.shift_slots ? (int64_t)p.shift_slots[row] : row;
+  const int64_t sdst = srow * (int64_t)C;
+  if constexpr (NMIX > 0) {
+    // An index outside its table (x_rows past the embedding, shift_slots past the pool):
+    // the row's outputs are NaN and no shift row is read or written.  Block-uniform.
+    if ((p.x_rows && (xrow < 0 || xrow >= p.n_x)) || (p.shift_slots && (srow < 0 || srow >= p.n_shift))) {
+      const _Float16 nan = (_Float16)__builtin_nanf("");
+      for (int c = tid; c < C; c += kThreads) {
+        p.x_out[dst + c] = nan;
+        const int64_t o = p.out_frag ? frag_index(row, c, C) : dst + c;
+#pragma unroll
+        for (int i = 0; i < NMIX; ++i) p.out[i][o] = nan;
+      }
+      return;
+    }
+  }
 
   // Vector path: every input of the row -- x, residual, the LN weight and bias, the
   // previous token's shift row and the mix vectors -- is requested here, before the
@@ -363,8 +379,8 @@ namespace {
 int add_ln_mix(const char* fn, int64_t rows, int C, const uint16_t* x, const uint16_t* residual,
                uint16_t* shift_state, const uint16_t* weight, const uint16_t* bias, int n_mix,
                const uint16_t* const* mix, float eps, uint16_t* x_out, uint16_t* const* out,
-               const int32_t* x_rows, const int32_t* shift_slots, int frag, void* stream,
-               const float* x_parts = nullptr, int n_parts = 0, int64_t part_stride = 0) {
+               const int32_t* x_rows, const int32_t* shift_slots, int64_t n_x, int64_t n_shift, int frag,
+               void* stream, const float* x_parts = nullptr, int n_parts = 0, int64_t part_stride = 0) {
   VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
   VK_REQUIRE(mix && out, "%s: null pointer", fn);
   LnArgs p{};
@@ -378,8 +394,12 @@ int add_ln_mix(const char* fn, int64_t rows, int C, const uint16_t* x, const uin
   p.eps = eps;
   p.x_out = reinterpret_cast<_Float16*>(x_out);
   p.shift = reinterpret_cast<_Float16*>(shift_state);
+  VK_REQUIRE(!x_rows || n_x >= 0, "%s: negative n_x", fn);
+  VK_REQUIRE(!shift_slots || n_shift >= 0, "%s: negative n_shift", fn);
   p.x_rows = x_rows;
   p.shift_slots = shift_slots;
+  p.n_x = n_x;
+  p.n_shift = n_shift;
   p.out_frag = frag;
   p.x_parts = x_parts;
   p.n_parts = n_parts;
@@ -403,10 +423,11 @@ extern "C" int vkwr_add_layer_norm_mix_f16(int64_t rows, int C, const uint16_t* 
                                            const uint16_t* weight, const uint16_t* bias, int n_mix,
                                            const uint16_t* const* mix, float eps, uint16_t* x_out,
                                            uint16_t* const* out, const int32_t* x_rows,
-                                           const int32_t* shift_slots, void* stream) {
+                                           const int32_t* shift_slots, int64_t n_x, int64_t n_shift,
+                                           void* stream) {
   clear_error();
   return add_ln_mix("vkwr_add_layer_norm_mix_f16", rows, C, x, residual, shift_state, weight, bias, n_mix,
-                    mix, eps, x_out, out, x_rows, shift_slots, 0, stream);
+                    mix, eps, x_out, out, x_rows, shift_slots, n_x, n_shift, 0, stream);
 }
 
 extern "C" int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint16_t* x,
@@ -415,10 +436,10 @@ extern "C" int vkwr_add_layer_norm_mix_frag_f16(int64_t rows, int C, const uint1
                                                 int n_mix, const uint16_t* const* mix, float eps,
                                                 uint16_t* x_out, uint16_t* const* out,
                                                 const int32_t* x_rows, const int32_t* shift_slots,
-                                                void* stream) {
+                                                int64_t n_x, int64_t n_shift, void* stream) {
   clear_error();
   return add_ln_mix("vkwr_add_layer_norm_mix_frag_f16", rows, C, x, residual, shift_state, weight, bias,
-                    n_mix, mix, eps, x_out, out, x_rows, shift_slots, 1, stream);
+                    n_mix, mix, eps, x_out, out, x_rows, shift_slots, n_x, n_shift, 1, stream);
 }
 
 extern "C" int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, const float* x_parts, int n_parts,
@@ -426,13 +447,14 @@ extern "C" int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, const
                                                       uint16_t* shift_state, const uint16_t* weight,
                                                       const uint16_t* bias, int n_mix, const uint16_t* const* mix,
                                                       float eps, uint16_t* x_out, uint16_t* const* out,
-                                                      const int32_t* shift_slots, void* stream) {
+                                                      const int32_t* shift_slots, int64_t n_shift,
+                                                      void* stream) {
   clear_error();
   const char* fn = "vkwr_add_layer_norm_mix_parts_frag_f16";
   VK_REQUIRE(rows == 0 || x_parts, "%s: null x_parts", fn);
   VK_REQUIRE(part_stride >= rows * (int64_t)C, "%s: part_stride below rows * C", fn);
   return add_ln_mix(fn, rows, C, nullptr, residual, shift_state, weight, bias, n_mix, mix, eps, x_out, out, nullptr,
-                    shift_slots, 1, stream, x_parts, n_parts, part_stride);
+                    shift_slots, 0, n_shift, 1, stream, x_parts, n_parts, part_stride);
 }
 
 extern "C" int vkwr_add_f16(int64_t n, const uint16_t* x, const uint16_t* y, uint16_t* out,
