@@ -14,7 +14,7 @@
  * Each entry point names the reference interface (szxysdt/VKWR, paths relative
  * to its root) whose device work it replaces.  The reference exposes those
  * through torch ops; the torch extension modules of this repository
- * (vkwr_amd/_v1_*_C, vkwr_amd/_rwkv7_C) register the same op names and
+ * (vkwr/_v1_*_C, vkwr/_rwkv7_C, vkwr/_sampling_C) register the same op names and
  * schemas and call these functions.
  */
 #ifndef VKWR_AMD_H
@@ -340,6 +340,22 @@ VKWR_EXPORT int64_t vkwr_gemm_f16_workspace_bytes(int n_problems, const vkwr_gem
  * csrc/v1/linear/torch_bindings.cpp:8-225 and csrc/v1/rank/torch_bindings.cpp:8-122. */
 VKWR_EXPORT int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, void* workspace,
                               int64_t workspace_bytes, void* stream);
+
+/* vkwr_gemm_f16 without a workspace argument and without any allocation: the K-split /
+ * stream-K partials go to a scratch array of vkwr_gemm_f16_noalloc_max_bytes() bytes
+ * (32 MiB) that the library holds in device memory, one copy per device, for the life of
+ * the process.  Same plan, same kernels, same results bit for bit as vkwr_gemm_f16 with a
+ * workspace.  A batch whose plan needs more scratch (vkwr_gemm_f16_workspace_bytes) than
+ * that is rejected with VKWR_ERR_INVALID before any GPU work; every GEMM batch of the
+ * 1.5B-shape decode step (C = 2048) at up to 256 rows fits.  It calls no hipMalloc / hipFree.  Calls that overlap on
+ * one device (concurrent streams, or host threads) share that device's scratch and race:
+ * serialise them.  The first call on a device looks the array's device address up once.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory,
+ * e.g. code under HIP graph capture, tight serving loops, or harnesses that forbid it. */
+VKWR_EXPORT int vkwr_gemm_f16_noalloc(int n_problems, const vkwr_gemm_problem* problems, void* stream);
+
+/* The scratch size of vkwr_gemm_f16_noalloc in bytes (its limit). */
+VKWR_EXPORT int64_t vkwr_gemm_f16_noalloc_max_bytes(void);
 
 /* Frag-output variants of three producers: identical arithmetic to
  * vkwr_add_layer_norm_mix_f16, vkwr_add_last_layer_norm_f16 and

@@ -27,6 +27,7 @@
 // once, 2 flops per weight element per row); MFMA-bound for large M.
 
 #include <algorithm>
+#include <mutex>
 
 #include "vk_capi.h"
 #include "vk_common.cuh"
@@ -828,17 +829,18 @@ extern "C" int64_t vkwr_gemm_f16_workspace_bytes(int n_problems, const vkwr_gemm
   return plan(bt, cfg, kTargetWgs);
 }
 
-extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, void* workspace,
-                             int64_t workspace_bytes, void* stream) {
-  clear_error();
-  const char* fn = "vkwr_gemm_f16";
-  Batch bt;
-  Config cfg;
-  if (int e = build_batch(fn, n_problems, problems, bt, cfg)) return e;
-  const int64_t need = plan(bt, cfg, kTargetWgs);
-  VK_REQUIRE(need <= workspace_bytes && (need == 0 || workspace != nullptr),
-             "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need,
-             (long long)workspace_bytes);
+// Scratch of vkwr_gemm_f16_noalloc: the K-split / stream-K partials of one launch.  Each
+// device that loads the library holds its own copy for the life of the process.  Host code
+// reaches it only through the address hipGetSymbolAddress returns for the current device
+// (scratch_ptr below); the array's name itself is a host-side stand-in.
+static constexpr int64_t kNoAllocScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// Launches a planned batch whose workspace (need bytes, checked by the caller) is at
+// `workspace`.  Shared by vkwr_gemm_f16 and vkwr_gemm_f16_noalloc.
+int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void* stream) {
   // Zero-sized problems and K == 0: nothing to tile; K == 0 writes epilogue(0).
   float* ws = reinterpret_cast<float*>(workspace);
   for (int i = 0; i < bt.n; ++i) {
@@ -898,4 +900,63 @@ extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, 
     if (int e = check_launch(fn)) return e;
   }
   return VKWR_OK;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, set on first use
+
+// The device address of the current device's copy of `scratch` (the array's name is a
+// host-side stand-in and must never reach a kernel).  Looked up once per device.
+int scratch_ptr(const char* fn, void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  VK_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices, "%s: no current device (%s)", fn,
+             hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    VK_REQUIRE(r == hipSuccess && p, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+               hipGetErrorString(r));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return VKWR_OK;
+}
+
+}  // namespace
+
+extern "C" int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_gemm_f16";
+  Batch bt;
+  Config cfg;
+  if (int e = build_batch(fn, n_problems, problems, bt, cfg)) return e;
+  const int64_t need = plan(bt, cfg, kTargetWgs);
+  VK_REQUIRE(need <= workspace_bytes && (need == 0 || workspace != nullptr),
+             "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need,
+             (long long)workspace_bytes);
+  return gemm_run(fn, bt, cfg, workspace, stream);
+}
+
+extern "C" int64_t vkwr_gemm_f16_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int vkwr_gemm_f16_noalloc(int n_problems, const vkwr_gemm_problem* problems, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_gemm_f16_noalloc";
+  Batch bt;
+  Config cfg;
+  if (int e = build_batch(fn, n_problems, problems, bt, cfg)) return e;
+  const int64_t need = plan(bt, cfg, kTargetWgs);
+  VK_REQUIRE(need <= kNoAllocScratchBytes,
+             "%s: this batch needs %lld bytes of scratch; the allocation-free entry point holds at most "
+             "%lld (use vkwr_gemm_f16 with a workspace)",
+             fn, (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int e = scratch_ptr(fn, &ws)) return e;
+  }
+  return gemm_run(fn, bt, cfg, ws, stream);
 }
