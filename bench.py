@@ -55,6 +55,9 @@ def parse_args():
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph (for counter runs); "
                          "skips the cache variants")
+    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling"],
+                    help="run one section alone and print its JSON object (for profiler runs); with --eager "
+                         "the decode steps are launched directly")
     return ap.parse_args()
 
 
@@ -112,11 +115,12 @@ def capture(step_fn, n_steps, stream):
     return g
 
 
-def model_decode(dev, steps, warmup=3, frag=True):
+def model_decode(dev, steps, warmup=3, frag=True, eager=False):
     """the RWKV-7 1.5B-shape decode step (L=24, C=2048, random fp16
     weights) for 128 sequences at T=1 from a 160-slot state pool.  One step is captured
     into a HIP graph and replayed `steps` times (the recurrent state advances every
-    replay); HIP events on the replay stream time it."""
+    replay); HIP events on the replay stream time it.  eager=True launches every step
+    directly (profiler counter runs)."""
     from vkwr.model_executor import DecodeEngine, RWKV7Config, RWKV7Model, RWKV7State
     from vkwr.model_executor.rwkv7 import flops_per_step, gbytes_per_step
 
@@ -134,21 +138,29 @@ def model_decode(dev, steps, warmup=3, frag=True):
         eng.step(state, tokens, slots)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
-    graph = capture(lambda i: eng.step(state, tokens, slots), 1, stream)
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-        for _ in range(steps):
+    if eager:
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            for _ in range(steps):
+                eng.step(state, tokens, slots)
+            ev1.record(stream)
+        torch.cuda.synchronize()
+    else:
+        graph = capture(lambda i: eng.step(state, tokens, slots), 1, stream)
+        for _ in range(warmup):
             graph.replay()
-        ev1.record(stream)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            for _ in range(steps):
+                graph.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        del graph
     ms = ev0.elapsed_time(ev1) / steps
     nbytes = gbytes_per_step(cfg, B)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    del graph
     return {
         "workload": "RWKV-7 1.5B-shape decode step (BASELINE config 3): L=24, C=2048, H=32, F=8192, "
                     "ranks w/a/v/g 96/96/64/256, V=65536, bs=128, T=1, random-init fp16 weights, "
@@ -161,7 +173,8 @@ def model_decode(dev, steps, warmup=3, frag=True):
                      "tokens_per_s_at_peak": round(B / (nbytes / (HBM_PEAK_GBS * 1e9)), 1)},
         "gemm_tflops": round(flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
         "gemm_path": "frag (vkwr_frag_gemm_f16, weights packed at load)" if frag else "row-major (vkwr_gemm_f16)",
-        "timing": "one decode step captured as a HIP graph, replayed; HIP events on the replay stream",
+        "timing": ("eager launches" if eager else "one decode step captured as a HIP graph, replayed") +
+                  "; HIP events on the launch stream",
     }
 
 
@@ -352,6 +365,14 @@ def main():
     from vkwr._ops.v1 import v1_wkv_ops as ops
 
     dev = torch.device("cuda:0")
+    if args.only:
+        copy_calibration(dev)  # a reference dispatch of known size for counter runs
+        run = {"decode": lambda: model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm, eager=args.eager),
+               "prefill": lambda: prefill_c2(dev, args.prefill_calls),
+               "serve": lambda: serve_mixed_7b(dev, args.serve_steps),
+               "sampling": lambda: sampling_bs128(dev, args.sampling_calls)}[args.only]
+        print(json.dumps({args.only: run()}), flush=True)
+        return
     K, W = args.steps, args.warmup
     gen = torch.Generator().manual_seed(0)
     pool = (torch.randn(P_SLOTS, H, HEAD, HEAD, generator=gen) * 0.1).to(dev)
