@@ -142,3 +142,98 @@ def test_scheduler_with_gpu_sampler(gpu):
     _, s2 = run(GpuSampler(16, cfg.vocab, gpu, seed=9, temperature=1.3, top_k=20, top_p=0.9))
     assert s1 == s2
     assert all(0 <= t < cfg.vocab for out in s1 for t in out)
+
+
+# ------------------------------------------------------------------ against the float32 oracle
+
+
+def _f32_model(model):
+    """The model's weights converted to float32 once, so that oracle/model_ref.decode_step
+    (which converts with .float()) does no per-call copies."""
+    import types
+    return types.SimpleNamespace(cfg=model.cfg, layers=[{k: v.float() for k, v in L.items()} for L in model.layers],
+                                 emb=model.emb.float(), ln_out_w=model.ln_out_w.float(),
+                                 ln_out_b=model.ln_out_b.float(), head=model.head.float())
+
+
+def _mixed_vs_oracle(gpu, cfg, P, Bd, Bp, T, seed, state_tol):
+    """One MixedEngine step of Bd decode rows plus Bp prefill chunks of T tokens against
+    oracle/model_ref: decode rows against one reference decode step, each chunk's
+    last-token logits and final states against T sequential reference decode steps, and
+    the last layer's WKV of both groups bit for bit against the C oracle on the engine's
+    own WKV inputs (decode rows: the one-chain order of the T = 1 kernel; chunks: the
+    row-split order of the prefill kernel).  Untouched slots stay bitwise unchanged.
+    End to end the states drift from the float32 model's by the fp16 rounding of the
+    intermediates, compounded over the chunk's T tokens; state_tol bounds that drift
+    relative to the largest state value."""
+    import os
+
+    import numpy as np
+    from oracle import model_ref
+    from oracle import oracle as orc
+    orc.set_threads(min(16, len(os.sched_getaffinity(0))))
+    from vkwr_amd import capi
+    from vkwr.model_executor import MixedEngine, RWKV7Model, RWKV7State
+    model = RWKV7Model(cfg, gpu, seed=seed)
+    state = RWKV7State(cfg, P, gpu, std=0.1, seed=seed + 1, layout=capi.WKV_STATE_STD)
+    g = torch.Generator().manual_seed(seed + 2)
+    perm = torch.randperm(P, generator=g)
+    sd, sp = perm[:Bd].to(torch.int32), perm[Bd:Bd + Bp].to(torch.int32)
+    td = torch.randint(0, cfg.vocab, (Bd,), generator=g, dtype=torch.int32)
+    tp = torch.randint(0, cfg.vocab, (Bp, T), generator=g, dtype=torch.int32)
+    used = torch.cat([sd, sp]).long().to(gpu)
+    wkv0, att0, ffn0 = (t[:, used].clone() for t in (state.wkv, state.att_shift, state.ffn_shift))
+    probe = [int(perm[-1]), int(perm[-2])]  # slots no group names
+    probe0 = state.wkv[:, probe].clone()
+    eng = MixedEngine(model, Bd + Bp * T, max_seqs=Bd + Bp)
+    logits = eng.step(state, decode=(td.to(gpu), sd.to(gpu)), prefill=[(tp.to(gpu), sp.to(gpu))]).float()
+    torch.cuda.synchronize()
+    H, C = cfg.n_head, cfg.n_embd
+    L = cfg.n_layer - 1
+    v_last = eng.v_new if cfg.n_layer > 1 else eng.v_first
+    # ---- last layer's WKV, bit for bit, on the engine's own inputs
+    ins = [t.cpu().numpy() for t in (eng.r, eng.w, eng.new_k, v_last, eng.neg_kk, eng.kka)]
+    y_eng = eng.y.cpu().numpy()
+    for (B, TT, r0, order, sl, base) in ((Bd, 1, 0, "seq", sd, 0), (Bp, T, Bd, "rows", sp, Bd)):
+        n = B * TT
+        pool = wkv0[L, base:base + B].cpu().numpy().copy()
+        y_ref = orc.wkv_fp32_slots(B, TT, C, H, pool, np.arange(B, dtype=np.int64),
+                                   *(x[r0:r0 + n].reshape(B, TT, C) for x in ins), order=order)
+        assert np.array_equal(y_eng[r0:r0 + n].view(np.uint16), y_ref.reshape(n, C).view(np.uint16)), order
+        assert np.array_equal(state.wkv[L, sl.long().to(gpu)].cpu().numpy(), pool), order
+    # ---- end to end against the float32 model
+    m32 = _f32_model(model)
+    with torch.no_grad():
+        idx_d = torch.arange(Bd, device=gpu)
+        wkv, att, ffn = wkv0.clone(), att0.clone(), ffn0.clone()
+        ref_d = model_ref.decode_step(m32, wkv, att, ffn, td.to(gpu), idx_d, round_fp16=False)
+        err_d = (logits[:Bd] - ref_d).abs().max().item()
+        sd_err = ((state.wkv[:, sd.long().to(gpu)] - wkv[:, :Bd]).abs().max() / wkv[:, :Bd].abs().max()).item()
+        idx_p = torch.arange(Bd, Bd + Bp, device=gpu)
+        for t in range(T):
+            ref_p = model_ref.decode_step(m32, wkv, att, ffn, tp[:, t].to(gpu), idx_p, round_fp16=False)
+        err_p = (logits[Bd:] - ref_p).abs().max().item()
+        sp_err = ((state.wkv[:, sp.long().to(gpu)] - wkv[:, Bd:]).abs().max() / wkv[:, Bd:].abs().max()).item()
+        shift_err = max((state.att_shift[:, used] - att).abs().max().item(),
+                        (state.ffn_shift[:, used] - ffn).abs().max().item())
+    print(f"logits max-abs: decode rows {err_d:.3g}, chunk last tokens {err_p:.3g}; state max-abs / max|S|: "
+          f"decode {sd_err:.3g}, chunks {sp_err:.3g}; shift rows max-abs {shift_err:.3g}", flush=True)
+    assert err_d <= TOL and err_p <= TOL
+    assert sd_err <= state_tol and sp_err <= state_tol
+    assert torch.equal(state.wkv[:, probe], probe0)
+
+
+def test_tiny_mixed_step_against_oracle(gpu):
+    """The tiny preset: 6 decode rows + 3 chunks of 9 tokens."""
+    from vkwr.model_executor import RWKV7Config
+    _mixed_vs_oracle(gpu, RWKV7Config.preset("tiny"), P=16, Bd=6, Bp=3, T=9, seed=20, state_tol=1e-3)
+
+
+def test_7b_layer_shape_mixed_step_against_oracle(gpu):
+    """BASELINE config 4 at the 7B layer shape (C=4096, H=64, F=16384, ranks w/a/v/g
+    128/128/96/480, V=65536) with L=2 layers so the float32 oracle stays cheap: one step of
+    256 decode rows + 4 prefill chunks x 512 tokens (2304 GEMM rows, the large-M GEMM path)
+    on a 2048-slot pool."""
+    from vkwr.model_executor import RWKV7Config
+    cfg = RWKV7Config(2, 4096, 16384, 128, 128, 96, 480, 65536)
+    _mixed_vs_oracle(gpu, cfg, P=2048, Bd=256, Bp=4, T=512, seed=30, state_tol=1e-2)
