@@ -537,3 +537,28 @@ def test_ref_wkv_seq_fp16_performance(gpu):
         ops.wkv_seq_fp16(B, T, C, H, state.clone(), *[x.clone() for x in ins])
     torch.cuda.synchronize()
     assert (time.perf_counter() - t0) / 30 * 1000 < 200.0
+
+
+def test_slots_large_pool_nontemporal_path_same_bits(gpu):
+    """A pool larger than the 256 MiB memory-side cache takes the decode step's
+    non-temporal state path: same bits as the cached path on a small pool (y and the
+    updated slot states), other slots untouched."""
+    from vkwr._ops.v1 import v1_wkv_ops as ops
+
+    B, H = 5, 32
+    C = H * 64
+    P_big = 520  # 520 x 32 x 16 KiB = 260 MiB > 256 MiB
+    big = torch.zeros(P_big, H, 64, 64, device=gpu)
+    small = torch.from_numpy(make_state(B, H, seed=40)).to(gpu)
+    slots_big = torch.tensor([513, 7, 260, 0, 519], dtype=torch.int32, device=gpu)
+    big[slots_big.long()] = small
+    before = big.clone()
+    ins = _dev([x.reshape(B, C) for x in make_wkv_inputs(B, 1, H, seed=40)], gpu)
+    y_big = ops.wkv_one_slots_fp32(B, C, H, big, slots_big, *ins)
+    y_small = ops.wkv_one_slots_fp32(B, C, H, small, torch.arange(B, dtype=torch.int32, device=gpu), *ins)
+    torch.cuda.synchronize()
+    assert torch.equal(y_big, y_small)
+    assert torch.equal(big[slots_big.long()], small)
+    others = torch.ones(P_big, dtype=torch.bool, device=gpu)
+    others[slots_big.long()] = False
+    assert torch.equal(big[others], before[others])

@@ -82,6 +82,11 @@ __device__ __forceinline__ float h2f(uint16_t bits) {
 __device__ __forceinline__ void dma16(const void* gsrc, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, (VK_LDS void*)lds_base, 16, 0, 0);
 }
+// The same with the non-temporal cache policy (nt): streamed data that will not be
+// read again soon is not kept in the caches it passes.
+__device__ __forceinline__ void dma16_nt(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (VK_LDS void*)lds_base, 16, 0, 2);
+}
 
 // ---------------------------------------------------------------- reductions
 

@@ -45,7 +45,9 @@ struct Fp32Args {
 };
 
 // ---- fp32 state staging: HBM <-> LDS (swizzled) <-> VGPRs, one column half
-// per phase (see the State I/O note above).  `st` is the 8 KiB tile.
+// per phase (see the State I/O note above).  `st` is the 8 KiB tile.  kNT: the
+// state is loaded and stored with the non-temporal cache policy.
+template <bool kNT = false>
 __device__ __forceinline__ void load_state_fp32(const float* S, f4* st, float* s, int lane) {
   const int sub = lane & 7;
 #pragma unroll
@@ -53,7 +55,8 @@ __device__ __forceinline__ void load_state_fp32(const float* S, f4* st, float* s
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int row = 8 * c + (lane >> 3);
-      dma16(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4, &st[c * 64]);
+      if constexpr (kNT) dma16_nt(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4, &st[c * 64]);
+      else dma16(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4, &st[c * 64]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -70,6 +73,7 @@ __device__ __forceinline__ void load_state_fp32(const float* S, f4* st, float* s
   }
 }
 
+template <bool kNT = false>
 __device__ __forceinline__ void store_state_fp32(float* S, f4* st, const float* s, int lane) {
   const int sub = lane & 7;
   __syncthreads();
@@ -84,7 +88,9 @@ __device__ __forceinline__ void store_state_fp32(float* S, f4* st, const float* 
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int row = 8 * c + (lane >> 3);
-      *reinterpret_cast<f4*>(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4) = st[c * 64 + lane];
+      f4* const dst = reinterpret_cast<f4*>(S + row * kHead + ph * 32 + (sub ^ (row & 7)) * 4);
+      if constexpr (kNT) __builtin_nontemporal_store(st[c * 64 + lane], dst);
+      else *dst = st[c * 64 + lane];
     }
     __syncthreads();
   }
@@ -162,8 +168,13 @@ __device__ __forceinline__ float* state_block(const Fp32Args& p, int bi, int h) 
 // Decode step (T == 1).  At most 128 VGPRs (4 waves per SIMD, 16 per CU):
 // with the 8 KiB LDS tile a 4096-wave step then fits on the 256 CUs in one
 // round.  The token's inputs are loaded before the state so that their
-// latency overlaps the state transfer.
-template <bool kSlots>
+// latency overlaps the state transfer.  kNT: non-temporal state loads and
+// stores, for state tables larger than the memory-side cache (a step's slots
+// are then unlikely to be cached when next visited, and the stores would only
+// evict other lines): cold 64 MiB read-modify-write measures 26 us with them
+// against 31 us without, while a cache-resident set is faster without them
+// (21 us against 24 us).
+template <bool kSlots, bool kNT>
 __global__ __launch_bounds__(64, 4) void wkv7_fp32_step_kernel(Fp32Args p) {
   __shared__ f4 st[512];
   const int lane = threadIdx.x;
@@ -179,9 +190,9 @@ __global__ __launch_bounds__(64, 4) void wkv7_fp32_step_kernel(Fp32Args p) {
     return;
   }
   float s[kHead];
-  load_state_fp32(S, st, s, lane);
+  load_state_fp32<kNT>(S, st, s, lane);
   p.y[tok] = token_fp32(s, reinterpret_cast<float*>(st), lane, xr, xw, xk, xv, xa, xb);
-  store_state_fp32(S, st, s, lane);
+  store_state_fp32<kNT>(S, st, s, lane);
 }
 
 // T tokens; the next token's inputs are loaded while the current one computes,
@@ -498,10 +509,17 @@ bool rows_vec_ok(const Fp32Args& p) {
 
 // rows: T > 1 uses the row-split kernel (dot products in its order); otherwise
 // the row-per-lane kernels (one FMA chain per dot product).
+// MI355X's memory-side cache (Infinity Cache).
+constexpr int64_t kMallBytes = (int64_t)256 << 20;
+
 template <bool kSlots>
 void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
   if (p.T == 1) {
-    hipLaunchKernelGGL(wkv7_fp32_step_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
+    const int64_t table = (int64_t)(kSlots ? p.n_slots : B) * p.H * kHead * kHead * 4;
+    if (table > kMallBytes)
+      hipLaunchKernelGGL((wkv7_fp32_step_kernel<kSlots, true>), dim3(B * p.H), dim3(64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((wkv7_fp32_step_kernel<kSlots, false>), dim3(B * p.H), dim3(64), 0, stream, p);
   } else if (rows) {
     RowsArgs ra{p, rows_vec_ok(p) ? 1 : 0};
     if (ra.vec && B * p.H < 2 * device_cus())
