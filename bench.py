@@ -55,7 +55,9 @@ def parse_args():
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph (for counter runs); "
                          "skips the cache variants")
-    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling"],
+    ap.add_argument("--ops-calls", type=int, default=30,
+                    help="timed calls per shape of the op-surface GEMMs at M=1 and M=128 (0: skip)")
+    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling", "ops"],
                     help="run one section alone and print its JSON object (for profiler runs); with --eager "
                          "the decode steps are launched directly")
     return ap.parse_args()
@@ -273,6 +275,92 @@ def sampling_bs128(dev, calls, warmup=3):
     }
 
 
+def ops_small_m(dev, calls, warmup=3):
+    """The reference op surface at decode sizes: vkwr_v1_linear ops (torch.ops, row-major
+    weights as the reference's callers pass them) at M = 1 (the reference's GEMV table:
+    head 2048 -> 65536, 4096 -> 4096, 4096 -> 16384, [K,N] weights of linear_f16) and at
+    M = 128 (the 1.5B projection shapes, nn.Linear [N,K] weights of linear_f16_orig),
+    beside the decode driver's frag-layout GEMM on the same M = 128 shapes.  Weights are
+    rotated over copies spanning >= 512 MiB, so every call streams them from HBM."""
+    from vkwr_amd import capi
+    from vkwr._ops.v1 import v1_linear_ops as L
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    stream = torch.cuda.Stream()
+
+    def timed(fn, n):
+        """Device time per call: n calls captured into one HIP graph, replayed once after an
+        untimed replay (the op surface's host-side dispatch is not what is measured)."""
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        graph = capture(fn, n, stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            graph.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        del graph
+        return ev0.elapsed_time(ev1) / n * 1e3  # us
+
+    def copies(shape):
+        nb = shape[0] * shape[1] * 2
+        n = max(2, -(-(512 << 20) // nb))
+        return [(torch.randn(*shape, device=dev, generator=g) * 0.02).half() for _ in range(n)]
+
+    out = {}
+    for (K, N) in ((2048, 65536), (4096, 4096), (4096, 16384)):
+        ws = copies((K, N))
+        x = torch.randn(1, K, device=dev, generator=g).half()
+        us = timed(lambda i: L.linear_f16(x, ws[i % len(ws)]), calls)
+        gbs = K * N * 2 / (us * 1e-6) / 1e9
+        out[f"m1_linear_f16_K{K}_N{N}"] = {"us": round(us, 2), "weight_GBps": round(gbs, 1),
+                                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del ws
+    for (K, N) in ((2048, 65536), (4096, 4096)):  # nn.Linear [N,K] weights (linear_f16_orig)
+        ws = copies((N, K))
+        x = torch.randn(1, K, device=dev, generator=g).half()
+        us = timed(lambda i: L.linear_f16_orig(x, ws[i % len(ws)]), calls)
+        gbs = K * N * 2 / (us * 1e-6) / 1e9
+        out[f"m1_linear_f16_orig_K{K}_N{N}"] = {"us": round(us, 2), "weight_GBps": round(gbs, 1),
+                                                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del ws
+    for (K, N, role) in ((2048, 2048, "r/k/v/o"), (2048, 8192, "ffn_key"), (8192, 2048, "ffn_value")):
+        ws = copies((N, K))
+        x = torch.randn(128, K, device=dev, generator=g).half()
+        us = timed(lambda i: L.linear_f16_orig(x, ws[i % len(ws)]), calls)
+        # the decode driver's path: both operands packed in the frag layout
+        xf = capi.frag_empty(128, K, dev)
+        capi.frag_pack(x, 128, K, xf)
+        wf = []
+        for w in ws:
+            f = capi.frag_empty(N, K, dev, zero=False)
+            capi.frag_pack(w, N, K, f)
+            wf.append(f)
+        del ws
+        y = torch.empty(128, N, dtype=torch.float16, device=dev)
+        us_frag = timed(lambda i: capi.frag_gemm([capi.frag_problem(xf, wf[i % len(wf)], y, 128, N, K)]), calls)
+        gbs = N * K * 2 / (us * 1e-6) / 1e9
+        out[f"m128_linear_f16_orig_{role}_K{K}_N{N}"] = {
+            "us": round(us, 2), "weight_GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "frag_path_us": round(us_frag, 2), "vs_frag": round(us / us_frag, 3)}
+        del wf
+        torch.cuda.empty_cache()
+    return {
+        "workload": "vkwr_v1_linear ops through torch.ops at M=1 ([K,N] weights, linear_f16) and M=128 "
+                    "([N,K] weights, linear_f16_orig), weights cold (rotated over >= 512 MiB of copies); "
+                    "frag_path_us: the decode driver's frag GEMM on the same M=128 shapes (unpadded, one call)",
+        "calls": calls,
+        "shapes": out,
+        "timing": "each shape's calls captured into one HIP graph and replayed; HIP events on the replay "
+                  "stream, mean per call",
+    }
+
+
 def serve_mixed_7b(dev, steps, warmup=1):
     """the RWKV-7 7B shape (L=32, C=4096, F=16384, random fp16 weights),
     one continuous-batching step = 256 decode rows + 4 prefill chunks of 512 tokens
@@ -370,7 +458,8 @@ def main():
         run = {"decode": lambda: model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm, eager=args.eager),
                "prefill": lambda: prefill_c2(dev, args.prefill_calls),
                "serve": lambda: serve_mixed_7b(dev, args.serve_steps),
-               "sampling": lambda: sampling_bs128(dev, args.sampling_calls)}[args.only]
+               "sampling": lambda: sampling_bs128(dev, args.sampling_calls),
+               "ops": lambda: ops_small_m(dev, args.ops_calls)}[args.only]
         print(json.dumps({args.only: run()}), flush=True)
         return
     K, W = args.steps, args.warmup
@@ -494,6 +583,8 @@ def main():
         result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
     if args.sampling_calls > 0 and not args.eager:
         result["sampling_bs128"] = sampling_bs128(dev, args.sampling_calls)
+    if args.ops_calls > 0 and not args.eager:
+        result["ops_small_m"] = ops_small_m(dev, args.ops_calls)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -369,3 +369,111 @@ def test_big_gemm_split_tail(gpu, M, K, N):
     r2 = run(w, capi.GEMM_B_NK, capi.EPI_RELU_SQUARE)
     torch.cuda.synchronize()
     assert torch.equal(r1, r2)
+
+
+# (M, K, N, layout): decode-sized shapes that take the small-M LDS-staged kernel, one per tile
+# shape -- 64 x 64 (M > 32, enough tiles), 32 x 64, 32 x 32, [K,N] weights at 64 and 32 rows --
+# with ragged M, K (a multiple of 8, not of 64) and N.
+RM_SHAPES = [
+    (128, 2048, 8192, "nk"), (100, 1000, 8200, "nk"), (128, 2048, 2048, "nk"), (8, 2048, 16384, "nk"),
+    (24, 264, 16392, "nk"), (128, 2048, 8192, "kn"), (77, 1032, 10248, "kn"), (5, 4096, 16384, "kn"),
+]
+# GEMV-shaped (M <= 4): [N,K] rows streamed per wave; [K,N] columns per workgroup, K split
+# over workgroups (fp32 partials + ordered reduce) when the columns alone leave CUs idle.
+GV_SHAPES = [
+    (1, 4096, 4096, "nk"), (3, 1000, 1032, "nk"), (4, 8192, 2056, "nk"), (2, 2048, 96, "nk"),
+    (1, 4096, 4096, "kn"), (1, 2048, 65536, "kn"), (2, 16384, 4096, "kn"), (3, 1032, 1000, "kn"),
+    (4, 4096, 16384, "kn"),
+]
+
+
+@pytest.mark.parametrize("M,K,N,layout", RM_SHAPES + GV_SHAPES)
+def test_small_m_lds_kernel_vs_oracle(gpu, M, K, N, layout):
+    from vkwr._ops.v1 import v1_linear_ops as L
+    a = h(M, K)
+    w = h(N, K, scale=0.05) if layout == "nk" else h(K, N, scale=0.05)
+    y = (L.linear_f16_orig if layout == "nk" else L.linear_f16)(dev(a, gpu), dev(w, gpu))
+    y2 = (L.linear_f16_orig if layout == "nk" else L.linear_f16)(dev(a, gpu), dev(w, gpu))
+    assert torch.equal(y, y2)  # deterministic
+    ref, abs_sum = R.gemm(a, w, layout)
+    check(y, ref, ACC * abs_sum, f"{layout} {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("act,epi", [("tanh", "none"), ("sigmoid", "bias"), ("relu2", "vres"), (None, "relu2")])
+def test_small_m_lds_kernel_activations_and_epilogues(gpu, act, epi):
+    """A-operand activations (rounded to fp16, as the staging kernels do) and the fused
+    epilogues on the small-M kernel, in a batch of three problems (M = 96, N = 2048..4104)."""
+    from vkwr_amd import capi
+    acts = {None: capi.ACT_NONE, "tanh": capi.ACT_TANH, "sigmoid": capi.ACT_SIGMOID, "relu2": capi.ACT_RELU_SQUARE}
+    epis = {"none": capi.EPI_NONE, "bias": capi.EPI_BIAS, "vres": capi.EPI_VALUE_RESIDUAL, "relu2": capi.EPI_RELU_SQUARE}
+    M, K = 96, 512
+    probs, keep, refs = [], [], []
+    for N in (2048, 4104, 3072):
+        a, w = h(M, K), h(N, K, scale=0.05)
+        v, vf, v0 = h(M, N), h(M, N), h(N)
+        c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+        ta, tw, tv, tvf, tv0 = (dev(x, gpu) for x in (a, w, v, vf, v0))
+        probs.append(capi.gemm_problem(ta, tw, c, a_act=acts[act], epilogue=epis[epi],
+                                       v=tv if epi == "vres" else None, v_first=tvf if epi == "vres" else None,
+                                       v0=tv0 if epi in ("bias", "vres") else None))
+        keep += [ta, tw, tv, tvf, tv0, c]
+        y64, abs_sum = R.gemm(a, w, "nk", a_act=act, epi="relu2" if epi == "relu2" else None)
+        if epi in ("bias", "vres"):
+            pre, abs_sum = R.gemm(a, w, "nk", a_act=act)
+            a64 = R._act(R._f(a), act)
+            if act is not None:
+                a64 = a64.astype(np.float16).astype(np.float64)
+            z = a64 @ R._f(w).T
+            if epi == "bias":
+                y64 = (z + R._f(v0)).astype(np.float16)
+            else:
+                y64 = R.vres_gate(v, vf, v0, z)
+        refs.append((c, y64, abs_sum))
+    assert capi.gemm_workspace_bytes(probs) == 0  # the small-M kernel needs no workspace
+    capi.gemm(probs, torch.empty(0, dtype=torch.uint8, device=gpu))
+    torch.cuda.synchronize()
+    for c, y64, abs_sum in refs:
+        # epilogue derivatives are bounded by 1 (sigmoid gate: 1/4 of |v_first - v| <= a few)
+        slack = ACC * abs_sum * (8.0 if epi == "vres" else 1.0)
+        if epi == "relu2":
+            slack = 2 * np.abs(np.sqrt(y64.astype(np.float64))) * ACC * abs_sum + ACC * abs_sum
+        check(c, y64, slack, f"{act} {epi}")
+
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+@pytest.mark.parametrize("act,epi", [("tanh", "none"), ("sigmoid", "bias"), (None, "vres"), ("relu2", "relu2")])
+def test_gemv_activations_and_epilogues(gpu, layout, act, epi):
+    """The GEMV kernels (M = 3) with A-operand activations and fused epilogues."""
+    from vkwr_amd import capi
+    acts = {None: capi.ACT_NONE, "tanh": capi.ACT_TANH, "sigmoid": capi.ACT_SIGMOID, "relu2": capi.ACT_RELU_SQUARE}
+    epis = {"none": capi.EPI_NONE, "bias": capi.EPI_BIAS, "vres": capi.EPI_VALUE_RESIDUAL, "relu2": capi.EPI_RELU_SQUARE}
+    M, K, N = 3, 2048, 1032
+    a = h(M, K)
+    w = h(N, K, scale=0.05) if layout == "nk" else h(K, N, scale=0.05)
+    v, vf, v0 = h(M, N), h(M, N), h(N)
+    c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    ta, tw, tv, tvf, tv0 = (dev(x, gpu) for x in (a, w, v, vf, v0))
+    prob = capi.gemm_problem(ta, tw, c, b_layout=capi.GEMM_B_NK if layout == "nk" else capi.GEMM_B_KN,
+                             a_act=acts[act], epilogue=epis[epi], v=tv if epi == "vres" else None,
+                             v_first=tvf if epi == "vres" else None, v0=tv0 if epi in ("bias", "vres") else None)
+    ws = torch.empty(max(capi.gemm_workspace_bytes([prob]), 1), dtype=torch.uint8, device=gpu)
+    capi.gemm([prob], ws)
+    torch.cuda.synchronize()
+    a64 = R._act(R._f(a), act)
+    if act is not None:
+        a64 = a64.astype(np.float16).astype(np.float64)
+    wt = R._f(w).T if layout == "nk" else R._f(w)
+    z = a64 @ wt
+    abs_sum = np.abs(a64) @ np.abs(wt)
+    if epi == "none":
+        y64 = z.astype(np.float16)
+    elif epi == "bias":
+        y64 = (z + R._f(v0)).astype(np.float16)
+    elif epi == "vres":
+        y64 = R.vres_gate(v, vf, v0, z)
+    else:
+        y64 = (np.maximum(z, 0) ** 2).astype(np.float16)
+    slack = ACC * abs_sum * (8.0 if epi == "vres" else 1.0)
+    if epi == "relu2":
+        slack = 2 * np.sqrt(np.abs(y64.astype(np.float64))) * ACC * abs_sum + ACC * abs_sum
+    check(c, y64, slack, f"{layout} {act} {epi}")

@@ -16,16 +16,16 @@ _noalloc = capi._sig("vkwr_gemm_f16_noalloc", [ctypes.c_int, ctypes.POINTER(capi
 _max = capi._sig("vkwr_gemm_f16_noalloc_max_bytes", [], ctypes.c_int64)
 
 
-def _batch(gpu, m, n, k, seed, epilogue=capi.EPI_NONE, nprob=1):
+def _batch(gpu, m, n, k, seed, epilogue=capi.EPI_NONE, nprob=1, kn=False):
     g = torch.Generator(device=gpu).manual_seed(seed)
     probs, outs, keep = [], [], []
     for i in range(nprob):
         a = torch.randn(m, k, device=gpu, generator=g).half()
-        b = (torch.randn(n, k, device=gpu, generator=g) * 0.05).half()
+        b = (torch.randn(*((k, n) if kn else (n, k)), device=gpu, generator=g) * 0.05).half()
         c = torch.full((m, n), float("nan"), device=gpu).half()
         v0 = torch.randn(n, device=gpu, generator=g).half()
-        probs.append(capi.gemm_problem(a, b, c, epilogue=epilogue,
-                                       v0=v0 if epilogue == capi.EPI_BIAS else None))
+        probs.append(capi.gemm_problem(a, b, c, b_layout=capi.GEMM_B_KN if kn else capi.GEMM_B_NK,
+                                       epilogue=epilogue, v0=v0 if epilogue == capi.EPI_BIAS else None))
         outs.append(c)
         keep += [a, b, v0]
     return probs, outs, keep
@@ -44,15 +44,17 @@ def _run_ws(probs, gpu):
 
 
 @pytest.mark.parametrize("shapes", [
-    # (m, n, k, epilogue, problems): a K-split row-major batch, then a smaller one
-    [(128, 2048, 8192, capi.EPI_NONE, 1), (40, 1024, 2048, capi.EPI_BIAS, 3)],
+    # (m, n, k, epilogue, problems, [K,N] weights): a K-split batch, then a smaller one
+    [(128, 1024, 8192, capi.EPI_NONE, 1, False), (40, 1024, 2048, capi.EPI_BIAS, 3, False)],
     # the large-M kernel's split last round (stream-K partials), then a smaller split batch
-    [(500, 4096, 1024, capi.EPI_RELU_SQUARE, 1), (64, 2048, 4096, capi.EPI_NONE, 2)],
+    [(500, 4096, 1024, capi.EPI_RELU_SQUARE, 1, False), (64, 1024, 4096, capi.EPI_NONE, 2, False)],
+    # the GEMV kernel's K parts ([K,N] weights, M <= 4), then a smaller one
+    [(3, 4096, 4096, capi.EPI_NONE, 1, True), (1, 2048, 2048, capi.EPI_BIAS, 2, True)],
 ])
 def test_noalloc_equals_workspace_entry_point(gpu, shapes):
     assert _max() == 32 << 20
-    for i, (m, n, k, epi, npb) in enumerate(shapes):
-        probs, outs, keep = _batch(gpu, m, n, k, seed=10 + i, epilogue=epi, nprob=npb)
+    for i, (m, n, k, epi, npb, kn) in enumerate(shapes):
+        probs, outs, keep = _batch(gpu, m, n, k, seed=10 + i, epilogue=epi, nprob=npb, kn=kn)
         need = capi.gemm_workspace_bytes(probs)
         assert 0 < need <= _max(), need  # the scratch is really used
         _run_noalloc(probs)

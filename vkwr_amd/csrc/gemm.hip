@@ -646,11 +646,382 @@ __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan p
   }
 }
 
+// ---- small-M path (decode-sized batches, M <= 128): row-major operands staged through LDS.
+//
+// At M <= 128 every weight byte is used M times, so the launch streams the weights
+// once and is bound by how many bytes each CU keeps in flight.  A workgroup owns a
+// (32 TM) x (32 TN) output tile over the whole of K; its 4 waves take the 64-deep k blocks
+// w, w + 4, ... (an in-workgroup K split: no workspace, no second kernel), and each wave
+// stages its blocks through two private LDS buffers with the DMA form of the vector
+// load (global_load_lds_dwordx4, no VGPR staging): one instruction moves 8 whole
+// 128-byte rows (64 k of a row is one cache line), chunk c of row r landing at slot
+// r*8 + (c ^ ((r >> 1) & 7)) so that the fragment reads (ds_read_b128, 8 consecutive k
+// of one row per lane) are conflict-free.  A [K,N] weight is staged as k-rows of 64
+// columns and its fragments gathered with 2-byte LDS reads (8 per fragment).  The wave
+// issues the next block's DMA before computing on the current one; the waits are
+// explicit, the DMA being invisible to the compiler.  After the loop the 4 wave
+// partials are added in wave order through LDS and each thread finishes 8 consecutive
+// columns with the generic epilogue (the A activation is applied to each fragment
+// after it is read, rounded to fp16, as gemm_kernel applies it while staging).
+// Rows past M and columns past N are read clamped to the last valid row / column and
+// discarded; k chunks past K (K % 8 == 0) are zeroed in the A fragment.
+constexpr int kRmBK = 64;
+
+// Waves per workgroup: 8 for the 32 x 32 tile (its LDS stages are half the size, so twice
+// the waves keep the same bytes in flight), 4 otherwise.
+template <int TM, int TN>
+constexpr int rm_waves() { return TM * TN == 1 ? 8 : 4; }
+
+template <int TM, int TN, bool kKN>
+__global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batch bt) {
+  constexpr int kRmNW = rm_waves<TM, TN>();
+  static_assert(!kKN || TN == 2, "[K,N] weights are staged as 128-byte k rows of 64 columns");
+  constexpr int kA = 32 * TM * kRmBK, kB = 32 * TN * kRmBK, kStage = kA + kB;  // halves
+  constexpr int kTiles = TM * TN;
+  constexpr int kBDma = kKN ? 8 : 4 * TN;           // DMA instructions per B block
+  constexpr int kDmaPerStage = 4 * TM + kBDma;
+  __shared__ __attribute__((aligned(1024))) _Float16 sm[kRmNW][2][kStage];
+  const int t = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProblems; ++i)
+    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  const Prob& P = bt.p[pi];
+  const int lt = t - P.tile_begin;
+  const int m0 = (lt / P.tiles_n) * (32 * TM), n0 = (lt % P.tiles_n) * (32 * TN);
+  const int M = P.m, N = P.n, K = P.k, a_act = P.a_act;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nkb = (K + kRmBK - 1) / kRmBK;
+  const int nb = nkb > w ? (nkb - w + kRmNW - 1) / kRmNW : 0;  // this wave's k blocks
+
+  // DMA instruction j of a stage fills slots 64 j + lane: row (64 j + lane) >> 3, chunk
+  // (slot & 7) ^ swizzle -- byte offsets for k block 0 (32-bit: the host checks that every
+  // operand is below 4 GiB).
+  uint32_t ao[TM * 4], bo[kBDma];
+#pragma unroll
+  for (int j = 0; j < TM * 4; ++j) {
+    const int sl = 64 * j + lane, r = sl >> 3, c = (sl & 7) ^ ((r >> 1) & 7);
+    ao[j] = (uint32_t)(((int64_t)min(m0 + r, M - 1) * K + c * 8) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < kBDma; ++j) {
+    const int sl = 64 * j + lane, r = sl >> 3, c = (sl & 7) ^ ((r >> 1) & 7);
+    if constexpr (kKN) bo[j] = (uint32_t)(min(n0 + c * 8, N - 8) * 2);  // the k row is added per block
+    else bo[j] = (uint32_t)(((int64_t)min(n0 + r, N - 1) * K + c * 8) * 2);
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sm[w][0][0]);
+  const void* const abase = uniform_ptr(P.a);
+  const void* const bbase = uniform_ptr(P.b);
+  auto dma = [&](int buf, int kb) __attribute__((always_inline)) {
+    const uint32_t la = lds0 + (uint32_t)(buf * kStage * 2), lb = la + kA * 2;
+    // k past K: the chunk offset is clamped to the row's last chunk (read, then zeroed)
+    const int k0 = kb * kRmBK;
+#pragma unroll
+    for (int j = 0; j < TM * 4; ++j) {
+      const int c = ((64 * j + lane) & 7) ^ ((((64 * j + lane) >> 3) >> 1) & 7);
+      const int kk = min(k0 + c * 8, K - 8) - c * 8;
+      dma16_m0(abase, ao[j] + (uint32_t)(kk * 2), la + j * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < kBDma; ++j) {
+      if constexpr (kKN) {
+        const int r = (64 * j + lane) >> 3;
+        dma16_m0(bbase, bo[j] + (uint32_t)((int64_t)(min(k0 + r, K - 1)) * N * 2), lb + j * 1024);
+      } else {
+        const int c = ((64 * j + lane) & 7) ^ ((((64 * j + lane) >> 3) >> 1) & 7);
+        const int kk = min(k0 + c * 8, K - 8) - c * 8;
+        dma16_m0(bbase, bo[j] + (uint32_t)(kk * 2), lb + j * 1024);
+      }
+    }
+  };
+
+  fv16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int lr = lane & 31, lh = lane >> 5;
+  auto compute = [&](int buf, int kb) __attribute__((always_inline)) {
+    const _Float16* sa = &sm[w][buf][0];
+    const _Float16* sb = sa + kA;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int ch = 2 * kk + lh;
+      const bool kin = kb * kRmBK + ch * 8 < K;
+      hv8 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = 32 * i + lr;
+        fa[i] = *reinterpret_cast<const hv8*>(sa + (r * 8 + (ch ^ ((r >> 1) & 7))) * 8);
+        if (a_act != VKWR_GEMM_ACT_NONE) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) fa[i][e] = (_Float16)act_in((float)fa[i][e], a_act);
+        }
+        if (!kin) fa[i] = hv8{};
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (kKN) {
+          const int n = 32 * j + lr, cn = n >> 3, e0 = n & 7;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int r = 16 * kk + 8 * lh + e;  // k row of the block
+            fb[j][e] = sb[(r * 8 + (cn ^ ((r >> 1) & 7))) * 8 + e0];
+          }
+        } else {
+          const int r = 32 * j + lr;
+          fb[j] = *reinterpret_cast<const hv8*>(sb + (r * 8 + (ch ^ ((r >> 1) & 7))) * 8);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  if (nb > 0) dma(0, w);
+  for (int it = 0; it < nb; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < nb) {
+      // the other buffer was last read in the previous iteration
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      dma(buf ^ 1, w + (it + 1) * kRmNW);
+      // only the block just issued may still be in flight
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerStage) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    compute(buf, w + it * kRmNW);
+  }
+
+  // ---- add the wave partials in wave order, then 8 columns per thread
+  float* red = reinterpret_cast<float*>(&sm[0][0][0]);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+#pragma unroll
+  for (int tt = 0; tt < kTiles; ++tt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[((w * kTiles + tt) * 16 + r) * 64 + lane] = acc[tt / TN][tt % TN][r];
+  __syncthreads();
+  for (int g = tid; g < kTiles * 16 * 8; g += 64 * kRmNW) {
+    const int tt = g >> 7, r = (g >> 3) & 15, l0 = (g & 7) * 8;
+    f4 s0 = *reinterpret_cast<const f4*>(&red[(tt * 16 + r) * 64 + l0]);
+    f4 s1 = *reinterpret_cast<const f4*>(&red[(tt * 16 + r) * 64 + l0 + 4]);
+#pragma unroll
+    for (int ww = 1; ww < kRmNW; ++ww) {
+      s0 += *reinterpret_cast<const f4*>(&red[((ww * kTiles + tt) * 16 + r) * 64 + l0]);
+      s1 += *reinterpret_cast<const f4*>(&red[((ww * kTiles + tt) * 16 + r) * 64 + l0 + 4]);
+    }
+    const int i = tt / TN, j = tt % TN;
+    const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * (l0 >> 5) + (r & 3);
+    const int col = n0 + 32 * j + (l0 & 31);
+    if (row >= M || col >= N) continue;
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const int64_t idx = (int64_t)row * N + col;
+    if (P.vec_out && col + 8 <= N) {
+      hv8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float y = epilogue(P, sv[e], row, col + e);
+        asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+        o[e] = (_Float16)y;
+      }
+      *reinterpret_cast<hv8*>(P.c + idx) = o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (col + e >= N) break;
+        float y = epilogue(P, sv[e], row, col + e);
+        asm volatile("" : "+v"(y));
+        P.c[idx + e] = (_Float16)y;
+      }
+    }
+  }
+}
+
+// ---- GEMV-shaped path (M <= 4): the weights stream straight into registers.
+//
+// With one to four activation rows there is no operand reuse worth a matrix tile: every
+// weight byte is used M times, so each workgroup streams its weight slice with fully
+// coalesced 16-byte loads and does the M dot products on the vector ALU in fp32.  The
+// activation rows (at most 64 KiB) are staged once per workgroup in LDS, with the A
+// activation applied and rounded to fp16 as gemm_kernel does.
+constexpr int kGvMaxM = 4;
+constexpr int kGvLdsHalfs = 32768;  // 64 KiB
+constexpr int kGvRowsNK = 16;       // [N,K]: weight rows per workgroup (4 per wave)
+constexpr int kGvColsKN = 512;      // [K,N]: columns per workgroup (a kilobyte of each k row)
+
+__device__ __forceinline__ void gv_stage_x(_Float16* xs, const Prob& P, int k0, int kn, int stride) {
+  // x[m][k0 .. k0 + kn) -> xs[m * stride + ...], 16 bytes per thread and step (kn % 8 == 0)
+  const int nch = kn / 8;
+  for (int i = threadIdx.x; i < P.m * nch; i += 256) {
+    const int m = i / nch, c = i - m * nch;
+    hv8 v = *reinterpret_cast<const hv8*>(P.a + (int64_t)m * P.k + k0 + 8 * c);
+    if (P.a_act != VKWR_GEMM_ACT_NONE) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (_Float16)act_in((float)v[e], P.a_act);
+    }
+    *reinterpret_cast<hv8*>(xs + m * stride + 8 * c) = v;
+  }
+}
+
+// [N,K] weights: a wave owns 4 rows over the whole of K; lane l reads chunks l, l + 64, ...
+// of each row (a kilobyte per instruction), and the (row, m) sums are reduced across the
+// wave in a fixed order.
+template <int M>
+__global__ __launch_bounds__(256) void gemv_nk_kernel(Batch bt) {
+  __shared__ __attribute__((aligned(16))) _Float16 xs[kGvLdsHalfs];
+  const int t = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProblems; ++i)
+    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  const Prob& P = bt.p[pi];
+  const int N = P.n, K = P.k;
+  const int nr0 = (t - P.tile_begin) * kGvRowsNK;
+  gv_stage_x(xs, P, 0, K, K);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nch = K / 8;
+  float acc[4][M];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+  const _Float16* wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = P.b + (int64_t)min(nr0 + 4 * w + r, N - 1) * K;
+  // 4 chunks of each of the 4 rows (16 loads, 16 KiB per wave) in flight per batch; chunks
+  // past the row end are read clamped and weighted by zero.
+  constexpr int kU = 4;
+  for (int c0 = lane; c0 < nch; c0 += 64 * kU) {
+    hv8 wv[kU][4];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        wv[u][r] = *reinterpret_cast<const hv8*>(wr[r] + 8 * min(c0 + 64 * u, nch - 1));
+    // every load of the batch is issued before the first use (no branch between them)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int c = min(c0 + 64 * u, nch - 1);
+      const bool in = c0 + 64 * u < nch;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        hv8 xv = *reinterpret_cast<const hv8*>(xs + m * K + 8 * c);
+        if (!in) xv = hv8{};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][m] = __builtin_fmaf((float)wv[u][r][e], (float)xv[e], acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = nr0 + 4 * w + r;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float s = wave_sum(acc[r][m]);
+      if (lane == m && n < N && m < P.m) {
+        float y = epilogue(P, s, m, n);
+        asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+        P.c[(int64_t)m * N + n] = (_Float16)y;
+      }
+    }
+  }
+}
+
+// [K,N] weights: a workgroup owns 512 columns (a kilobyte of each k row, lane l the 8
+// columns 8 l .. 8 l + 7) over the k rows of its K part; wave w takes k rows k0 + w, + 4, ...,
+// so every load instruction reads one contiguous kilobyte and each lane accumulates its own
+// columns with no cross-lane reduction.  The 4 wave partials are added in wave order.  With
+// K split over workgroups (P.splits > 1) each part stores fp32 sums to the workspace and
+// splitk_reduce_kernel adds the parts in order and applies the epilogue.
+template <int M>
+__global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
+  __shared__ __attribute__((aligned(16))) _Float16 xs[kGvLdsHalfs];
+  __shared__ __attribute__((aligned(16))) float red[4][M][kGvColsKN];
+  const int t = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProblems; ++i)
+    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  const Prob& P = bt.p[pi];
+  const int N = P.n, K = P.k;
+  int lt = t - P.tile_begin;
+  const int part = lt % P.splits;
+  lt /= P.splits;
+  const int n0 = lt * kGvColsKN;
+  const int k0 = part * P.k_per_split, kn = min(K, k0 + P.k_per_split) - k0;
+  const int xstride = P.k_per_split;
+  gv_stage_x(xs, P, k0, kn, xstride);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int col = min(n0 + 8 * lane, N - 8);
+  float acc[M][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
+  const _Float16* wp = P.b + (int64_t)k0 * N + col;
+  // 16 k rows per lane (16 KiB per wave) in flight per batch; rows past the part are read
+  // clamped and weighted by zero.
+  constexpr int kU = 16;
+  for (int kb = w; kb < kn; kb += 4 * kU) {
+    hv8 wv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      wv[u] = *reinterpret_cast<const hv8*>(wp + (int64_t)min(kb + 4 * u, kn - 1) * N);
+    // every load of the batch is issued before the first use (no branch between them)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = min(kb + 4 * u, kn - 1);
+      const bool in = kb + 4 * u < kn;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float xm = in ? (float)xs[m * xstride + k] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][e] = __builtin_fmaf((float)wv[u][e], xm, acc[m][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    *reinterpret_cast<f4*>(&red[w][m][8 * lane]) = f4{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+    *reinterpret_cast<f4*>(&red[w][m][8 * lane + 4]) = f4{acc[m][4], acc[m][5], acc[m][6], acc[m][7]};
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < P.m * kGvColsKN; i += 256) {
+    const int m = i / kGvColsKN, cc = i - m * kGvColsKN, n = n0 + cc;
+    if (n >= N) continue;
+    const float s = ((red[0][m][cc] + red[1][m][cc]) + red[2][m][cc]) + red[3][m][cc];
+    if (P.splits > 1) {
+      P.ws[((int64_t)part * P.m + m) * N + n] = s;
+    } else {
+      float y = epilogue(P, s, m, n);
+      asm volatile("" : "+v"(y));
+      P.c[(int64_t)m * N + n] = (_Float16)y;
+    }
+  }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 struct Config {
   int bm, bn;
-  bool big;  // gemm_big_kernel (256x256 tiles, no K splits)
+  bool big;         // gemm_big_kernel (256x256 tiles, no K splits)
+  bool rm = false;  // gemm_rm_kernel (bm x bn tiles, K split over its waves, no workspace)
+  bool kn = false;  // ... with [K,N] weights
+  int gv = 0;       // gemv_{nk,kn}_kernel<gv> (M <= gv <= 4), 0: not this path
 };
 
 // Tile shape from the largest M of the batch (all problems of one launch share it).
@@ -675,6 +1046,68 @@ bool big_eligible(const Batch& bt, int max_m) {
   return true;
 }
 
+// gemm_rm_kernel takes a batch of decode-sized problems (M <= 128) when every non-empty
+// problem has 16-byte aligned rows with K a multiple of 8 (and N one for [K,N] weights),
+// N >= 8, one weight layout, operands below 4 GiB (32-bit DMA offsets), and the batch
+// fills the CUs with tiles: it then streams the weights through LDS without a workspace.
+// The tile is the largest of 64 x 64, 32 x 64 and 32 x 32 ([K,N]: 64 columns) that
+// still gives every CU a workgroup.
+constexpr int kRmMaxM = 128;
+
+bool rm_config(const Batch& bt, int max_m, Config& cfg) {
+  if (max_m < 1 || max_m > kRmMaxM) return false;
+  int kn = -1;
+  for (int i = 0; i < bt.n; ++i) {
+    const Prob& P = bt.p[i];
+    if (P.m == 0 || P.n == 0) continue;
+    if (!P.vec || P.n < 8 || (P.k > 0 && P.k < 8)) return false;
+    if (kn >= 0 && kn != P.b_kn) return false;
+    kn = P.b_kn;
+    if ((int64_t)P.m * P.k * 2 >= 0xFFFFFFFFLL || (int64_t)P.n * P.k * 2 >= 0xFFFFFFFFLL) return false;
+  }
+  if (kn < 0) return false;
+  const int cus = device_cus();
+  const int shapes[3][2] = {{64, 64}, {32, 64}, {32, 32}};
+  int pick = -1;
+  for (int c = 0; c < 3; ++c) {
+    const int bm = shapes[c][0], bn = shapes[c][1];
+    if (bm == 64 && max_m <= 32) continue;
+    if (kn && bn != 64) continue;
+    int64_t tiles = 0;
+    for (int i = 0; i < bt.n; ++i) {
+      const Prob& P = bt.p[i];
+      if (P.m == 0 || P.n == 0) continue;
+      tiles += (int64_t)((P.m + bm - 1) / bm) * ((P.n + bn - 1) / bn);
+    }
+    if (tiles >= cus) {
+      pick = c;
+      break;
+    }
+  }
+  if (pick < 0) return false;  // too few tiles: the K-split kernel fills the CUs better
+  cfg = Config{shapes[pick][0], shapes[pick][1], false, true, kn == 1};
+  return true;
+}
+
+// The GEMV kernels take a batch of at most 4 rows when every non-empty problem has 16-byte
+// aligned rows, K (and N for [K,N]) a multiple of 8, N >= 8 and one weight layout, and
+// (for [N,K]) the activation rows fit the 64 KiB staging buffer.
+bool gv_config(const Batch& bt, int max_m, Config& cfg) {
+  if (max_m < 1 || max_m > kGvMaxM) return false;
+  int kn = -1;
+  for (int i = 0; i < bt.n; ++i) {
+    const Prob& P = bt.p[i];
+    if (P.m == 0 || P.n == 0) continue;
+    if (!P.vec || P.n < 8 || P.k < 8) return false;
+    if (kn >= 0 && kn != P.b_kn) return false;
+    kn = P.b_kn;
+    if (!P.b_kn && (int64_t)max_m * P.k > kGvLdsHalfs) return false;
+  }
+  if (kn < 0) return false;
+  cfg = Config{1, kn ? kGvColsKN : kGvRowsNK, false, false, kn == 1, max_m <= 2 ? max_m : 4};
+  return true;
+}
+
 int64_t plan_big(Batch& bt, BigPlan& pl);
 
 // Fills tiling fields and returns the workspace bytes the batch needs.
@@ -682,6 +1115,53 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
   if (cfg.big) {
     BigPlan pl;
     return plan_big(bt, pl);
+  }
+  if (cfg.gv) {
+    // [K,N]: split K over workgroups until the batch has a workgroup per CU, each part >= 128
+    // k rows (a multiple of 32) whose activation slice fits the staging buffer.
+    int tiles = 0;
+    for (int i = 0; i < bt.n; ++i) {
+      Prob& P = bt.p[i];
+      const bool empty = P.m == 0 || P.n == 0;
+      P.tiles_m = empty ? 0 : 1;
+      P.tiles_n = empty ? 0 : (P.n + cfg.bn - 1) / cfg.bn;
+      tiles += P.tiles_n;
+    }
+    int64_t ws = 0;
+    int begin = 0;
+    for (int i = 0; i < bt.n; ++i) {
+      Prob& P = bt.p[i];
+      P.splits = 1;
+      P.k_per_split = P.k;
+      if (cfg.kn && P.tiles_n > 0) {
+        const int kmax = kGvLdsHalfs / cfg.gv / 32 * 32;  // staging limit, rows of K
+        const int cus = device_cus();
+        int s = tiles > 0 ? (cus + tiles - 1) / tiles : 1;
+        s = std::max(1, std::min({s, 64, P.k / 128}));
+        s = std::max(s, (P.k + kmax - 1) / kmax);
+        const int kps = ((P.k + s - 1) / s + 31) / 32 * 32;
+        P.splits = (P.k + kps - 1) / kps;
+        P.k_per_split = P.splits > 1 ? kps : P.k;
+        if (P.splits > 1) ws += (int64_t)P.splits * P.m * P.n * 4;
+      }
+      P.tile_begin = begin;
+      begin += P.tiles_m * P.tiles_n * P.splits;
+    }
+    return ws;
+  }
+  if (cfg.rm) {
+    int begin = 0;
+    for (int i = 0; i < bt.n; ++i) {
+      Prob& P = bt.p[i];
+      const bool empty = P.m == 0 || P.n == 0;
+      P.tiles_m = empty ? 0 : (P.m + cfg.bm - 1) / cfg.bm;
+      P.tiles_n = empty ? 0 : (P.n + cfg.bn - 1) / cfg.bn;
+      P.splits = 1;
+      P.k_per_split = P.k;
+      P.tile_begin = begin;
+      begin += P.tiles_m * P.tiles_n;
+    }
+    return 0;
   }
   int tiles = 0;
   for (int i = 0; i < bt.n; ++i) {
@@ -811,6 +1291,7 @@ int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, C
   }
   cfg = pick_config(max_m, min_n);
   if (big_eligible(bt, max_m)) cfg = Config{kBigBM, kBigBM, true};
+  else if (!gv_config(bt, max_m, cfg)) rm_config(bt, max_m, cfg);
   return VKWR_OK;
 }
 
@@ -864,6 +1345,31 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
   const int wgs = total_wgs(bt);
   if (wgs == 0) return VKWR_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (cfg.gv) {
+    if (cfg.kn) {
+      if (cfg.gv == 1) hipLaunchKernelGGL(gemv_kn_kernel<1>, dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.gv == 2) hipLaunchKernelGGL(gemv_kn_kernel<2>, dim3(wgs), dim3(256), 0, s, bt);
+      else hipLaunchKernelGGL(gemv_kn_kernel<4>, dim3(wgs), dim3(256), 0, s, bt);
+    } else {
+      if (cfg.gv == 1) hipLaunchKernelGGL(gemv_nk_kernel<1>, dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.gv == 2) hipLaunchKernelGGL(gemv_nk_kernel<2>, dim3(wgs), dim3(256), 0, s, bt);
+      else hipLaunchKernelGGL(gemv_nk_kernel<4>, dim3(wgs), dim3(256), 0, s, bt);
+    }
+    if (int e = check_launch(fn)) return e;
+    if (any_split) {
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(256, bt.n), dim3(256), 0, s, bt);
+      if (int e = check_launch(fn)) return e;
+    }
+    return VKWR_OK;
+  }
+  if (cfg.rm) {
+    if (cfg.kn && cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, true>), dim3(wgs), dim3(256), 0, s, bt);
+    else if (cfg.kn) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, true>), dim3(wgs), dim3(256), 0, s, bt);
+    else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, false>), dim3(wgs), dim3(256), 0, s, bt);
+    else if (cfg.bn == 64) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, false>), dim3(wgs), dim3(256), 0, s, bt);
+    else hipLaunchKernelGGL((gemm_rm_kernel<1, 1, false>), dim3(wgs), dim3(512), 0, s, bt);
+    return check_launch(fn);
+  }
   if (cfg.big) {
     BigPlan pl;
     plan_big(bt, pl);  // same plan as above (need)
