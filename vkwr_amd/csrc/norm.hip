@@ -25,6 +25,35 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxC = 8192;
 
+// Sum over the 64 lanes of a wave with DPP (pairs, quads, 8, 16, then the row broadcasts
+// into the last row); the total is read from lane 63.  Fixed order, deterministic.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+#define VK_DPP_ADD(ctrl, rows)                                                                                 \
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rows, 0xF, false))
+  VK_DPP_ADD(0xB1, 0xF);   // quad_perm [1,0,3,2]
+  VK_DPP_ADD(0x4E, 0xF);   // quad_perm [2,3,0,1]
+  VK_DPP_ADD(0x141, 0xF);  // row_half_mirror: 8-lane sums
+  VK_DPP_ADD(0x140, 0xF);  // row_mirror: 16-lane (row) sums
+  VK_DPP_ADD(0x142, 0xA);  // row_bcast15 into rows 1 and 3: 32-lane sums there
+  VK_DPP_ADD(0x143, 0xC);  // row_bcast31 into rows 2 and 3: the 64-lane sum in row 3
+#undef VK_DPP_ADD
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Workgroup sum: DPP wave sums, then the wave totals added in wave order.  The barrier waits
+// only for LDS traffic (loads of the row's other inputs may stay in flight); each call site
+// has its own `red` slots, so no barrier is needed after the read.
+template <int NW>
+__device__ __forceinline__ float block_sum_ln(float v, float* red) {
+  v = wave_sum_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) t += red[w];
+  return t;
+}
+
 struct LnArgs {
   int C;
   int64_t rows;
@@ -66,8 +95,13 @@ __device__ __forceinline__ float ld_in(const void* p, int64_t i) {
 // NP > 0: x comes as NP fp32 K-part planes (vector path only).
 template <int VW, int NV, int NMIX, bool kBf16, int NP = 0>
 __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
-  __shared__ float red[kWaves];
-  const int64_t row = blockIdx.x;
+  __shared__ float red[2][kWaves];
+  // Frag outputs: 8 consecutive rows share each 128-byte line of the output, so those rows
+  // are given to workgroups of one XCD (workgroup b runs on XCD b % 8): row block x of
+  // rows / 8 rows goes to XCD x, and the partial-line stores meet in one L2.
+  const int64_t row = (p.out_frag && (p.rows & 7) == 0)
+                          ? (int64_t)(blockIdx.x & 7) * (p.rows >> 3) + (blockIdx.x >> 3)
+                          : (int64_t)blockIdx.x;
   const int tid = threadIdx.x;
   const int C = p.C;
   const int64_t xrow = p.x_rows ? (int64_t)p.x_rows[row] : row * p.src_mul + p.src_add;
@@ -157,7 +191,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       for (int e = 0; e < VW; ++e) sum += v[n][e];
     }
   }
-  const float mean = block_sum<kWaves>(sum, red) / (float)C;
+  const float mean = block_sum_ln<kWaves>(sum, red[0]) / (float)C;
   float ss = 0.0f;
 #pragma unroll
   for (int n = 0; n < NV; ++n) {
@@ -170,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       }
     }
   }
-  const float rstd = rsqrtf(block_sum<kWaves>(ss, red) / (float)C + p.eps);
+  const float rstd = rsqrtf(block_sum_ln<kWaves>(ss, red[1]) / (float)C + p.eps);
 
 #pragma unroll
   for (int n = 0; n < NV; ++n) {
