@@ -571,24 +571,13 @@ __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
     return;
   }
   float* S = p.pool + ((size_t)sl * p.H + h) * (kHead * kHead);
+  // The lane's token and channel inputs are requested first and the state right after
+  // them, before any arithmetic: the gate's reductions then run while the state is in
+  // flight (every wave of the launch starts at once; with the loads after the gate the
+  // memory would sit idle meanwhile), and waiting for an input never waits for the state.
   const _Float16 xr = p.r[tok], xw = p.w[tok], xv = p.v[tok];
-  const float kv = (float)p.k[tok], a12 = (float)p.a12[tok];
-  // kk / a gate
-  const float u = kv * (float)p.k_k[c];
-  const float inv = 1.0f / fmaxf(sqrtf(wave_sum_prod(u, u)), kKkEps);
-  const float kk = u * inv;
-  const float a = sigmoidf((float)p.a0[c] + a12);
-  const float ka = (float)p.k_a[c];
-  const _Float16 new_k = f16_of(kv * __builtin_fmaf(a, ka, 1.0f - ka));
-  const _Float16 neg_kk = (_Float16)(-kk);
-  const _Float16 kka = f16_of(kk * a);
-  // The r.k bonus does not depend on the WKV output: reduce it now (a
-  // wave-uniform scalar) so r and new_k need not stay live across the state phase.
-  const float rkv = wave_sum_prod((float)xr * (float)new_k, (float)p.r_k[c]);
-  // WKV-7 (the channel vectors go to LDS first: only v stays in a register
-  // across the state load)
-  token_stage(vb, lane, xr, xw, new_k, neg_kk, kka);
-  const float vi = (float)xv;
+  const _Float16 xk = p.k[tok], xa12 = p.a12[tok];
+  const _Float16 pk_k = p.k_k[c], pa0 = p.a0[c], pk_a = p.k_a[c], pr_k = p.r_k[c];
   float s[kHead];
   if constexpr (kIlv) {
 #pragma unroll
@@ -600,6 +589,26 @@ __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
       s[4 * q + 2] = x.z;
       s[4 * q + 3] = x.w;
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float kv = (float)xk, a12 = (float)xa12;
+  // kk / a gate
+  const float u = kv * (float)pk_k;
+  const float inv = 1.0f / fmaxf(sqrtf(wave_sum_prod(u, u)), kKkEps);
+  const float kk = u * inv;
+  const float a = sigmoidf((float)pa0 + a12);
+  const float ka = (float)pk_a;
+  const _Float16 new_k = f16_of(kv * __builtin_fmaf(a, ka, 1.0f - ka));
+  const _Float16 neg_kk = (_Float16)(-kk);
+  const _Float16 kka = f16_of(kk * a);
+  // The r.k bonus does not depend on the WKV output: reduce it now (a
+  // wave-uniform scalar) so r and new_k need not stay live across the state phase.
+  const float rkv = wave_sum_prod((float)xr * (float)new_k, (float)pr_k);
+  // WKV-7 (the channel vectors go to LDS first: only v stays in a register
+  // across the state load)
+  token_stage(vb, lane, xr, xw, new_k, neg_kk, kka);
+  const float vi = (float)xv;
+  if constexpr (kIlv) {
     __syncthreads();  // orders the vb writes before token_run's broadcast reads
   } else {
     load_state_fp32(S, st, s, lane);  // its barriers also order the vb writes
