@@ -329,6 +329,24 @@ def ops_small_m(dev, calls, warmup=3):
         out[f"m1_linear_f16_orig_K{K}_N{N}"] = {"us": round(us, 2), "weight_GBps": round(gbs, 1),
                                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         del ws
+    # the activation-sparse FFN down projection at M = 1: relu^2 of a N(0,1) pre-activation
+    # leaves about half of the F rows zero, and only the other rows of value_fc are read
+    from vkwr._ops.v1 import v1_mix_ops as MX
+    for (C, F) in ((2048, 8192), (4096, 16384)):
+        ws = copies((F, C))
+        pre = torch.randn(F, device=dev, generator=g).half()
+        live = int((pre > 0).sum())
+        us = timed(lambda i: MX.cmix_sparse_down_relu_one(C, F, pre, ws[i % len(ws)]), calls)
+        dense_x = pre.view(1, F).abs() + 0.01  # no zero row
+        us_dense = timed(lambda i: L.linear_f16(dense_x, ws[i % len(ws)]), calls)
+        read = live * C * 2
+        out[f"m1_cmix_sparse_down_relu_one_C{C}_F{F}"] = {
+            "us": round(us, 2), "rows_read_frac": round(live / F, 4),
+            "read_GBps": round(read / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(read / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "dense_weight_GBps": round(F * C * 2 / (us * 1e-6) / 1e9, 1),
+            "dense_activation_us": round(us_dense, 2)}
+        del ws
     for (K, N, role) in ((2048, 2048, "r/k/v/o"), (2048, 8192, "ffn_key"), (8192, 2048, "ffn_value")):
         ws = copies((N, K))
         x = torch.randn(128, K, device=dev, generator=g).half()
@@ -353,7 +371,10 @@ def ops_small_m(dev, calls, warmup=3):
     return {
         "workload": "vkwr_v1_linear ops through torch.ops at M=1 ([K,N] weights, linear_f16) and M=128 "
                     "([N,K] weights, linear_f16_orig), weights cold (rotated over >= 512 MiB of copies); "
-                    "frag_path_us: the decode driver's frag GEMM on the same M=128 shapes (unpadded, one call)",
+                    "frag_path_us: the decode driver's frag GEMM on the same M=128 shapes (unpadded, one call); "
+                    "m1_cmix_sparse_down_relu_one: vkwr_v1_mix's activation-sparse FFN down projection, "
+                    "relu^2 of an N(0,1) pre-activation (read bytes = nonzero rows x C x 2; "
+                    "dense_activation_us: the same GEMV with no zero row)",
         "calls": calls,
         "shapes": out,
         "timing": "each shape's calls captured into one HIP graph and replayed; HIP events on the replay "

@@ -241,7 +241,8 @@ def test_cmix_down_ops(gpu):
         y2 = fn(B, T, C, F, dev(pre, gpu), dev(value, gpu))
         assert torch.equal(y2, y)
     y1 = M.cmix_sparse_down_one(C, F, dev(act[0, 0], gpu), dev(value, gpu))
-    assert y1.shape == (1, 1, C) and torch.equal(y1.view(C), y[0, 0])
+    assert y1.shape == (1, 1, C)
+    check(y1.view(1, C), ref[:1], ACC * abs_sum[:1], "down_one")
     y1r = M.cmix_sparse_down_relu_one(C, F, dev(pre[0, 0], gpu), dev(value, gpu))
     assert torch.equal(y1r, y1)
     with pytest.raises(RuntimeError):
@@ -250,6 +251,47 @@ def test_cmix_down_ops(gpu):
         x100 = dev(h(1, 1, 100), gpu)
         M.cmix_sparse_one(100, 128, x100, dev(h(1, 100), gpu), dev(h(100), gpu), dev(h(128, 100), gpu),
                           dev(h(128, 100), gpu))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 8192, 2048), (2, 16384, 4096), (4, 1032, 1000), (1, 2048, 65536)])
+def test_gemv_kn_skips_zero_activation_rows(gpu, M, K, N):
+    """The [K,N] GEMV reads only the weight rows where some activation row is nonzero (the
+    reference's activation-sparse down projection, mix_ops.cu:522-583): weight rows under an
+    all-zero activation column are filled with NaN here, and the result must still be the
+    dense product of the remaining rows.  Zeros are +0 and -0 alike; the pattern has
+    runs of zeros longer and shorter than a wave's 64-row ballot, and one K part with no
+    nonzero row at all."""
+    from vkwr._ops.v1 import v1_linear_ops as L
+    a = h(M, K)
+    live = rng.random(K) < 0.3
+    live[: min(K, 700)] = False        # a run of zero rows across ballots and K parts
+    live[K // 2: K // 2 + 5] = True
+    a[:, ~live] = 0.0
+    a[0, ~live & (np.arange(K) % 3 == 0)] = np.float16(-0.0)
+    if M > 1:
+        # a row live in only one of the activation rows is still read
+        a[1:, K // 2] = 0.0
+    w = h(K, N, scale=0.05)
+    ref, abs_sum = R.gemm(a, w, "kn")
+    w[~live, :] = np.nan
+    y = L.linear_f16(dev(a, gpu), dev(w, gpu))
+    assert torch.isfinite(y).all()
+    check(y, ref, ACC * abs_sum, f"sparse kn {M}x{K}x{N}")
+    z = L.linear_f16(dev(np.zeros((M, K), np.float16), gpu), dev(w, gpu))
+    assert torch.equal(z, torch.zeros_like(z))
+
+
+def test_cmix_down_relu_one_sparse_shapes(gpu):
+    """cmix_sparse_down_relu_one at the 1.5B and 7B FFN shapes (relu^2 leaves about half
+    of the rows zero) against the oracle."""
+    from vkwr._ops.v1 import v1_mix_ops as M
+    for C, F in ((2048, 8192), (4096, 16384)):
+        pre = h(F)
+        value = h(F, C, scale=0.05)
+        act = R.relu_square(pre)
+        ref, abs_sum = R.gemm(act.reshape(1, F), value, "kn")
+        y = M.cmix_sparse_down_relu_one(C, F, dev(pre, gpu), dev(value, gpu))
+        check(y.view(1, C), ref, ACC * abs_sum, f"down_relu_one {C}x{F}")
 
 
 # ---------------------------------------------------------------- large-M path

@@ -333,21 +333,51 @@ __global__ __launch_bounds__(256) void gemm_kernel(Batch bt) {
   }
 }
 
-// Adds the K-split partials of every split problem in split order and applies
-// the epilogue.  blockIdx.y = problem index.
+// Adds the K-split partials of every split problem and applies the epilogue.
+// blockIdx.y = problem index.  A workgroup takes 64 consecutive outputs at a time; wave w
+// adds the parts [w q, w q + q) (q = ceil(splits / 4)) in part order, with 8 loads in
+// flight per step, and the 4 wave sums are added in wave order.  The order is fixed, so
+// results are run-to-run identical, and a 64-part split costs two round trips to memory
+// instead of 64.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(Batch bt) {
+  __shared__ float wsum[4][64];
   const Prob& P = bt.p[blockIdx.y];
   if (P.splits <= 1) return;
   const int64_t mn = (int64_t)P.m * P.n;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
-    float s = P.ws[i];
-    for (int z = 1; z < P.splits; ++z) s += P.ws[z * mn + i];
-    const int row = (int)(i / P.n), col = (int)(i % P.n);
-    float y = epilogue(P, s, row, col);
-    asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
-    P.c[i] = (_Float16)y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q = (P.splits + 3) / 4;
+  const int z0 = min(P.splits, w * q), z1 = min(P.splits, z0 + q);
+  for (int64_t i0 = (int64_t)blockIdx.x * 64; i0 < mn; i0 += (int64_t)gridDim.x * 64) {
+    const int64_t i = min(i0 + lane, mn - 1);
+    float s = 0.0f;
+    for (int z = z0; z < z1; z += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = P.ws[(int64_t)min(z + u, z1 - 1) * mn + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (z + u < z1) s += v[u];
+    }
+    wsum[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && i0 + lane < mn) {
+      const float t = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
+      const int row = (int)(i / P.n), col = (int)(i % P.n);
+      float y = epilogue(P, t, row, col);
+      asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
+      P.c[i] = (_Float16)y;
+    }
+    __syncthreads();
   }
+}
+
+// Workgroups of splitk_reduce_kernel: one per 64 outputs of the largest split problem,
+// at most 1024 (they loop beyond).
+int reduce_wgs(const Batch& bt) {
+  int64_t mn = 0;
+  for (int i = 0; i < bt.n; ++i)
+    if (bt.p[i].splits > 1) mn = std::max(mn, (int64_t)bt.p[i].m * bt.p[i].n);
+  return (int)std::min<int64_t>(1024, std::max<int64_t>(1, (mn + 63) / 64));
 }
 
 // ---- large-M path (prefill / mixed batches): 256x256 output tiles, matrix-core bound.
@@ -856,6 +886,7 @@ constexpr int kGvMaxM = 4;
 constexpr int kGvLdsHalfs = 32768;  // 64 KiB
 constexpr int kGvRowsNK = 16;       // [N,K]: weight rows per workgroup (4 per wave)
 constexpr int kGvColsKN = 512;      // [K,N]: columns per workgroup (a kilobyte of each k row)
+constexpr int kGvRowsKN = 8192;     // [K,N]: most k rows of one workgroup's K part
 
 __device__ __forceinline__ void gv_stage_x(_Float16* xs, const Prob& P, int k0, int kn, int stride) {
   // x[m][k0 .. k0 + kn) -> xs[m * stride + ...], 16 bytes per thread and step (kn % 8 == 0)
@@ -940,15 +971,21 @@ __global__ __launch_bounds__(256) void gemv_nk_kernel(Batch bt) {
 }
 
 // [K,N] weights: a workgroup owns 512 columns (a kilobyte of each k row, lane l the 8
-// columns 8 l .. 8 l + 7) over the k rows of its K part; wave w takes k rows k0 + w, + 4, ...,
-// so every load instruction reads one contiguous kilobyte and each lane accumulates its own
-// columns with no cross-lane reduction.  The 4 wave partials are added in wave order.  With
-// K split over workgroups (P.splits > 1) each part stores fp32 sums to the workspace and
-// splitk_reduce_kernel adds the parts in order and applies the epilogue.
+// columns 8 l .. 8 l + 7) over the k rows of its K part, and wave w the w-th quarter of those
+// rows.  Only the k rows where some activation row is nonzero are read: each wave first
+// lists its nonzero rows in LDS (a ballot per 64 rows), then streams those weight rows,
+// every load instruction one contiguous kilobyte, and each lane accumulates its own columns
+// in row order with no cross-lane reduction.  This is the reference's activation-sparse
+// down projection (a relu^2 activation is zero for about half of the rows); a zero row adds
+// exact zeros, so for finite weights the sum is the dense product's.  The 4 wave partials
+// are added in wave order.  With K split over workgroups (P.splits > 1) each part stores
+// fp32 sums to the workspace and splitk_reduce_kernel adds the parts in order and applies
+// the epilogue.
 template <int M>
 __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
-  __shared__ __attribute__((aligned(16))) _Float16 xs[kGvLdsHalfs];
+  __shared__ __attribute__((aligned(16))) _Float16 xs[M * kGvRowsKN];
   __shared__ __attribute__((aligned(16))) float red[4][M][kGvColsKN];
+  __shared__ unsigned short nz[kGvRowsKN];  // wave w's list starts at w * q
   const int t = blockIdx.x;
   int pi = 0;
 #pragma unroll
@@ -965,6 +1002,25 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
   gv_stage_x(xs, P, k0, kn, xstride);
   __syncthreads();
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // this wave's rows [r0, r1) of the part, and the nonzero ones among them
+  const int q = (kn + 3) / 4;
+  const int r0 = min(kn, w * q), r1 = min(kn, r0 + q);
+  unsigned short* list = nz + w * q;
+  int cnt = 0;
+  for (int rb = r0; rb < r1; rb += 64) {
+    const int r = rb + lane;
+    bool on = false;
+    if (r < r1) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        on |= (__builtin_bit_cast(unsigned short, xs[m * xstride + r]) & 0x7fff) != 0;
+    }
+    const uint64_t msk = __builtin_amdgcn_ballot_w64(on);
+    const int at = cnt + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(msk >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)msk, 0u));
+    if (on) list[at] = (unsigned short)r;
+    cnt += __builtin_popcountll(msk);
+  }
   const int col = min(n0 + 8 * lane, N - 8);
   float acc[M][8];
 #pragma unroll
@@ -972,23 +1028,24 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
   const _Float16* wp = P.b + (int64_t)k0 * N + col;
-  // 16 k rows per lane (16 KiB per wave) in flight per batch; rows past the part are read
-  // clamped and weighted by zero.
+  // 16 listed rows per lane (16 KiB per wave) in flight per batch; entries past the list end
+  // read its last row again and are weighted by zero.
   constexpr int kU = 16;
-  for (int kb = w; kb < kn; kb += 4 * kU) {
+  for (int i0 = 0; i0 < cnt; i0 += kU) {
+    int rows[kU];
     hv8 wv[kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
-      wv[u] = *reinterpret_cast<const hv8*>(wp + (int64_t)min(kb + 4 * u, kn - 1) * N);
+    for (int u = 0; u < kU; ++u) rows[u] = list[min(i0 + u, cnt - 1)];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) wv[u] = *reinterpret_cast<const hv8*>(wp + (int64_t)rows[u] * N);
     // every load of the batch is issued before the first use (no branch between them)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int k = min(kb + 4 * u, kn - 1);
-      const bool in = kb + 4 * u < kn;
+      const bool in = i0 + u < cnt;
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float xm = in ? (float)xs[m * xstride + k] : 0.0f;
+        const float xm = in ? (float)xs[m * xstride + rows[u]] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[m][e] = __builtin_fmaf((float)wv[u][e], xm, acc[m][e]);
       }
@@ -1134,7 +1191,7 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
       P.splits = 1;
       P.k_per_split = P.k;
       if (cfg.kn && P.tiles_n > 0) {
-        const int kmax = kGvLdsHalfs / cfg.gv / 32 * 32;  // staging limit, rows of K
+        const int kmax = kGvRowsKN;  // staging and row-list limit, rows of K
         const int cus = device_cus();
         int s = tiles > 0 ? (cus + tiles - 1) / tiles : 1;
         s = std::max(1, std::min({s, 64, P.k / 128}));
@@ -1357,7 +1414,7 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
     }
     if (int e = check_launch(fn)) return e;
     if (any_split) {
-      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(256, bt.n), dim3(256), 0, s, bt);
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_wgs(bt), bt.n), dim3(256), 0, s, bt);
       if (int e = check_launch(fn)) return e;
     }
     return VKWR_OK;
@@ -1402,7 +1459,7 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
   else hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2>), dim3(wgs), dim3(256), 0, s, bt);
   if (int e = check_launch(fn)) return e;
   if (any_split) {
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(256, bt.n), dim3(256), 0, s, bt);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_wgs(bt), bt.n), dim3(256), 0, s, bt);
     if (int e = check_launch(fn)) return e;
   }
   return VKWR_OK;
