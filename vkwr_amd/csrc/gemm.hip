@@ -971,21 +971,21 @@ __global__ __launch_bounds__(256) void gemv_nk_kernel(Batch bt) {
 }
 
 // [K,N] weights: a workgroup owns 512 columns (a kilobyte of each k row, lane l the 8
-// columns 8 l .. 8 l + 7) over the k rows of its K part, and wave w the w-th quarter of those
-// rows.  Only the k rows where some activation row is nonzero are read: each wave first
-// lists its nonzero rows in LDS (a ballot per 64 rows), then streams those weight rows,
-// every load instruction one contiguous kilobyte, and each lane accumulates its own columns
-// in row order with no cross-lane reduction.  This is the reference's activation-sparse
-// down projection (a relu^2 activation is zero for about half of the rows); a zero row adds
+// columns 8 l .. 8 l + 7) over the k rows of its K part, wave w the rows w, w + 4, ...
+// Only the k rows where some activation row is nonzero are read: each wave first lists
+// its nonzero rows in LDS (a ballot per 64 rows), then streams those weight rows, every
+// load instruction one contiguous kilobyte, and each lane accumulates its own columns in
+// row order with no cross-lane reduction.  This is the reference's activation-sparse down
+// projection (a relu^2 activation is zero for about half of the rows); a zero row adds
 // exact zeros, so for finite weights the sum is the dense product's.  The 4 wave partials
 // are added in wave order.  With K split over workgroups (P.splits > 1) each part stores
-// fp32 sums to the workspace and splitk_reduce_kernel adds the parts in order and applies
-// the epilogue.
+// fp32 sums to the workspace and splitk_reduce_kernel adds the parts and applies the
+// epilogue.
 template <int M>
 __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
   __shared__ __attribute__((aligned(16))) _Float16 xs[M * kGvRowsKN];
   __shared__ __attribute__((aligned(16))) float red[4][M][kGvColsKN];
-  __shared__ unsigned short nz[kGvRowsKN];  // wave w's list starts at w * q
+  __shared__ __attribute__((aligned(16))) unsigned short nz[kGvRowsKN];  // wave w's list at w * q16
   const int t = blockIdx.x;
   int pi = 0;
 #pragma unroll
@@ -1003,14 +1003,14 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
   __syncthreads();
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   // this wave's rows [r0, r1) of the part, and the nonzero ones among them
-  const int q = (kn + 3) / 4;
-  const int r0 = min(kn, w * q), r1 = min(kn, r0 + q);
-  unsigned short* list = nz + w * q;
+  const int q16 = ((kn + 3) / 4 + 15) & ~15;
+  const int nw = kn > w ? (kn - w + 3) / 4 : 0;  // this wave's rows w, w + 4, ...
+  unsigned short* list = nz + w * q16;
   int cnt = 0;
-  for (int rb = r0; rb < r1; rb += 64) {
-    const int r = rb + lane;
+  for (int jb = 0; jb < nw; jb += 64) {
+    const int r = w + 4 * (jb + lane);
     bool on = false;
-    if (r < r1) {
+    if (jb + lane < nw) {
 #pragma unroll
       for (int m = 0; m < M; ++m)
         on |= (__builtin_bit_cast(unsigned short, xs[m * xstride + r]) & 0x7fff) != 0;
@@ -1021,6 +1021,10 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
     if (on) list[at] = (unsigned short)r;
     cnt += __builtin_popcountll(msk);
   }
+  // the list padded to a multiple of 16 with its last row (weighted by zero below), so a
+  // batch reads its 16 entries as two 16-byte LDS loads
+  if (cnt > 0 && lane < ((16 - (cnt & 15)) & 15)) list[cnt + lane] = list[cnt - 1];
+  const bool dense = cnt == nw;  // no zero row: the rows are w, w + 4, ...
   const int col = min(n0 + 8 * lane, N - 8);
   float acc[M][8];
 #pragma unroll
@@ -1034,8 +1038,16 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
   for (int i0 = 0; i0 < cnt; i0 += kU) {
     int rows[kU];
     hv8 wv[kU];
+    if (dense) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u) rows[u] = list[min(i0 + u, cnt - 1)];
+      for (int u = 0; u < kU; ++u) rows[u] = w + 4 * min(i0 + u, cnt - 1);
+    } else {
+      const uint4 l0 = *reinterpret_cast<const uint4*>(list + i0);
+      const uint4 l1 = *reinterpret_cast<const uint4*>(list + i0 + 8);
+      const unsigned lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+#pragma unroll
+      for (int u = 0; u < kU; ++u) rows[u] = (lw[u >> 1] >> (16 * (u & 1))) & 0xffff;
+    }
 #pragma unroll
     for (int u = 0; u < kU; ++u) wv[u] = *reinterpret_cast<const hv8*>(wp + (int64_t)rows[u] * N);
     // every load of the batch is issued before the first use (no branch between them)
