@@ -154,3 +154,33 @@ def test_validate_slots_host_check():
         v1_wkv_ops.validate_slots(torch.tensor([4], dtype=torch.int32), 4)
     with pytest.raises(RuntimeError):
         v1_wkv_ops.validate_slots(torch.tensor([-1], dtype=torch.int32), 4)
+
+
+@pytest.mark.parametrize("slots", [[3, 3], [4], [-1, 0]], ids=["duplicate", "past_end", "negative"])
+def test_slot_ops_raise_on_bad_slots_by_default(slots):
+    """The slot-pool WKV wrappers check the slot table before any launch (the dispatcher
+    would reject these CPU tensors only afterwards, with NotImplementedError)."""
+    B, H = len(slots), 1
+    C = 64 * H
+    pool = torch.zeros(4, H, 64, 64)
+    ins = [torch.zeros(B, C, dtype=torch.float16) for _ in range(6)]
+    sl = torch.tensor(slots, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="slot"):
+        v1_wkv_ops.wkv_one_slots_fp32(B, C, H, pool, sl, *ins)
+    with pytest.raises(RuntimeError, match="slot"):
+        v1_wkv_ops.wkv_forward_slots_fp32(B, 1, C, H, pool, sl, *(x.view(B, 1, C) for x in ins))
+    with pytest.raises(NotImplementedError):  # validate=False: straight to the (GPU-only) op
+        v1_wkv_ops.wkv_one_slots_fp32(B, C, H, pool, sl, *ins, validate=False)
+
+
+def test_slot_allocator_rejects_double_free_and_foreign_slots():
+    from vkwr.model_executor.scheduler import SlotAllocator
+    a = SlotAllocator(3)
+    s = [a.alloc() for _ in range(3)]
+    assert sorted(s) == [0, 1, 2] and a.alloc() is None
+    a.free(s[1])
+    with pytest.raises(RuntimeError):
+        a.free(s[1])          # double free
+    with pytest.raises(RuntimeError):
+        a.free(7)             # out of range
+    assert a.alloc() == s[1] and a.available == 0

@@ -122,10 +122,16 @@ def validate_slots(slots, pool_size):
         raise RuntimeError("slots must be distinct")
 
 
-def wkv_forward_slots_fp32(B, T, C, H, state_pool, slots, r, w, k, v, a, b, validate=False):
+def wkv_forward_slots_fp32(B, T, C, H, state_pool, slots, r, w, k, v, a, b, validate=True):
     """WKV-7 over T tokens with sequence i's fp32 state read from and written back to
     state_pool[slots[i]] in the same pass (replaces index_select -> wkv_forward_fp32 ->
-    index_copy_).  Entries of state_pool not named by slots are left bitwise unchanged."""
+    index_copy_).  Entries of state_pool not named by slots are left bitwise unchanged.
+
+    Out-of-range or duplicate slots raise RuntimeError before the launch (a host check:
+    the slots are copied to the host).  validate=False skips it, for callers whose slot
+    table is checked on the host already (the continuous batcher's allocator); the kernel
+    then still bounds-checks every slot (an out-of-range slot's y rows are NaN and the pool
+    is untouched), but duplicate slots race."""
     if validate:
         validate_slots(slots, state_pool.size(0))
     y = torch.empty(B, T, C, dtype=r.dtype, device=r.device)
@@ -133,7 +139,7 @@ def wkv_forward_slots_fp32(B, T, C, H, state_pool, slots, r, w, k, v, a, b, vali
     return y
 
 
-def wkv_one_slots_fp32(B, C, H, state_pool, slots, r, w, k, v, a, b, validate=False):
+def wkv_one_slots_fp32(B, C, H, state_pool, slots, r, w, k, v, a, b, validate=True):
     """Decode step (T=1) of wkv_forward_slots_fp32; r..b are [B,C], y is [B,C]."""
     y = wkv_forward_slots_fp32(B, 1, C, H, state_pool, slots,
                                *(x.view(B, 1, C) for x in (r, w, k, v, a, b)), validate=validate)

@@ -43,17 +43,27 @@ class Request:
 
 
 class SlotAllocator:
-    """Free list over the state pool's slots (FIFO reuse)."""
+    """Free list over the state pool's slots (FIFO reuse).  Freeing a slot that is out of
+    range or not allocated raises RuntimeError, so the slot lists the batcher builds from
+    allocated slots are distinct and in range: it checks them on the host and passes
+    them to the kernels without a device-side check."""
 
     def __init__(self, n_slots):
         self.n_slots = n_slots
         self._free = deque(range(n_slots))
+        self._used = set()
 
     def alloc(self):
-        return self._free.popleft() if self._free else None
+        if not self._free:
+            return None
+        slot = self._free.popleft()
+        self._used.add(slot)
+        return slot
 
     def free(self, slot):
-        assert 0 <= slot < self.n_slots
+        if not (0 <= slot < self.n_slots) or slot not in self._used:
+            raise RuntimeError(f"slot {slot} is not allocated (pool of {self.n_slots})")
+        self._used.remove(slot)
         self._free.append(slot)
 
     @property
@@ -95,6 +105,13 @@ class ContinuousBatcher:
     def _i32(self, values):
         return torch.tensor(values, dtype=torch.int32).to(self.device, non_blocking=True)
 
+    def _check_slots(self, reqs):
+        """Host-side slot-table check of one step (no device sync): every slot allocated,
+        each used by one sequence only."""
+        slots = [r.slot for r in reqs]
+        if len(set(slots)) != len(slots) or any(s not in self.slots._used for s in slots):
+            raise RuntimeError(f"invalid slot table for this step: {slots}")
+
     def step(self):
         """Runs one forward step; returns the requests that finished in it."""
         while self.waiting and self.slots.available:
@@ -124,6 +141,7 @@ class ContinuousBatcher:
             n_chunks += 1
         if rows == 0:
             return []
+        self._check_slots(dec + [r for reqs in groups.values() for r in reqs])
         decode = None
         if dec:
             decode = (self._i32([r.output[-1] for r in dec]), self._i32([r.slot for r in dec]))
