@@ -388,7 +388,8 @@ int reduce_wgs(const Batch& bt) {
 // advances 64 per stage through two 64 KiB LDS buffers (A and B tiles of 256 rows x 64):
 //   * the next stage's tiles are copied global -> LDS by the DMA form of the vector load
 //     (global_load_lds_dwordx4: 16 bytes per lane straight into LDS, no VGPR staging),
-//     issued at the start of the current stage; the lanes of one load instruction cover
+//     issued right after the barrier that frees its buffer, so four k16 groups of MFMAs
+//     run before the barrier that waits for it; the lanes of one load instruction cover
 //     8 whole 128-byte rows, and row r's 16-byte chunk c lands at LDS slot
 //     r*8 + (c ^ ((r >> 1) & 7)), so that the fragment reads below touch 16 distinct
 //     16-byte bank groups per 16 lanes (conflict-free);
@@ -571,12 +572,12 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
   };
   dma(0, ks);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  dma(1, ks + 1);
   fread(0, 0, 0);
   int cb = 0;
   for (int s = ks; s < ke; ++s) {
     const int nb = cb ^ 1;
     fread(cb, 1, 1);
-    dma(nb, s + 1);  // buffer nb was last read before the previous barrier
     mfma16(0);
     __builtin_amdgcn_sched_barrier(0);
     fread(cb, 2, 0);
@@ -585,7 +586,9 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
     fread(cb, 3, 1);
     mfma16(0);
     __builtin_amdgcn_sched_barrier(0);
+    // stage s + 1 (buffer nb, issued one stage ago) has landed and buffer cb is read
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    dma(cb, s + 2);  // four k16 groups of MFMAs before the barrier that waits for it
     fread(nb, 0, 0);
     mfma16(1);
     __builtin_amdgcn_sched_barrier(0);
