@@ -388,13 +388,15 @@ int reduce_wgs(const Batch& bt) {
 // advances 64 per stage through two 64 KiB LDS buffers (A and B tiles of 256 rows x 64):
 //   * the next stage's tiles are copied global -> LDS by the DMA form of the vector load
 //     (global_load_lds_dwordx4: 16 bytes per lane straight into LDS, no VGPR staging),
-//     issued right after the barrier that frees its buffer, so four k16 groups of MFMAs
-//     run before the barrier that waits for it; the lanes of one load instruction cover
+//     16 instructions per wave and stage, issued one after every other MFMA of the two
+//     k16 groups that follow the barrier freeing its buffer (a burst of them would stall
+//     the wave's in-order issue of MFMAs), so two to four groups of MFMAs run before the
+//     barrier that waits for them; the lanes of one load instruction cover
 //     8 whole 128-byte rows, and row r's 16-byte chunk c lands at LDS slot
 //     r*8 + (c ^ ((r >> 1) & 7)), so that the fragment reads below touch 16 distinct
 //     16-byte bank groups per 16 lanes (conflict-free);
 //   * fragments for the next k16 group are read (ds_read_b128) while the current group's
-//     16 MFMAs run;
+//     16 MFMAs run, one read after each of the first 8;
 //   * one barrier per stage, after the third group: this wave's DMA has landed
 //     (vmcnt(0)) and its reads of the current buffer are done (lgkmcnt(0)); after the
 //     barrier both hold for every wave, so the next stage's buffer may be read and the
@@ -544,16 +546,26 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  auto dma = [&](int buf, int st) __attribute__((always_inline)) {
+  // read once: the DMA statements clobber memory, so P.a / P.b would be reloaded after each
+  const _Float16* const pa = (const _Float16*)uniform_ptr(P.a);
+  const _Float16* const pb = (const _Float16*)uniform_ptr(P.b);
+  // DMA instruction d (0..15) of a stage: A rows of instruction d / 2 for even d, B for odd
+  auto dma_one = [&](int d, const void* ab, const void* bb, uint32_t la) __attribute__((always_inline)) {
+    if (d & 1) dma16_m0(bb, bo[d >> 1], la + kBigTile * 2 + (d >> 1) * 256 * 16);
+    else dma16_m0(ab, ao[d >> 1], la + (d >> 1) * 256 * 16);
+  };
+  auto stage_src = [&](int st, const void*& ab, const void*& bb) __attribute__((always_inline)) {
     const int k0 = min(st, ke - 1) * kBigBK;  // past the range: re-load its last stage (unused)
-    const void* ab = uniform_ptr(P.a + k0);
-    const void* bb = uniform_ptr(P.b + k0);
-    const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2), lb = la + kBigTile * 2;
+    ab = uniform_ptr(pa + k0);
+    bb = uniform_ptr(pb + k0);
+  };
+  auto dma = [&](int buf, int st, int d0, int d1) __attribute__((always_inline)) {
+    const void *ab, *bb;
+    stage_src(st, ab, bb);
+    const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      dma16_m0(ab, ao[j], la + j * 256 * 16);
-      dma16_m0(bb, bo[j], lb + j * 256 * 16);
-    }
+    for (int d = 0; d < 16; ++d)
+      if (d >= d0 && d < d1) dma_one(d, ab, bb, la);
   };
   hv8 fa[2][4], fb[2][4];
   auto fread = [&](int buf, int kk, int set) __attribute__((always_inline)) {
@@ -563,22 +575,44 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
       fb[set][i] = *reinterpret_cast<const hv8*>(&sm[buf][1][frb[kk][i]]);
     }
   };
+  // 16 MFMAs with the next group's 8 fragment reads interleaved, one after each of the first 8
   auto mfma16 = [&](int set) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   };
-  dma(0, ks);
+  // 16 MFMAs with DMA instructions d0 .. d0 + 7 of stage st (buffer buf) after every other
+  // one: a burst of DMA issues would hold up the wave's in-order issue of the MFMAs
+  auto mfma16_dma = [&](int set, int buf, int st, int d0) __attribute__((always_inline)) {
+    const void *ab, *bb;
+    stage_src(st, ab, bb);
+    const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+        if ((j & 1) == 0) dma_one(d0 + 2 * i + (j >> 1), ab, bb, la);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  };
+  dma(0, ks, 0, 16);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  dma(1, ks + 1);
+  dma(1, ks + 1, 0, 8);
   fread(0, 0, 0);
   int cb = 0;
   for (int s = ks; s < ke; ++s) {
     const int nb = cb ^ 1;
     fread(cb, 1, 1);
-    mfma16(0);
+    mfma16_dma(0, nb, s + 1, 8);  // the second half of stage s + 1
     __builtin_amdgcn_sched_barrier(0);
     fread(cb, 2, 0);
     mfma16(1);
@@ -586,11 +620,10 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
     fread(cb, 3, 1);
     mfma16(0);
     __builtin_amdgcn_sched_barrier(0);
-    // stage s + 1 (buffer nb, issued one stage ago) has landed and buffer cb is read
+    // stage s + 1 (buffer nb) has landed and buffer cb is read
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    dma(cb, s + 2);  // four k16 groups of MFMAs before the barrier that waits for it
     fread(nb, 0, 0);
-    mfma16(1);
+    mfma16_dma(1, cb, s + 2, 0);  // the first half of stage s + 2, into the buffer just freed
     __builtin_amdgcn_sched_barrier(0);
     cb = nb;
   }
