@@ -483,31 +483,78 @@ __device__ __forceinline__ float big_epilogue(const Prob& P, float y, int row, i
   }
 }
 
-// Stores a 256x256 accumulator tile through epilogue kEpi (fp16, clipped to M x N).
+// Epilogue kEpi of 8 consecutive columns of one row (16-byte operand loads), rounded in fp32
+// and then to fp16, the same arithmetic per element as big_epilogue.
 template <int kEpi>
-__device__ __forceinline__ void big_store(const Prob& P, const fv16 (&acc)[4][4], int m0, int n0, int wm, int wn,
-                                          int lr, int lh) {
-  const int M = P.m, N = P.n;
+__device__ __forceinline__ hv8 big_epi8(const Prob& P, const float (&s8)[8], int row, int col) {
+  const int64_t idx = (int64_t)row * P.n + col;
+  hv8 o;
+  if constexpr (kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
+    const hv8 vv = *reinterpret_cast<const hv8*>(P.v + idx), vf = *reinterpret_cast<const hv8*>(P.vf + idx),
+              v0 = *reinterpret_cast<const hv8*>(P.v0 + col);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (float)vv[e];
+      float y = __builtin_fmaf((float)vf[e] - x, sigmoidf((float)v0[e] + s8[e]), x);
+      asm volatile("" : "+v"(y));
+      o[e] = (_Float16)y;
+    }
+  } else if constexpr (kEpi == VKWR_GEMM_EPI_BIAS) {
+    const hv8 v0 = *reinterpret_cast<const hv8*>(P.v0 + col);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float y = s8[e] + (float)v0[e];
+      asm volatile("" : "+v"(y));
+      o[e] = (_Float16)y;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float y = big_epilogue<kEpi>(P, s8[e], row, col + e);
+      asm volatile("" : "+v"(y));
+      o[e] = (_Float16)y;
+    }
+  }
+  return o;
+}
+
+// Stores a 256x256 accumulator tile through epilogue kEpi (fp16, clipped to M x N) via LDS
+// (P.vec_out: 16-byte aligned rows, N a multiple of 8): wave w writes two horizontally
+// adjacent 32x32 blocks of fp32 sums at a time to its own LDS area st (32 rows of kBigStRow
+// floats), then lane l finishes row l / 2, columns 32 (l % 2) .. + 31 of that 32x64 strip
+// (two lanes per 128-byte line of the output) with 16-byte loads and stores.  Written
+// straight from the MFMA layout every store would be 2 bytes per lane, the value-residual
+// operands 2-byte loads, and that form kept the accumulator tile in scratch memory for the
+// value-residual and mixed-epilogue instances.
+constexpr int kBigStRow = 68;  // 64 columns + 4 floats of padding
+template <int kEpi>
+__device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv16 (&acc)[4][4], int m0, int n0,
+                                              int wm, int wn, int lane) {
+  const int lr = lane & 31, lh = lane >> 5, rr = lane >> 1, ch = (lane & 1) * 32;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // one 32x32 block at a time: an epilogue that reads memory (value residual) would
-      // otherwise have every block's loads hoisted and the tile spilled
-      if constexpr (kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL) asm volatile("" ::: "memory");
-      const int col = n0 + wn * 128 + j * 32 + lr;
-      if (col >= N) continue;
+    for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (row >= M) continue;
-        float y = big_epilogue<kEpi>(P, acc[i][j][r], row, col);
-        asm volatile("" : "+v"(y));  // round in fp32, then to fp16 (no fused mixed-precision op)
-        P.c[(int64_t)row * N + col] = (_Float16)y;
+        const int rl = 8 * (r >> 2) + 4 * lh + (r & 3);
+        st[rl * kBigStRow + lr] = acc[i][2 * jj][r];
+        st[rl * kBigStRow + 32 + lr] = acc[i][2 * jj + 1][r];
+      }
+      const int row = m0 + wm * 128 + i * 32 + rr;
+      const int col0 = n0 + wn * 128 + jj * 64 + ch;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const f4 lo = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h);
+        const f4 hi = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h + 4);
+        const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const int col = col0 + 8 * h;
+        if (row < P.m && col < P.n) *reinterpret_cast<hv8*>(P.c + (int64_t)row * P.n + col) = big_epi8<kEpi>(P, s8, row, col);
       }
     }
   }
 }
+
 
 // One 256x256 tile over k-stages [ks, ke): kPartial stores the fp32 sums to part in
 // register order -- element ((4 i + j) * 16 + r) * 256 + thread is accumulator r of block
@@ -627,7 +674,10 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
     __builtin_amdgcn_sched_barrier(0);
     cb = nb;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last stage's re-load has landed
+  // every wave's DMA (the last stage's re-load) has landed and its LDS reads are done: the
+  // epilogue may reuse the buffers
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float* const st = reinterpret_cast<float*>(&sm[0][0][0]) + w * 32 * kBigStRow;
 
   if constexpr (kPartial) {
 #pragma unroll
@@ -637,19 +687,19 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
 #pragma unroll
         for (int r = 0; r < 16; ++r) part[((4 * i + j) * 16 + r) * 256 + tid] = acc[i][j][r];
   } else if constexpr (kEpi >= 0) {
-    big_store<kEpi>(P, acc, m0, n0, wm, wn, lr, lh);
+    big_store_lds<kEpi>(st, P, acc, m0, n0, wm, wn, lane);
   } else {
     // a batch of mixed epilogues: one branch per tile to a specialized store loop
     // (a per-element switch would not keep the accumulator tile in registers)
     switch (P.epi) {
-      case VKWR_GEMM_EPI_RELU_SQUARE: big_store<VKWR_GEMM_EPI_RELU_SQUARE>(P, acc, m0, n0, wm, wn, lr, lh); break;
+      case VKWR_GEMM_EPI_RELU_SQUARE: big_store_lds<VKWR_GEMM_EPI_RELU_SQUARE>(st, P, acc, m0, n0, wm, wn, lane); break;
       case VKWR_GEMM_EPI_VALUE_RESIDUAL:
-        big_store<VKWR_GEMM_EPI_VALUE_RESIDUAL>(P, acc, m0, n0, wm, wn, lr, lh);
+        big_store_lds<VKWR_GEMM_EPI_VALUE_RESIDUAL>(st, P, acc, m0, n0, wm, wn, lane);
         break;
-      case VKWR_GEMM_EPI_BIAS: big_store<VKWR_GEMM_EPI_BIAS>(P, acc, m0, n0, wm, wn, lr, lh); break;
-      case VKWR_GEMM_EPI_TANH: big_store<VKWR_GEMM_EPI_TANH>(P, acc, m0, n0, wm, wn, lr, lh); break;
-      case VKWR_GEMM_EPI_SIGMOID: big_store<VKWR_GEMM_EPI_SIGMOID>(P, acc, m0, n0, wm, wn, lr, lh); break;
-      default: big_store<VKWR_GEMM_EPI_NONE>(P, acc, m0, n0, wm, wn, lr, lh); break;
+      case VKWR_GEMM_EPI_BIAS: big_store_lds<VKWR_GEMM_EPI_BIAS>(st, P, acc, m0, n0, wm, wn, lane); break;
+      case VKWR_GEMM_EPI_TANH: big_store_lds<VKWR_GEMM_EPI_TANH>(st, P, acc, m0, n0, wm, wn, lane); break;
+      case VKWR_GEMM_EPI_SIGMOID: big_store_lds<VKWR_GEMM_EPI_SIGMOID>(st, P, acc, m0, n0, wm, wn, lane); break;
+      default: big_store_lds<VKWR_GEMM_EPI_NONE>(st, P, acc, m0, n0, wm, wn, lane); break;
     }
   }
 }
@@ -1138,14 +1188,15 @@ Config pick_config(int max_m, int min_n) {
 }
 
 // gemm_big_kernel takes the batch when every non-empty problem has an unactivated A, a
-// [N,K] B, K a multiple of 64, 16-byte aligned rows, 32-bit byte offsets into A and B,
-// and some problem has M >= 256.
+// [N,K] B, K a multiple of 64, 16-byte aligned rows (operands and output, N a multiple of 8),
+// 32-bit byte offsets into A and B, and some problem has M >= 256.
 bool big_eligible(const Batch& bt, int max_m) {
   if (max_m < kBigBM) return false;
   for (int i = 0; i < bt.n; ++i) {
     const Prob& P = bt.p[i];
     if (P.m == 0 || P.n == 0) continue;
-    if (P.b_kn || P.a_act != VKWR_GEMM_ACT_NONE || !P.vec || P.k < kBigBK || P.k % kBigBK) return false;
+    if (P.b_kn || P.a_act != VKWR_GEMM_ACT_NONE || !P.vec || !P.vec_out || P.k < kBigBK || P.k % kBigBK)
+      return false;
     if ((int64_t)std::max(P.m, P.n) * P.k * 2 > 0xFFFF0000LL) return false;
   }
   return true;
@@ -1497,6 +1548,8 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
       go(gemm_big_kernel<VKWR_GEMM_EPI_RELU_SQUARE>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_RELU_SQUARE>);
     else if (epi == VKWR_GEMM_EPI_BIAS)
       go(gemm_big_kernel<VKWR_GEMM_EPI_BIAS>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_BIAS>);
+    else if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL)
+      go(gemm_big_kernel<VKWR_GEMM_EPI_VALUE_RESIDUAL>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_VALUE_RESIDUAL>);
     else
       go(gemm_big_kernel<-1>, gemm_big_fixup_kernel<-1>);
     return check_launch(fn);
