@@ -12,7 +12,9 @@ Per layer (x: previous block output, res: residual stream, rows = all rows):
   res, xx = add + LN1 over rows
   xr..xg  = token-shift lerps per group (slot-indexed att shift pool)
   r, k, v, w1, a1, g1, v1 = projections over rows            (one GEMM launch)
-  w, a12, g, v = low-rank outputs (tanh / - / sigmoid / value residual) (one launch)
+  w, a12, g, v = low-rank outputs (tanh / - / sigmoid / value residual) (one launch;
+          the adapter ranks padded to multiples of 64 with zeros, so the launch runs on
+          the large-M kernel)
   k', -kk, kk*a = kk/a gate over rows
   y   = WKV-7 per group on the slot pool (T = 1 decode kernel, T > 1 prefill kernel)
   o   = (GroupNorm(y) + bonus) * g  W_o^T over rows
@@ -34,6 +36,21 @@ from vkwr_amd import capi
 from vkwr.model_executor.rwkv7 import HEAD
 
 TMIX_MIX = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
+RANK_ALIGN = 64  # the large-M GEMM kernel takes K in multiples of 64
+
+
+def _pad_rank(w1, w2, r):
+    """Low-rank adapter pair (w1 [rank, C], w2 [C, rank]) with the rank padded to r: zero
+    rows of w1 give zero inputs to w2's zero columns, which add exact zeros (also through
+    the tanh / sigmoid applied in between: their values meet zero weights)."""
+    rank, C = w1.shape
+    if rank == r:
+        return w1, w2
+    p1 = torch.zeros(r, C, dtype=w1.dtype, device=w1.device)
+    p1[:rank] = w1
+    p2 = torch.zeros(w2.shape[0], r, dtype=w2.dtype, device=w2.device)
+    p2[:, :rank] = w2
+    return p1, p2
 
 
 class MixedEngine:
@@ -55,7 +72,19 @@ class MixedEngine:
         self.xx = buf(R, C)
         self.mix = [buf(R, C) for _ in range(6)]
         self.r, self.k, self.v, self.v_first, self.v_new = (buf(R, C) for _ in range(5))
-        self.w1, self.a1, self.g1, self.v1 = buf(R, cfg.rank_w), buf(R, cfg.rank_a), buf(R, cfg.rank_g), buf(R, cfg.rank_v)
+        # Low-rank adapters with the rank padded to a multiple of 64 (96 -> 128, 480 -> 512 at
+        # the 7B shape), so that the rank-out batch runs on the large-M kernel.
+        up = lambda r: -(-r // RANK_ALIGN) * RANK_ALIGN  # noqa: E731
+        self.ranks = {k: up(getattr(cfg, "rank_" + k)) for k in ("w", "a", "g", "v")}
+        self.lw = []
+        for l, L in enumerate(model.layers):
+            d = {}
+            for k in ("w", "a", "g", "v"):
+                if k + "1" in L:
+                    d[k + "1"], d[k + "2"] = _pad_rank(L[k + "1"], L[k + "2"], self.ranks[k])
+            self.lw.append(d)
+        rk = self.ranks
+        self.w1, self.a1, self.g1, self.v1 = buf(R, rk["w"]), buf(R, rk["a"]), buf(R, rk["g"]), buf(R, rk["v"])
         self.w, self.a12, self.g = buf(R, C), buf(R, C), buf(R, C)
         self.new_k, self.neg_kk, self.kka, self.y, self.o_in, self.o = (buf(R, C) for _ in range(6))
         self.xk = buf(R, C)
@@ -70,27 +99,29 @@ class MixedEngine:
         self.ws = torch.empty(max(need, 0), dtype=torch.uint8, device=dev)
 
     # -- GEMM batches (shared by planning and execution)
-    def _proj(self, L, R, first):
+    def _proj(self, L, W, R, first):
         s, gp = self, capi.gemm_problem
         ps = [gp(s.mix[0][:R], L["Wr"], s.r[:R]), gp(s.mix[2][:R], L["Wk"], s.k[:R]),
               gp(s.mix[3][:R], L["Wv"], (s.v_first if first else s.v)[:R]),
-              gp(s.mix[1][:R], L["w1"], s.w1[:R]), gp(s.mix[4][:R], L["a1"], s.a1[:R]),
-              gp(s.mix[5][:R], L["g1"], s.g1[:R])]
+              gp(s.mix[1][:R], W["w1"], s.w1[:R]), gp(s.mix[4][:R], W["a1"], s.a1[:R]),
+              gp(s.mix[5][:R], W["g1"], s.g1[:R])]
         if not first:
-            ps.append(gp(s.mix[3][:R], L["v1"], s.v1[:R]))
+            ps.append(gp(s.mix[3][:R], W["v1"], s.v1[:R]))
         return ps
 
-    def _rank_out(self, L, R, first):
+    def _rank_out(self, L, W, R, first):
         """The low-rank output GEMMs; tanh(w1) and sigmoid(g1) are applied by
         _rank_act first (once per element: as an A-operand activation every
         column tile of the GEMM recomputed them, 56 of the 103 us of g2 at the 7B
         shape).  Same fp16 values as the A-operand form."""
         s, gp = self, capi.gemm_problem
-        ps = [gp(s.w1[:R], L["w2"], s.w[:R], epilogue=capi.EPI_BIAS, v0=L["w0"]),
-              gp(s.a1[:R], L["a2"], s.a12[:R]),
-              gp(s.g1[:R], L["g2"], s.g[:R])]
+        # g2 (the longest K) first: its tiles start in the first round and the short ones
+        # fill in behind them
+        ps = [gp(s.g1[:R], W["g2"], s.g[:R]),
+              gp(s.w1[:R], W["w2"], s.w[:R], epilogue=capi.EPI_BIAS, v0=L["w0"]),
+              gp(s.a1[:R], W["a2"], s.a12[:R])]
         if not first:
-            ps.append(gp(s.v1[:R], L["v2"], s.v_new[:R], epilogue=capi.EPI_VALUE_RESIDUAL, v=s.v[:R],
+            ps.append(gp(s.v1[:R], W["v2"], s.v_new[:R], epilogue=capi.EPI_VALUE_RESIDUAL, v=s.v[:R],
                          v_first=s.v_first[:R], v0=L["v0"]))
         return ps
 
@@ -102,7 +133,7 @@ class MixedEngine:
         m, s, gp = self.model, self, capi.gemm_problem
         out = []
         for l, L in enumerate(m.layers[:max(nl, 2)]):
-            out += [self._proj(L, R, l == 0), self._rank_out(L, R, l == 0)]
+            out += [self._proj(L, self.lw[l], R, l == 0), self._rank_out(L, self.lw[l], R, l == 0)]
         L = m.layers[-1]
         out += [[gp(s.o_in[:R], L["Wo"], s.o[:R])],
                 [gp(s.xk[:R], L["key"], s.act[:R], epilogue=capi.EPI_RELU_SQUARE)],
@@ -150,9 +181,9 @@ class MixedEngine:
                 n = B * T
                 capi.token_shift(B, T, C, s.xx[r0:r0 + n], state.att_shift[l], mixes,
                                  [t[r0:r0 + n] for t in s.mix], shift_slots=slots)
-            capi.gemm(self._proj(L, R, first), ws)
+            capi.gemm(self._proj(L, s.lw[l], R, first), ws)
             self._rank_act(R)
-            capi.gemm(self._rank_out(L, R, first), ws)
+            capi.gemm(self._rank_out(L, s.lw[l], R, first), ws)
             v = (s.v_first if first else s.v_new)[:R]
             capi.kk_a_gate(R, 1, C, H, s.k[:R], L["k_k"], L["a0"], s.a12[:R], L["k_a"], s.new_k[:R],
                            s.neg_kk[:R], s.kka[:R])

@@ -531,30 +531,68 @@ template <int kEpi>
 __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv16 (&acc)[4][4], int m0, int n0,
                                               int wm, int wn, int lane) {
   const int lr = lane & 31, lh = lane >> 5, rr = lane >> 1, ch = (lane & 1) * 32;
+  constexpr bool kVres = kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL;
+  // Value residual: the v / v_first rows of strip p + 1 are loaded while strip p is
+  // finished (one round trip to memory per strip would otherwise serialise the epilogue).
+  hv8 ov[2][4], ovf[2][4], ov0[2][4];
+  auto load_ops = [&](int p, int slot) __attribute__((always_inline)) {
+    const int row = m0 + wm * 128 + (p >> 1) * 32 + rr, col0 = n0 + wn * 128 + (p & 1) * 64 + ch;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int h = 0; h < 4; ++h) {
+      const int col = col0 + 8 * h;
+      const bool in = row < P.m && col < P.n;
+      const int64_t idx = in ? (int64_t)row * P.n + col : 0;
+      ov[slot][h] = *reinterpret_cast<const hv8*>(P.v + idx);
+      ovf[slot][h] = *reinterpret_cast<const hv8*>(P.vf + idx);
+    }
+  };
+  if constexpr (kVres) {
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
+    for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rl = 8 * (r >> 2) + 4 * lh + (r & 3);
-        st[rl * kBigStRow + lr] = acc[i][2 * jj][r];
-        st[rl * kBigStRow + 32 + lr] = acc[i][2 * jj + 1][r];
-      }
-      const int row = m0 + wm * 128 + i * 32 + rr;
-      const int col0 = n0 + wn * 128 + jj * 64 + ch;
+      for (int h = 0; h < 4; ++h)
+        ov0[jj][h] = *reinterpret_cast<const hv8*>(P.v0 + min(n0 + wn * 128 + jj * 64 + ch + 8 * h, P.n - 8));
+    load_ops(0, 0);
+  }
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const f4 lo = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h);
-        const f4 hi = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h + 4);
-        const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        const int col = col0 + 8 * h;
-        if (row < P.m && col < P.n) *reinterpret_cast<hv8*>(P.c + (int64_t)row * P.n + col) = big_epi8<kEpi>(P, s8, row, col);
+  for (int p = 0; p < 8; ++p) {
+    const int i = p >> 1, jj = p & 1;
+    if constexpr (kVres) {
+      if (p + 1 < 8) load_ops(p + 1, (p + 1) & 1);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rl = 8 * (r >> 2) + 4 * lh + (r & 3);
+      st[rl * kBigStRow + lr] = acc[i][2 * jj][r];
+      st[rl * kBigStRow + 32 + lr] = acc[i][2 * jj + 1][r];
+    }
+    const int row = m0 + wm * 128 + i * 32 + rr;
+    const int col0 = n0 + wn * 128 + jj * 64 + ch;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const f4 lo = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h);
+      const f4 hi = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h + 4);
+      const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const int col = col0 + 8 * h;
+      if (row < P.m && col < P.n) {
+        hv8 o;
+        if constexpr (kVres) {
+          const hv8 vv = ov[p & 1][h], vf = ovf[p & 1][h], v0 = ov0[jj][h];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = (float)vv[e];
+            float y = __builtin_fmaf((float)vf[e] - x, sigmoidf((float)v0[e] + s8[e]), x);
+            asm volatile("" : "+v"(y));
+            o[e] = (_Float16)y;
+          }
+        } else {
+          o = big_epi8<kEpi>(P, s8, row, col);
+        }
+        *reinterpret_cast<hv8*>(P.c + (int64_t)row * P.n + col) = o;
       }
     }
   }
 }
-
 
 // One 256x256 tile over k-stages [ks, ke): kPartial stores the fp32 sums to part in
 // register order -- element ((4 i + j) * 16 + r) * 256 + thread is accumulator r of block
