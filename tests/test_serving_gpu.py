@@ -160,9 +160,10 @@ def _mixed_vs_oracle(gpu, cfg, P, Bd, Bp, T, seed, state_tol):
     """One MixedEngine step of Bd decode rows plus Bp prefill chunks of T tokens against
     oracle/model_ref: decode rows against one reference decode step, each chunk's
     last-token logits and final states against T sequential reference decode steps, and
-    the last layer's WKV of both groups bit for bit against the C oracle on the engine's
-    own WKV inputs (decode rows: the one-chain order of the T = 1 kernel; chunks: the
-    row-split order of the prefill kernel).  Untouched slots stay bitwise unchanged.
+    the last layer's WKV of both groups against the C oracle on the engine's own WKV
+    inputs: bit for bit for the decode rows (the one-chain order of the T = 1 kernel) and
+    chunks under 16 tokens (the row-split order), at tolerance for longer chunks (the
+    chunked kernel, against the reference order).  Untouched slots stay bitwise unchanged.
     End to end the states drift from the float32 model's by the fp16 rounding of the
     intermediates, compounded over the chunk's T tokens; state_tol bounds that drift
     relative to the largest state value."""
@@ -191,16 +192,25 @@ def _mixed_vs_oracle(gpu, cfg, P, Bd, Bp, T, seed, state_tol):
     H, C = cfg.n_head, cfg.n_embd
     L = cfg.n_layer - 1
     v_last = eng.v_new if cfg.n_layer > 1 else eng.v_first
-    # ---- last layer's WKV, bit for bit, on the engine's own inputs
+    # ---- last layer's WKV on the engine's own inputs
     ins = [t.cpu().numpy() for t in (eng.r, eng.w, eng.new_k, v_last, eng.neg_kk, eng.kka)]
     y_eng = eng.y.cpu().numpy()
-    for (B, TT, r0, order, sl, base) in ((Bd, 1, 0, "seq", sd, 0), (Bp, T, Bd, "rows", sp, Bd)):
+    chunked = T >= 16
+    for (B, TT, r0, order, sl, base) in ((Bd, 1, 0, "seq", sd, 0),
+                                         (Bp, T, Bd, "seq" if chunked else "rows", sp, Bd)):
         n = B * TT
         pool = wkv0[L, base:base + B].cpu().numpy().copy()
         y_ref = orc.wkv_fp32_slots(B, TT, C, H, pool, np.arange(B, dtype=np.int64),
                                    *(x[r0:r0 + n].reshape(B, TT, C) for x in ins), order=order)
-        assert np.array_equal(y_eng[r0:r0 + n].view(np.uint16), y_ref.reshape(n, C).view(np.uint16)), order
-        assert np.array_equal(state.wkv[L, sl.long().to(gpu)].cpu().numpy(), pool), order
+        got = state.wkv[L, sl.long().to(gpu)].cpu().numpy()
+        if TT > 1 and chunked:
+            yg, yr = y_eng[r0:r0 + n].astype(np.float64), y_ref.reshape(n, C).astype(np.float64)
+            err = np.abs(yg - yr)
+            assert err.sum() / np.abs(yr).sum() <= 2e-6, "chunked y"
+            assert np.abs(got.astype(np.float64) - pool).max() <= 2e-5 * np.abs(pool).max(), "chunked state"
+        else:
+            assert np.array_equal(y_eng[r0:r0 + n].view(np.uint16), y_ref.reshape(n, C).view(np.uint16)), order
+            assert np.array_equal(got, pool), order
     # ---- end to end against the float32 model
     m32 = _f32_model(model)
     with torch.no_grad():

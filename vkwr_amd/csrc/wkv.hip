@@ -501,6 +501,341 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
   }
 }
 
+// ---- chunked prefill (T >= kChunkMinT): WKV-7 over chunks of 16 tokens on the matrix cores.
+//
+// Within a chunk of L = 16 tokens (t = 1..L, entry state S0, Λ_t = d_1 ... d_t elementwise
+// over the key index j) write S_t = X_t diag(Λ_t).  The recurrence
+//     S_t = S_{t-1} diag(d_t) + (S_{t-1} a_t) b_t^T + v_t k_t^T,   y_t = S_t r_t
+// becomes, with â_t = Λ_{t-1} a_t, b̂_t = b_t / Λ_t, k̂_t = k_t / Λ_t, r̂_t = Λ_t r_t and
+// z_t = S_{t-1} a_t,
+//     X_t = X_{t-1} + z_t b̂_t^T + v_t k̂_t^T,
+//     z_t = X0 â_t + Σ_{m<t} (b̂_m·â_t) z_m + (k̂_m·â_t) v_m,
+//     y_t = X0 r̂_t + Σ_{m≤t} (b̂_m·r̂_t) z_m + (k̂_m·r̂_t) v_m.
+// In matrix form (rows t): with the L x L matrices N = T_ab = strict-lower(Â B̂^T),
+// T_ak = strict-lower(Â K̂^T), T_rb = lower(R̂ B̂^T), T_rk = lower(R̂ K̂^T):
+//     Z = (I - N)^{-1} (Â X0^T + T_ak V),   Y = R̂ X0^T + T_rb Z + T_rk V,
+//     S_L^T = diag(Λ_L) (X0^T + B̂^T Z + K̂^T V),   X0 = S0,
+// The ratios Λ_{t-1}/Λ_m and Λ_t/Λ_m that these products form are at most 1 and at least
+// d_min^16 (d > 0.545 for every w, so > 6e-5): fp32 holds them without overflow, and the
+// results agree with the token-by-token recurrence to fp32 rounding.
+//
+// One 256-lane workgroup per (sequence, head); wave w owns the state rows (value index)
+// i = 16w .. 16w + 15, which evolve independently, as X^T tiles (16 x 16, j x i) in the
+// accumulator layout of v_mfma_f32_16x16x4_f32 (lane l, register r: row 4 (l / 16) + r,
+// column l % 16; written D(M) below).  D(M) serves directly as the B operand of a product
+// M' M when the k index is walked in the permuted order k = 4 (l / 16) + s over the 4 steps
+// s of a 16-wide k tile (a sum over k does not depend on its order), and D(M^T) as the A
+// operand of M M'; every other operand is read from LDS in the same permuted order.
+//
+// Pipeline: iteration c runs, in one block between two barriers, chunk c against the state
+// (Â X0^T, R̂ X0^T, K̂^T V, then Z, Y and B̂^T Z), chunk c + 1's four L x L matrices (one per
+// wave) and chunk c + 2's hat vectors (VALU work: Λ by a multiplicative DPP scan over the 16
+// lanes that hold one channel quad's tokens), so the scheduler interleaves the three; hat
+// vectors live in three LDS buffers, the matrices in two.  Each wave forms W^T =
+// ((I - N)^{-1})^T of chunk c from the powers of N next to the state products (N is
+// nilpotent, N^16 = 0, so (I - N)^{-1} = (I + N)(I + N^2)(I + N^4)(I + N^8); the powers in
+// both orientations: D(M^2) = Σ_s D(M^T)[s] x D(M)[s]), so the dependent chain of a chunk
+// is Â X0^T -> Z -> B̂^T Z.  (Back substitution on the vector ALU instead measured 25 %
+// slower.)  Per chunk and wave: 128 MFMAs, one barrier.
+constexpr int kCL = 16;          // tokens per chunk
+constexpr int kChunkMinT = 16;   // shorter prefills take the row-split kernel
+constexpr int kHP = kHead + 4;   // padded LDS row of a [t][j] hat vector (floats)
+constexpr int kTP = kCL + 4;     // padded LDS row of a transposed [j][t] vector (floats)
+
+typedef float fq4 __attribute__((ext_vector_type(4)));
+typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ fq4 mfma4(float a, float b, fq4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// exp(-e^{-1/2} sigmoid(w)) from the hardware exp2 / reciprocal (about 2 ulp): the chunked
+// form is not bit-matched to the token-by-token kernels anyway, and decay() with expf's
+// range checks and an IEEE division is several times longer
+__device__ __forceinline__ float decay_fast(float w) {
+  const float e = __builtin_amdgcn_exp2f(w * -1.4426950408889634f);  // exp(-w)
+  return __builtin_amdgcn_exp2f(-0.8750387749145276f * __builtin_amdgcn_rcpf(1.0f + e));  // e^{-1/2} log2(e)
+}
+
+typedef const __attribute__((address_space(1))) hv8 global_hv8;
+
+// x * (the value of the lane `n` below in the same 16-lane row, 1 for the first n lanes)
+#define VK_SCAN_MUL(x, ctrl) \
+  x *= __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, 1.0f), __builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false))
+
+struct ChunkLds {
+  hv8 raw[2][6 * kCL * 8];                                  // fp16 r, w, k, v, a, b: [vec][t][8 x 8]
+  __attribute__((aligned(16))) float lamL[3][kHead];         // Λ_L
+  __attribute__((aligned(16))) float hat[3][4][kCL][kHP];    // Â, R̂, B̂, K̂ as [t][j]
+  __attribute__((aligned(16))) float hatT[3][3][kHead][kTP]; // B̂^T, K̂^T as [j][t]; V^T as [i][t]
+  __attribute__((aligned(16))) float gram[2][4][kCL][kTP];   // N, T_ak, T_rb, T_rk as [t][m]
+  __attribute__((aligned(16))) float gramT[2][4][kCL][kTP];  // the same as [m][t]
+  __attribute__((aligned(16))) float lamSink[256];           // Λ stores of lanes that hold no Λ_L
+};
+
+// One workgroup per CU (the LDS pipeline takes 150 KiB): the compiler may use every register.
+template <bool kSlots>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
+  const Fp32Args& p = ra.a;
+  __shared__ ChunkLds L;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int li = lane & 15, g = lane >> 4;
+  const int bh = blockIdx.x, bi = bh / p.H, h = bh - bi * p.H;
+  const int T = p.T, C = p.C;
+  const size_t tok0 = (size_t)bi * T * C + (size_t)h * kHead;
+  float* S = state_block<kSlots>(p, bi, h);
+  if (S == nullptr) {
+    for (int idx = tid; idx < T * kHead; idx += 256)
+      p.y[tok0 + (size_t)(idx / kHead) * C + (idx % kHead)] = (_Float16)__builtin_nanf("");
+    return;
+  }
+  const int iw = 16 * w + li;  // this lane's state row (value index) in the accumulator layout
+  // X^T tile q (j = 16 q .. 16 q + 15): register r holds X^T[16 q + 4 g + r][iw] = S[iw][16 q + 4 g + r]
+  fq4 st[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) st[q] = *reinterpret_cast<const fq4*>(S + iw * kHead + 16 * q + 4 * g);
+
+  // raw token vectors: piece c = tid + 256 u is vector c >> 7, token (c >> 3) & 15, channels
+  // 8 (c & 7) .. + 7; tokens past T re-read token T - 1 (masked out below)
+  const _Float16* src[6] = {p.r, p.w, p.k, p.v, p.a, p.b};
+  hv8 pre[3];
+  auto load_raw = [&](int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int c = tid + 256 * u;
+      const int t = min(t0 + ((c >> 3) & 15), T - 1);
+      const _Float16* at = src[c >> 7] + tok0 + (size_t)t * C + (c & 7) * 8;
+      // a global (not flat) load: a flat load would also count against the LDS counter,
+      // and every wait for the LDS reads below would wait for this prefetch
+      if (ra.vec) {
+        pre[u] = *(global_hv8*)at;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pre[u][e] = *(const __attribute__((address_space(1))) _Float16*)(at + e);
+      }
+    }
+  };
+  auto store_raw = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) L.raw[buf][tid + 256 * u] = pre[u];
+  };
+
+  // hat vectors of chunk cc (raw buffer cc & 1) into hat buffer cc % 3: thread = token ht,
+  // channels j0 .. j0 + 3 (16 lanes of a row hold one quad's 16 tokens: the Λ scan).  A
+  // chunk past the end computes stale values nobody reads.  Split into the LDS reads and
+  // the arithmetic, so the reads can be issued early.
+  const int ht = lane & 15, j0 = 4 * (tid >> 4);
+  struct RawQuad {
+    hv4 r, w, k, v, a, b;
+  };
+  auto hats_read = [&](int cc) __attribute__((always_inline)) {
+    const int rb = cc & 1;
+    auto rd4 = [&](int vec) __attribute__((always_inline)) {
+      return *reinterpret_cast<const hv4*>(reinterpret_cast<const _Float16*>(&L.raw[rb][(vec * kCL + ht) * 8]) + j0);
+    };
+    return RawQuad{rd4(0), rd4(1), rd4(2), rd4(3), rd4(4), rd4(5)};
+  };
+  auto hats_write = [&](int cc, const RawQuad& x) __attribute__((always_inline)) {
+    const int b = cc % 3;
+    const int n = min(kCL, T - cc * kCL);
+    const float in = ht < n ? 1.0f : 0.0f;  // padded tokens: d = 1 and zero vectors (a select, no branch)
+    float l1[4], l0[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float d = __builtin_fmaf(in, decay_fast((float)x.w[e]), 1.0f - in);
+      VK_SCAN_MUL(d, 0x111);  // row_shr:1
+      VK_SCAN_MUL(d, 0x112);  // row_shr:2
+      VK_SCAN_MUL(d, 0x114);  // row_shr:4
+      VK_SCAN_MUL(d, 0x118);  // row_shr:8
+      l1[e] = d;              // Λ_t
+      l0[e] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, 1.0f),
+                                                                     __builtin_bit_cast(int, d), 0x111, 0xF, 0xF, false));
+    }
+    float ah[4], rh[4], bh[4], kh[4], vv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float rl = __builtin_amdgcn_rcpf(l1[e]);
+      ah[e] = l0[e] * ((float)x.a[e] * in);
+      rh[e] = l1[e] * ((float)x.r[e] * in);
+      bh[e] = ((float)x.b[e] * in) * rl;
+      kh[e] = ((float)x.k[e] * in) * rl;
+      vv[e] = (float)x.v[e] * in;
+    }
+    *reinterpret_cast<fq4*>(&L.hat[b][0][ht][j0]) = fq4{ah[0], ah[1], ah[2], ah[3]};
+    *reinterpret_cast<fq4*>(&L.hat[b][1][ht][j0]) = fq4{rh[0], rh[1], rh[2], rh[3]};
+    *reinterpret_cast<fq4*>(&L.hat[b][2][ht][j0]) = fq4{bh[0], bh[1], bh[2], bh[3]};
+    *reinterpret_cast<fq4*>(&L.hat[b][3][ht][j0]) = fq4{kh[0], kh[1], kh[2], kh[3]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      L.hatT[b][0][j0 + e][ht] = bh[e];
+      L.hatT[b][1][j0 + e][ht] = kh[e];
+      L.hatT[b][2][j0 + e][ht] = vv[e];
+    }
+    float* lamDst = ht == kCL - 1 ? &L.lamL[b][j0] : &L.lamSink[4 * (tid >> 2) & 252];
+    *reinterpret_cast<fq4*>(lamDst) = fq4{l1[0], l1[1], l1[2], l1[3]};
+  };
+  // wave w: the L x L matrix w of chunk cc (hat buffer cc % 3, matrix buffer cc & 1):
+  // (Â,B̂) (Â,K̂) (R̂,B̂) (R̂,K̂), masked (strictly lower for the first two)
+  const int xsel = w < 2 ? 0 : 1, ysel = (w & 1) ? 3 : 2, mlim = w < 2 ? 1 : 0;
+  struct GramOps {
+    fq4 x[4], y[4];
+  };
+  auto gram_read = [&](int cc) __attribute__((always_inline)) {
+    const int hb = cc % 3;
+    GramOps o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o.x[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][xsel][li][16 * q + 4 * g]);
+      o.y[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][ysel][li][16 * q + 4 * g]);
+    }
+    return o;
+  };
+  auto gram_mfma = [&](const GramOps& o) __attribute__((always_inline)) {
+    fq4 gm = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) gm = mfma4(o.x[q][s2], o.y[q][s2], gm);
+    return gm;
+  };
+  auto gram_write = [&](int cc, const fq4& gm) __attribute__((always_inline)) {
+    const int b = cc & 1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * g + r;
+      const float x = li <= t - mlim ? gm[r] : 0.0f;
+      L.gram[b][w][t][li] = x;
+      L.gramT[b][w][li][t] = x;
+    }
+  };
+
+  const int nchunk = (T + kCL - 1) / kCL;
+  // prologue: chunk 0's matrices and chunk 1's hats; chunk 2's raw vectors staged, chunk 3's
+  // loaded.  (Chunks past the end read token T - 1 and are never used.)
+  load_raw(0);
+  store_raw(0);
+  load_raw(kCL);
+  __syncthreads();
+  hats_write(0, hats_read(0));
+  store_raw(1);
+  load_raw(2 * kCL);
+  __syncthreads();
+  hats_write(1, hats_read(1));
+  gram_write(0, gram_mfma(gram_read(0)));
+  store_raw(0);
+  load_raw(3 * kCL);
+  __syncthreads();
+  for (int c = 0; c < nchunk; ++c) {
+    const int b = c & 1, hb = c % 3;
+    const int n = min(kCL, T - c * kCL);
+    // ---- phase 1: every LDS operand of the iteration
+    fq4 pm[4], pmt[4];  // pm[k] = D(N^(2^k)), pmt[k] = D((N^(2^k))^T)
+    pm[0] = *reinterpret_cast<const fq4*>(&L.gramT[b][0][li][4 * g]);
+    pmt[0] = *reinterpret_cast<const fq4*>(&L.gram[b][0][li][4 * g]);
+    fq4 a4[4], r4[4], k4[4], b4[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][0][li][16 * q + 4 * g]);
+      r4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][1][li][16 * q + 4 * g]);
+      k4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][1][16 * q + li][4 * g]);
+    }
+    const fq4 v4 = *reinterpret_cast<const fq4*>(&L.hatT[hb][2][iw][4 * g]);
+    const GramOps go = gram_read(c + 1);
+    const RawQuad rq = hats_read(c + 2);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) b4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][0][16 * q + li][4 * g]);
+    const fq4 tak = *reinterpret_cast<const fq4*>(&L.gram[b][1][li][4 * g]);
+    const fq4 trb = *reinterpret_cast<const fq4*>(&L.gram[b][2][li][4 * g]);
+    const fq4 trk = *reinterpret_cast<const fq4*>(&L.gram[b][3][li][4 * g]);
+    fq4 lamq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lamq[q] = *reinterpret_cast<const fq4*>(&L.lamL[hb][16 * q + 4 * g]);
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- phase 2 (independent chains, interleaved by the scheduler): W^T of this chunk,
+    // Â X0^T, R̂ X0^T, K̂^T V, chunk c + 1's matrix, chunk c + 2's hat vectors
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      fq4 x = {0.0f, 0.0f, 0.0f, 0.0f}, y = x;
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        x = mfma4(pmt[k - 1][s2], pm[k - 1][s2], x);
+        y = mfma4(pm[k - 1][s2], pmt[k - 1][s2], y);
+      }
+      pm[k] = x;
+      pmt[k] = y;
+    }
+    // W^T = (I + N^T)(I + (N^T)^2)(I + (N^T)^4)(I + (N^T)^8): Q <- Q + (N^T)^(2^k) Q, whose A
+    // operand D(((N^T)^(2^k))^T) is pm[k]
+    fq4 wt;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wt[r] = (4 * g + r == li ? 1.0f : 0.0f) + pmt[0][r];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      fq4 x = wt;
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) x = mfma4(pm[k][s2], wt[s2], x);
+      wt = x;
+    }
+    fq4 p1 = {0.0f, 0.0f, 0.0f, 0.0f}, y1 = p1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        p1 = mfma4(a4[q][s2], st[q][s2], p1);
+        y1 = mfma4(r4[q][s2], st[q][s2], y1);
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) st[q] = mfma4(k4[q][s2], v4[s2], st[q]);
+    const fq4 gm = gram_mfma(go);
+    hats_write(c + 2, rq);
+    // ---- phase 3: RHS = Â X0^T + T_ak V;  Y1 += T_rk V;  Z = W RHS;  Y = Y1 + T_rb Z;
+    // X^T += B̂^T Z;  S^T = diag(Λ_L) X^T
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      p1 = mfma4(tak[s2], v4[s2], p1);
+      y1 = mfma4(trk[s2], v4[s2], y1);
+    }
+    fq4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) z = mfma4(wt[s2], p1[s2], z);
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) y1 = mfma4(trb[s2], z[s2], y1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) st[q] = mfma4(b4[q][s2], z[s2], st[q]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[q][r] *= lamq[q][r];
+    }
+    gram_write(c + 1, gm);
+    // y rows t = 4 g + r of this wave's 16 value columns
+    _Float16 yh[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float yv = y1[r];
+      asm volatile("" : "+v"(yv));  // an fp32 value before the fp16 conversion
+      yh[r] = (_Float16)yv;
+    }
+    _Float16* yp = p.y + tok0 + (size_t)(c * kCL + 4 * g) * C + iw;
+    if (n == kCL) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yp[(size_t)r * C] = yh[r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (4 * g + r < n) yp[(size_t)r * C] = yh[r];
+    }
+    // chunk c + 3's raw vectors into the buffer chunk c + 1's hats read (one iteration ago)
+    store_raw((c + 1) & 1);
+    load_raw((c + 4) * kCL);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) *reinterpret_cast<fq4*>(S + iw * kHead + 16 * q + 4 * g) = st[q];
+}
+
 bool rows_vec_ok(const Fp32Args& p) {
   auto al = [](const void* x, uintptr_t m) { return ((uintptr_t)x & (m - 1)) == 0; };
   return al(p.r, 16) && al(p.w, 16) && al(p.k, 16) && al(p.v, 16) && al(p.a, 16) && al(p.b, 16) &&
@@ -522,7 +857,9 @@ void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
       hipLaunchKernelGGL((wkv7_fp32_step_kernel<kSlots, false>), dim3(B * p.H), dim3(64), 0, stream, p);
   } else if (rows) {
     RowsArgs ra{p, rows_vec_ok(p) ? 1 : 0};
-    if (ra.vec && B * p.H < 2 * device_cus())
+    if (p.T >= kChunkMinT)
+      hipLaunchKernelGGL(wkv7_fp32_chunk_kernel<kSlots>, dim3(B * p.H), dim3(256), 0, stream, ra);
+    else if (ra.vec && B * p.H < 2 * device_cus())
       hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 1>), dim3(2 * B * p.H), dim3(256), 0, stream, ra);
     else
       hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 2>), dim3(B * p.H), dim3(256), 0, stream, ra);
