@@ -483,115 +483,103 @@ __device__ __forceinline__ float big_epilogue(const Prob& P, float y, int row, i
   }
 }
 
-// Epilogue kEpi of 8 consecutive columns of one row (16-byte operand loads), rounded in fp32
-// and then to fp16, the same arithmetic per element as big_epilogue.
-template <int kEpi>
-__device__ __forceinline__ hv8 big_epi8(const Prob& P, const float (&s8)[8], int row, int col) {
-  const int64_t idx = (int64_t)row * P.n + col;
-  hv8 o;
-  if constexpr (kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL) {
-    const hv8 vv = *reinterpret_cast<const hv8*>(P.v + idx), vf = *reinterpret_cast<const hv8*>(P.vf + idx),
-              v0 = *reinterpret_cast<const hv8*>(P.v0 + col);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = (float)vv[e];
-      float y = __builtin_fmaf((float)vf[e] - x, sigmoidf((float)v0[e] + s8[e]), x);
-      asm volatile("" : "+v"(y));
-      o[e] = (_Float16)y;
-    }
-  } else if constexpr (kEpi == VKWR_GEMM_EPI_BIAS) {
-    const hv8 v0 = *reinterpret_cast<const hv8*>(P.v0 + col);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float y = s8[e] + (float)v0[e];
-      asm volatile("" : "+v"(y));
-      o[e] = (_Float16)y;
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float y = big_epilogue<kEpi>(P, s8[e], row, col + e);
-      asm volatile("" : "+v"(y));
-      o[e] = (_Float16)y;
-    }
-  }
-  return o;
-}
-
 // Stores a 256x256 accumulator tile through epilogue kEpi (fp16, clipped to M x N) via LDS
-// (P.vec_out: 16-byte aligned rows, N a multiple of 8): wave w writes two horizontally
-// adjacent 32x32 blocks of fp32 sums at a time to its own LDS area st (32 rows of kBigStRow
-// floats), then lane l finishes row l / 2, columns 32 (l % 2) .. + 31 of that 32x64 strip
-// (two lanes per 128-byte line of the output) with 16-byte loads and stores.  Written
-// straight from the MFMA layout every store would be 2 bytes per lane, the value-residual
-// operands 2-byte loads, and that form kept the accumulator tile in scratch memory for the
-// value-residual and mixed-epilogue instances.
-constexpr int kBigStRow = 68;  // 64 columns + 4 floats of padding
+// (P.vec_out: 16-byte aligned rows, N a multiple of 8).  Wave w walks its 128 x 128 part
+// in 8 strips of 32 x 64 (two horizontally adjacent 32 x 32 accumulator blocks): strip p's
+// fp32 sums go to one of two LDS buffers of the wave (32 rows of kBigStRow floats each)
+// while strip p - 1 is read back from the other, lane l taking 8 columns (8 (l % 8) .. + 7)
+// of rows l / 8 + 8 h, h = 0..3, so that each 16-byte store instruction writes 8 whole
+// 128-byte lines; epilogue operands are read the same way.  Written straight from the MFMA
+// layout every store would be 2 bytes per lane, and that form kept the accumulator tile in
+// scratch memory for the value-residual and mixed-epilogue instances.  Per-column operands
+// (bias / v0) are loaded once; the value residual's v and v_first rows one strip ahead.
+constexpr int kBigStRow = 68;               // 64 columns + 4 floats of padding
+constexpr int kBigStBuf = 32 * kBigStRow;   // floats per strip buffer
 template <int kEpi>
 __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv16 (&acc)[4][4], int m0, int n0,
                                               int wm, int wn, int lane) {
-  const int lr = lane & 31, lh = lane >> 5, rr = lane >> 1, ch = (lane & 1) * 32;
+  const int lr = lane & 31, lh = lane >> 5, r8 = lane >> 3, c8 = 8 * (lane & 7);
   constexpr bool kVres = kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL;
-  // Value residual: the v / v_first rows of strip p + 1 are loaded while strip p is
-  // finished (one round trip to memory per strip would otherwise serialise the epilogue).
-  hv8 ov[2][4], ovf[2][4], ov0[2][4];
-  auto load_ops = [&](int p, int slot) __attribute__((always_inline)) {
-    const int row = m0 + wm * 128 + (p >> 1) * 32 + rr, col0 = n0 + wn * 128 + (p & 1) * 64 + ch;
+  constexpr bool kCol = kVres || kEpi == VKWR_GEMM_EPI_BIAS;  // a per-column operand v0
+  const int rowb = m0 + wm * 128 + r8, colb = n0 + wn * 128 + c8;
+  hv8 ov0[2];
+  if constexpr (kCol) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) ov0[jj] = *reinterpret_cast<const hv8*>(P.v0 + min(colb + jj * 64, P.n - 8));
+  }
+  hv8 ov[2][4], ovf[2][4];
+  auto load_ops = [&](int p) __attribute__((always_inline)) {
+    const int col = colb + (p & 1) * 64;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const int col = col0 + 8 * h;
+      const int row = rowb + (p >> 1) * 32 + 8 * h;
       const bool in = row < P.m && col < P.n;
       const int64_t idx = in ? (int64_t)row * P.n + col : 0;
-      ov[slot][h] = *reinterpret_cast<const hv8*>(P.v + idx);
-      ovf[slot][h] = *reinterpret_cast<const hv8*>(P.vf + idx);
+      ov[p & 1][h] = *reinterpret_cast<const hv8*>(P.v + idx);
+      ovf[p & 1][h] = *reinterpret_cast<const hv8*>(P.vf + idx);
     }
   };
-  if constexpr (kVres) {
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-      for (int h = 0; h < 4; ++h)
-        ov0[jj][h] = *reinterpret_cast<const hv8*>(P.v0 + min(n0 + wn * 128 + jj * 64 + ch + 8 * h, P.n - 8));
-    load_ops(0, 0);
-  }
-#pragma unroll
-  for (int p = 0; p < 8; ++p) {
+  auto write_strip = [&](int p) __attribute__((always_inline)) {
+    float* sb = st + (p & 1) * kBigStBuf;
     const int i = p >> 1, jj = p & 1;
-    if constexpr (kVres) {
-      if (p + 1 < 8) load_ops(p + 1, (p + 1) & 1);
-    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int rl = 8 * (r >> 2) + 4 * lh + (r & 3);
-      st[rl * kBigStRow + lr] = acc[i][2 * jj][r];
-      st[rl * kBigStRow + 32 + lr] = acc[i][2 * jj + 1][r];
+      sb[rl * kBigStRow + lr] = acc[i][2 * jj][r];
+      sb[rl * kBigStRow + 32 + lr] = acc[i][2 * jj + 1][r];
     }
-    const int row = m0 + wm * 128 + i * 32 + rr;
-    const int col0 = n0 + wn * 128 + jj * 64 + ch;
+  };
+  auto finish_strip = [&](int p) __attribute__((always_inline)) {
+    const float* sb = st + (p & 1) * kBigStBuf + r8 * kBigStRow + c8;
+    f4 v[4][2];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const f4 lo = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h);
-      const f4 hi = *reinterpret_cast<const f4*>(st + rr * kBigStRow + ch + 8 * h + 4);
-      const float s8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      const int col = col0 + 8 * h;
-      if (row < P.m && col < P.n) {
-        hv8 o;
-        if constexpr (kVres) {
-          const hv8 vv = ov[p & 1][h], vf = ovf[p & 1][h], v0 = ov0[jj][h];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = (float)vv[e];
-            float y = __builtin_fmaf((float)vf[e] - x, sigmoidf((float)v0[e] + s8[e]), x);
-            asm volatile("" : "+v"(y));
-            o[e] = (_Float16)y;
-          }
-        } else {
-          o = big_epi8<kEpi>(P, s8, row, col);
-        }
-        *reinterpret_cast<hv8*>(P.c + (int64_t)row * P.n + col) = o;
-      }
+      v[h][0] = *reinterpret_cast<const f4*>(sb + 8 * h * kBigStRow);
+      v[h][1] = *reinterpret_cast<const f4*>(sb + 8 * h * kBigStRow + 4);
     }
+    const int col = colb + (p & 1) * 64;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int row = rowb + (p >> 1) * 32 + 8 * h;
+      const float s8[8] = {v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w, v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w};
+      hv8 o;
+      if constexpr (kVres) {
+        const hv8 vv = ov[p & 1][h], vf = ovf[p & 1][h], v0 = ov0[p & 1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = (float)vv[e];
+          float y = __builtin_fmaf((float)vf[e] - x, sigmoidf((float)v0[e] + s8[e]), x);
+          asm volatile("" : "+v"(y));
+          o[e] = (_Float16)y;
+        }
+      } else if constexpr (kEpi == VKWR_GEMM_EPI_BIAS) {
+        const hv8 v0 = ov0[p & 1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = s8[e] + (float)v0[e];
+          asm volatile("" : "+v"(y));
+          o[e] = (_Float16)y;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = big_epilogue<kEpi>(P, s8[e], row, col + e);
+          asm volatile("" : "+v"(y));
+          o[e] = (_Float16)y;
+        }
+      }
+      if (row < P.m && col < P.n) *reinterpret_cast<hv8*>(P.c + (int64_t)row * P.n + col) = o;
+    }
+  };
+  if constexpr (kVres) load_ops(0);
+  write_strip(0);
+#pragma unroll
+  for (int p = 1; p < 8; ++p) {
+    if constexpr (kVres) load_ops(p);
+    write_strip(p);
+    finish_strip(p - 1);
   }
+  finish_strip(7);
 }
 
 // One 256x256 tile over k-stages [ks, ke): kPartial stores the fp32 sums to part in
@@ -715,7 +703,7 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
   // every wave's DMA (the last stage's re-load) has landed and its LDS reads are done: the
   // epilogue may reuse the buffers
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  float* const st = reinterpret_cast<float*>(&sm[0][0][0]) + w * 32 * kBigStRow;
+  float* const st = reinterpret_cast<float*>(&sm[0][0][0]) + w * 2 * kBigStBuf;
 
   if constexpr (kPartial) {
 #pragma unroll
