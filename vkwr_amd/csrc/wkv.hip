@@ -564,7 +564,10 @@ typedef const __attribute__((address_space(1))) hv8 global_hv8;
   x *= __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, 1.0f), __builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false))
 
 struct ChunkLds {
-  hv8 raw[2][6 * kCL * 8];                                  // fp16 r, w, k, v, a, b: [vec][t][8 x 8]
+  // fp16 r, w, k, v, a, b: [vec][t][8 x 8 channels + 8 of padding].  The padding spreads the
+  // 16 tokens that one row of 16 lanes reads (one channel quad each) over distinct banks:
+  // with 128-byte rows they would all fall on two.
+  hv8 raw[2][6 * kCL][9];
   __attribute__((aligned(16))) float lamL[3][kHead];         // Λ_L
   __attribute__((aligned(16))) float hat[3][4][kCL][kHP];    // Â, R̂, B̂, K̂ as [t][j]
   __attribute__((aligned(16))) float hatT[3][3][kHead][kTP]; // B̂^T, K̂^T as [j][t]; V^T as [i][t]
@@ -617,7 +620,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
   auto store_raw = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 3; ++u) L.raw[buf][tid + 256 * u] = pre[u];
+    for (int u = 0; u < 3; ++u) {
+      const int c = tid + 256 * u;
+      L.raw[buf][c >> 3][c & 7] = pre[u];  // row (vector, token) c >> 3, channels 8 (c & 7) ..
+    }
   };
 
   // hat vectors of chunk cc (raw buffer cc & 1) into hat buffer cc % 3: thread = token ht,
@@ -631,7 +637,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto hats_read = [&](int cc) __attribute__((always_inline)) {
     const int rb = cc & 1;
     auto rd4 = [&](int vec) __attribute__((always_inline)) {
-      return *reinterpret_cast<const hv4*>(reinterpret_cast<const _Float16*>(&L.raw[rb][(vec * kCL + ht) * 8]) + j0);
+      return *reinterpret_cast<const hv4*>(reinterpret_cast<const _Float16*>(&L.raw[rb][vec * kCL + ht][0]) + j0);
     };
     return RawQuad{rd4(0), rd4(1), rd4(2), rd4(3), rd4(4), rd4(5)};
   };
