@@ -10,6 +10,18 @@
 // Reductions use a fixed order (wave butterfly + wave-ordered block sum), so
 // results are run-to-run deterministic.
 //
+// At decode sizes (128 rows of 2048) the kernel is latency-bound, so the code is
+// arranged to have as few dependent memory round trips as possible: all kernel
+// arguments in one scalar round trip, then every load of the row issued back to
+// back with no branch or wait between them (the slot-table lookup among them),
+// the shift row as soon as its slot arrives, and the conversions behind a
+// scheduling barrier.  Measured in a graph without a profiler (HIP events,
+// difference of 40-launch graphs with and without the kernel): an empty launch
+// costs 1.5 us, the residual + LN + 1 lerp 3.2 us, the 4-part + LN + 6 lerps
+// 5.4 us, of which ~1 us is the 6 frag outputs' 16-byte scattered stores (the
+// same kernel with row-major outputs: 4.5 us; spreading a row's stores over 2
+// or 4 workgroups does not shorten it, so the cost is in the L2, not the CU).
+//
 // Roofline: HBM.  Algorithmic bytes per row of C channels: plain LN 4C (read
 // x, write y); residual add 8C; decode fusion with n mix vectors
 // 2C (x) + 2C (residual) + 2C (shift read) + 2C (shift write) + 2C (x_out)
@@ -80,6 +92,16 @@ struct LnArgs {
   int n_parts;
 };
 
+// One int32 through a vector load whose wait the compiler places at the first use (the
+// address is moved to VGPRs, so the load cannot become a scalar one).
+// Global (not flat) address space, so the load counts only against vmcnt.
+__device__ __forceinline__ int32_t ld_vgpr(const int32_t* q) {
+  typedef const int32_t __attribute__((address_space(1)))* gptr;
+  gptr g = (gptr)q;
+  asm("" : "+v"(g));
+  return *g;
+}
+
 template <bool kBf16>
 __device__ __forceinline__ float ld_in(const void* p, int64_t i) {
   if constexpr (kBf16) {
@@ -92,10 +114,23 @@ __device__ __forceinline__ float ld_in(const void* p, int64_t i) {
 // VW: elements per lane access (8 = one 16-byte load, 1 = scalar); NV: accesses
 // per lane (VW * NV * 256 >= C); NMIX: 0 = plain LN output, 1 or 6 = decode
 // fusion with that many token-shift mix vectors.
-// NP > 0: x comes as NP fp32 K-part planes (vector path only).
-template <int VW, int NV, int NMIX, bool kBf16, int NP = 0>
+// NP > 0: x comes as NP fp32 K-part planes (vector path only).  kSlots: shift_slots is
+// given (its lookup then issues with the row's loads instead of ahead of them).
+template <int VW, int NV, int NMIX, bool kBf16, int NP = 0, bool kSlots = false>
 __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
   __shared__ float red[2][kWaves];
+  // Every argument the row needs, into SGPRs in one scalar round trip: left to itself the
+  // compiler loads them a cache line at a time as each is first used, behind branches that
+  // wait for the previous load.
+  if constexpr (NMIX > 0) {
+    asm volatile("" ::"s"(p.C), "s"(p.rows), "s"(p.src_mul), "s"(p.src_add), "s"(p.x), "s"(p.residual),
+                 "s"(p.weight), "s"(p.bias), "s"(p.eps), "s"(p.x_out), "s"(p.x_rows), "s"(p.shift_slots),
+                 "s"(p.n_x), "s"(p.n_shift), "s"(p.shift), "s"(p.mix[0]), "s"(p.mix[NMIX - 1]),
+                 "s"(p.out[0]), "s"(p.out[NMIX - 1]), "s"(p.out_frag), "s"(p.x_parts), "s"(p.part_stride));
+  } else {
+    asm volatile("" ::"s"(p.C), "s"(p.rows), "s"(p.src_mul), "s"(p.src_add), "s"(p.x), "s"(p.residual),
+                 "s"(p.weight), "s"(p.bias), "s"(p.eps), "s"(p.x_out), "s"(p.y), "s"(p.out_frag));
+  }
   // Frag outputs: 8 consecutive rows share each 128-byte line of the output, so those rows
   // are given to workgroups of one XCD (workgroup b runs on XCD b % 8): row block x of
   // rows / 8 rows goes to XCD x, and the partial-line stores meet in one L2.
@@ -104,17 +139,127 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
                           : (int64_t)blockIdx.x;
   const int tid = threadIdx.x;
   const int C = p.C;
-  const int64_t xrow = p.x_rows ? (int64_t)p.x_rows[row] : row * p.src_mul + p.src_add;
-  const int64_t src = xrow * (int64_t)C;
   const int64_t rrow = row * p.src_mul + p.src_add;  // residual row
   const int64_t rsrc = rrow * (int64_t)C;
   const int64_t dst = row * (int64_t)C;
-  const int64_t srow = p.shift_slots ? (int64_t)p.shift_slots[row] : row;
+  // Index-table lookups first, as vector loads (a scalar load would be waited for before
+  // the row's loads issue), so their round trip overlaps the row's loads below and the
+  // shift row can be requested as soon as its slot arrives.
+  int32_t slot_raw = 0, xrow_raw = 0;
+  if constexpr (NMIX > 0) {
+    if constexpr (kSlots) slot_raw = ld_vgpr(p.shift_slots + row);
+    if (p.x_rows) xrow_raw = ld_vgpr(p.x_rows + row);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Vector path: every input of the row -- x, residual, the LN weight and bias, the
+  // previous token's shift row and the mix vectors -- is requested before the two
+  // reductions, so the row costs one memory round trip instead of several.  The loads sit
+  // outside any branch (a lane past C reads the row's last 8 values and discards them),
+  // so they all issue back to back; loads that need no index table go out first, the
+  // x_rows / shift_slots lookups (a dependent round trip) overlap them, and the shift row,
+  // needed only by the final lerp, is requested last.
+  constexpr bool kVec = VW == 8 && !kBf16;
+  constexpr int kPre = kVec ? NV : 1;
+  auto col = [&](int n) {
+    const int c = (tid + n * kThreads) * VW;
+    return c < C ? c : C - VW;
+  };
+  h8 wpre[kPre], bpre[kPre], ppre[kPre], mpre[kPre][NMIX > 0 ? NMIX : 1];
+  if constexpr (kVec) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int cl = col(n);
+      wpre[n] = ld8(reinterpret_cast<const _Float16*>(p.weight) + cl);
+      bpre[n] = ld8(reinterpret_cast<const _Float16*>(p.bias) + cl);
+      if constexpr (NMIX > 0) {
+#pragma unroll
+        for (int i = 0; i < NMIX; ++i) mpre[n][i] = ld8(p.mix[i] + cl);
+      }
+    }
+  }
+
+  float v[NV][VW];
+  float sum = 0.0f;
+  // Vector path in two halves: issue_row requests x (or its K-part planes) and the
+  // residual into raw registers; finish_row, behind a scheduling barrier, converts them
+  // and forms the running sum, so no load waits for an earlier one's data.
+  h8 xraw[kPre], rraw[kPre];
+  f4 praw[kPre][NP > 0 ? NP : 1][2];
+  auto issue_row = [&](int64_t src) {
+#pragma unroll
+    for (int n = 0; n < kPre; ++n) {
+      const int cl = col(n);
+      if constexpr (NP > 0) {
+        const float* xp = p.x_parts + dst + cl;
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          praw[n][q][0] = *reinterpret_cast<const f4*>(xp + q * p.part_stride);
+          praw[n][q][1] = *reinterpret_cast<const f4*>(xp + q * p.part_stride + 4);
+        }
+      } else {
+        xraw[n] = ld8(reinterpret_cast<const _Float16*>(p.x) + src + cl);
+      }
+      if (p.residual) rraw[n] = ld8(p.residual + rsrc + cl);
+    }
+  };
+  auto finish_row = [&]() {
+#pragma unroll
+    for (int n = 0; n < kPre; ++n) {
+      const bool in = (tid + n * kThreads) * VW < C;
+      if constexpr (NP > 0) {
+        // the split GEMM's epilogue: parts added in K order, rounded to fp16
+        f4 a0 = praw[n][0][0], a1 = praw[n][0][1];
+#pragma unroll
+        for (int q = 1; q < NP; ++q) {
+          a0 += praw[n][q][0];
+          a1 += praw[n][q][1];
+        }
+        const float xs[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[n][e] = (float)(_Float16)xs[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[n][e] = (float)xraw[n].v[e];
+      }
+      if (p.residual) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)rraw[n].v[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += in ? v[n][e] : 0.0f;
+    }
+  };
+  // Scalar path (C not a multiple of 8, unaligned rows, or the bf16 table).
+  auto load_row_scalar = [&](int64_t src) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int c0 = (tid + n * kThreads) * VW;
+      if (c0 < C) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          v[n][e] = ld_in<kBf16>(p.x, src + c0 + e);
+          if (p.residual) v[n][e] = v[n][e] + (float)p.residual[rsrc + c0 + e];
+        }
+#pragma unroll
+        for (int e = 0; e < VW; ++e) sum += v[n][e];
+      }
+    }
+  };
+  const bool gather = NMIX > 0 && p.x_rows;
+  const int64_t src0 = (row * p.src_mul + p.src_add) * (int64_t)C;
+  if constexpr (kVec) {
+    if (!gather) issue_row(src0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  const int64_t srow = (NMIX > 0 && kSlots) ? (int64_t)__builtin_amdgcn_readfirstlane(slot_raw) : row;
   const int64_t sdst = srow * (int64_t)C;
+  const int64_t xrow = __builtin_amdgcn_readfirstlane(xrow_raw);
   if constexpr (NMIX > 0) {
     // An index outside its table (x_rows past the embedding, shift_slots past the pool):
     // the row's outputs are NaN and no shift row is read or written.  Block-uniform.
-    if ((p.x_rows && (xrow < 0 || xrow >= p.n_x)) || (p.shift_slots && (srow < 0 || srow >= p.n_shift))) {
+    if ((p.x_rows && (xrow < 0 || xrow >= p.n_x)) || (kSlots && (srow < 0 || srow >= p.n_shift))) {
       const _Float16 nan = (_Float16)__builtin_nanf("");
       for (int c = tid; c < C; c += kThreads) {
         p.x_out[dst + c] = nan;
@@ -124,73 +269,15 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       }
       return;
     }
-  }
-
-  // Vector path: every input of the row -- x, residual, the LN weight and bias, the
-  // previous token's shift row and the mix vectors -- is requested here, before the
-  // two reductions, so the row costs one memory round trip instead of three.
-  constexpr bool kVec = VW == 8 && !kBf16;
-  constexpr int kPre = kVec ? NV : 1;
-  h8 wpre[kPre], bpre[kPre], ppre[kPre], mpre[kPre][NMIX > 0 ? NMIX : 1];
-  if constexpr (kVec) {
+    if constexpr (kVec) {
+      if (gather) issue_row(xrow * (int64_t)C);
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-      const int c0 = (tid + n * kThreads) * VW;
-      if (c0 < C) {
-        wpre[n] = ld8(reinterpret_cast<const _Float16*>(p.weight) + c0);
-        bpre[n] = ld8(reinterpret_cast<const _Float16*>(p.bias) + c0);
-        if constexpr (NMIX > 0) {
-          ppre[n] = ld8(p.shift + sdst + c0);
-#pragma unroll
-          for (int i = 0; i < NMIX; ++i) mpre[n][i] = ld8(p.mix[i] + c0);
-        }
-      }
+      for (int n = 0; n < NV; ++n) ppre[n] = ld8(p.shift + sdst + col(n));
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-
-  float v[NV][VW];
-  float sum = 0.0f;
-#pragma unroll
-  for (int n = 0; n < NV; ++n) {
-    const int c0 = (tid + n * kThreads) * VW;
-    if (c0 < C) {
-      if constexpr (kVec && NP > 0) {
-        // the split GEMM's epilogue: parts added in K order, rounded to fp16
-        const float* xp = p.x_parts + dst + c0;
-        f4 a0 = *reinterpret_cast<const f4*>(xp), a1 = *reinterpret_cast<const f4*>(xp + 4);
-#pragma unroll
-        for (int q = 1; q < NP; ++q) {
-          a0 += *reinterpret_cast<const f4*>(xp + q * p.part_stride);
-          a1 += *reinterpret_cast<const f4*>(xp + q * p.part_stride + 4);
-        }
-        const float xs[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[n][e] = (float)(_Float16)xs[e];
-        if (p.residual) {
-          const h8 rv = ld8(p.residual + rsrc + c0);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)rv.v[e];
-        }
-      } else if constexpr (kVec) {
-        const h8 xv = ld8(reinterpret_cast<const _Float16*>(p.x) + src + c0);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[n][e] = (float)xv.v[e];
-        if (p.residual) {
-          const h8 rv = ld8(p.residual + rsrc + c0);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)rv.v[e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < VW; ++e) {
-          v[n][e] = ld_in<kBf16>(p.x, src + c0 + e);
-          if (p.residual) v[n][e] = v[n][e] + (float)p.residual[rsrc + c0 + e];
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < VW; ++e) sum += v[n][e];
-    }
-  }
+  if constexpr (kVec) finish_row();
+  else load_row_scalar(NMIX > 0 && p.x_rows ? xrow * (int64_t)C : src0);
   const float mean = block_sum_ln<kWaves>(sum, red[0]) / (float)C;
   float ss = 0.0f;
 #pragma unroll
@@ -293,16 +380,29 @@ int launch_ln(const char* fn, const LnArgs& p, bool vec_ok, hipStream_t stream) 
   VK_REQUIRE(!p.out_frag || (vec_ok && p.C % kFragPad == 0),
              "%s: frag output needs C %% %d == 0 and 16-byte aligned rows", fn, kFragPad);
   const dim3 grid((unsigned)p.rows), block(kThreads);
+  // launches instance K<..., kSlots> of the kernel, kSlots = (shift_slots given)
+#define VK_LN_GO(...)                                                                             \
+  do {                                                                                            \
+    bool launched = false;                                                                        \
+    if constexpr (NMIX > 0) {                                                                     \
+      if (p.shift_slots) {                                                                        \
+        hipLaunchKernelGGL((layer_norm_kernel<__VA_ARGS__, true>), grid, block, 0, stream, p);    \
+        launched = true;                                                                          \
+      }                                                                                           \
+    }                                                                                             \
+    if (!launched)                                                                                \
+      hipLaunchKernelGGL((layer_norm_kernel<__VA_ARGS__, false>), grid, block, 0, stream, p);     \
+  } while (0)
   if constexpr (NMIX > 0 && !kBf16) {
     if (p.x_parts) {
       VK_REQUIRE(vec_ok && p.C % kFragPad == 0 && p.C <= 4096,
                  "%s: K-part input needs C %% %d == 0, C <= 4096 and 16-byte aligned rows", fn, kFragPad);
       const bool one = p.C <= 8 * kThreads;
-#define VK_LN_PARTS(np)                                                                                  \
-  if (p.n_parts == np) {                                                                                 \
-    if (one) hipLaunchKernelGGL((layer_norm_kernel<8, 1, NMIX, false, np>), grid, block, 0, stream, p);  \
-    else hipLaunchKernelGGL((layer_norm_kernel<8, 2, NMIX, false, np>), grid, block, 0, stream, p);      \
-    return check_launch(fn);                                                                             \
+#define VK_LN_PARTS(np)                                 \
+  if (p.n_parts == np) {                                \
+    if (one) VK_LN_GO(8, 1, NMIX, false, np);           \
+    else VK_LN_GO(8, 2, NMIX, false, np);               \
+    return check_launch(fn);                            \
   }
       VK_LN_PARTS(2)
       VK_LN_PARTS(4)
@@ -313,14 +413,15 @@ int launch_ln(const char* fn, const LnArgs& p, bool vec_ok, hipStream_t stream) 
   }
   if (vec_ok && p.C % 8 == 0) {
     const int per = (p.C / 8 + kThreads - 1) / kThreads;  // 1..4
-    if (per == 1) hipLaunchKernelGGL((layer_norm_kernel<8, 1, NMIX, kBf16>), grid, block, 0, stream, p);
-    else if (per == 2) hipLaunchKernelGGL((layer_norm_kernel<8, 2, NMIX, kBf16>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((layer_norm_kernel<8, 4, NMIX, kBf16>), grid, block, 0, stream, p);
+    if (per == 1) VK_LN_GO(8, 1, NMIX, kBf16, 0);
+    else if (per == 2) VK_LN_GO(8, 2, NMIX, kBf16, 0);
+    else VK_LN_GO(8, 4, NMIX, kBf16, 0);
   } else {
     const int per = (p.C + kThreads - 1) / kThreads;  // 1..32
-    if (per <= 8) hipLaunchKernelGGL((layer_norm_kernel<1, 8, NMIX, kBf16>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((layer_norm_kernel<1, 32, NMIX, kBf16>), grid, block, 0, stream, p);
+    if (per <= 8) VK_LN_GO(1, 8, NMIX, kBf16, 0);
+    else VK_LN_GO(1, 32, NMIX, kBf16, 0);
   }
+#undef VK_LN_GO
   return check_launch(fn);
 }
 
