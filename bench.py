@@ -213,9 +213,9 @@ def prefill_c2(dev, steps, warmup=2):
     ms = ev0.elapsed_time(ev1) / steps
     nbytes = 7 * Bp * Tp * C * 2 + 2 * Bp * H * HEAD * HEAD * 4 + Bp * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    # matrix-core work the chunked kernel issues: 4 waves x 128 v_mfma_f32_16x16x4_f32
-    # (2048 flops each) per 16-token chunk and head
-    mfma_flops = Bp * H * ((Tp + 15) // 16) * 4 * 128 * 2048
+    # matrix-core work the chunked kernel issues per 16-token chunk and head: 4 state waves x 80
+    # v_mfma_f32_16x16x4_f32 (2048 flops each), 4 x 16 for the chunk matrices, 36 for W^T
+    mfma_flops = Bp * H * ((Tp + 15) // 16) * (4 * 80 + 4 * 16 + 36) * 2048
     del r, w, k, v, a, b, pool, y
     torch.cuda.empty_cache()
     return {
@@ -229,8 +229,8 @@ def prefill_c2(dev, steps, warmup=2):
                      "achieved": round(mfma_flops / (ms * 1e-3) / 1e12, 2), "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(mfma_flops / (ms * 1e-3) / 1e12 / 157.3, 4), "flops_per_call": mfma_flops,
                      "hbm_GBps": round(gbs, 2), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes},
-        "kernel": "wkv7_fp32_chunk_kernel (one 256-lane workgroup per (sequence, head), 16-token chunks on "
-                  "v_mfma_f32_16x16x4_f32)",
+        "kernel": "wkv7_fp32_chunk_kernel (one 512-lane workgroup per (sequence, head): 4 state waves + 4 "
+                  "waves preparing later chunks; 16-token chunks on v_mfma_f32_16x16x4_f32)",
     }
 
 

@@ -519,24 +519,28 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
 // d_min^16 (d > 0.545 for every w, so > 6e-5): fp32 holds them without overflow, and the
 // results agree with the token-by-token recurrence to fp32 rounding.
 //
-// One 256-lane workgroup per (sequence, head); wave w owns the state rows (value index)
-// i = 16w .. 16w + 15, which evolve independently, as X^T tiles (16 x 16, j x i) in the
-// accumulator layout of v_mfma_f32_16x16x4_f32 (lane l, register r: row 4 (l / 16) + r,
+// One 512-lane workgroup per (sequence, head).  State wave w (0-3) owns the state rows
+// (value index) i = 16w .. 16w + 15, which evolve independently, as X^T tiles (16 x 16, j x i)
+// in the accumulator layout of v_mfma_f32_16x16x4_f32 (lane l, register r: row 4 (l / 16) + r,
 // column l % 16; written D(M) below).  D(M) serves directly as the B operand of a product
 // M' M when the k index is walked in the permuted order k = 4 (l / 16) + s over the 4 steps
 // s of a 16-wide k tile (a sum over k does not depend on its order), and D(M^T) as the A
 // operand of M M'; every other operand is read from LDS in the same permuted order.
 //
-// Pipeline: iteration c runs, in one block between two barriers, chunk c against the state
-// (Â X0^T, R̂ X0^T, K̂^T V, then Z, Y and B̂^T Z), chunk c + 1's four L x L matrices (one per
-// wave) and chunk c + 2's hat vectors (VALU work: Λ by a multiplicative DPP scan over the 16
-// lanes that hold one channel quad's tokens), so the scheduler interleaves the three; hat
-// vectors live in three LDS buffers, the matrices in two.  Each wave forms W^T =
-// ((I - N)^{-1})^T of chunk c from the powers of N next to the state products (N is
-// nilpotent, N^16 = 0, so (I - N)^{-1} = (I + N)(I + N^2)(I + N^4)(I + N^8); the powers in
-// both orientations: D(M^2) = Σ_s D(M^T)[s] x D(M)[s]), so the dependent chain of a chunk
-// is Â X0^T -> Z -> B̂^T Z.  (Back substitution on the vector ALU instead measured 25 %
-// slower.)  Per chunk and wave: 128 MFMAs, one barrier.
+// Pipeline (one barrier per chunk): in iteration c the state waves run chunk c against the
+// state (Â X0^T, R̂ X0^T, K̂^T V, then Z = W RHS, Y and B̂^T Z: the dependent chain of a
+// chunk), while matrix waves 4-7 prepare chunk c + 3's hat vectors (VALU work: Λ by a
+// multiplicative DPP scan over the 16 lanes that hold one channel quad's tokens), chunk
+// c + 2's four L x L matrices and chunk c + 1's W^T from its N (described at the kernel).
+// Per chunk: 80 MFMAs on each state wave, 116 / 112 / 96 / 96 on the four SIMDs.  Measured
+// at config 2: 0.20 ms per call against 0.24 ms for the form with four waves, each running
+// all three stages for its own rows (132 MFMAs per wave, W^T computed four times).  The
+// matrix core and the vector ALU of a SIMD do not overlap across its two waves on gfx950
+// (a loop of MFMAs on one wave beside a loop of FMAs on the other takes the sum of both
+// times), so the split gains from moving the redundant W^T work out and from the second
+// wave filling dependency stalls, not from concurrent execution.  (W^T by forward
+// substitution on the vector ALU measured 5 % slower; back substitution of Z on the state
+// waves 25 % slower.)
 constexpr int kCL = 16;          // tokens per chunk
 constexpr int kChunkMinT = 16;   // shorter prefills take the row-split kernel
 constexpr int kHP = kHead + 4;   // padded LDS row of a [t][j] hat vector (floats)
@@ -568,48 +572,61 @@ struct ChunkLds {
   // 16 tokens that one row of 16 lanes reads (one channel quad each) over distinct banks:
   // with 128-byte rows they would all fall on two.
   hv8 raw[2][6 * kCL][9];
-  __attribute__((aligned(16))) float lamL[3][kHead];         // Λ_L
-  __attribute__((aligned(16))) float hat[3][4][kCL][kHP];    // Â, R̂, B̂, K̂ as [t][j]
-  __attribute__((aligned(16))) float hatT[3][3][kHead][kTP]; // B̂^T, K̂^T as [j][t]; V^T as [i][t]
-  __attribute__((aligned(16))) float gram[2][4][kCL][kTP];   // N, T_ak, T_rb, T_rk as [t][m]
-  __attribute__((aligned(16))) float gramT[2][4][kCL][kTP];  // the same as [m][t]
+  __attribute__((aligned(16))) float lamL[4][kHead];         // Λ_L
+  __attribute__((aligned(16))) float hat[4][2][kCL][kHP];    // Â, R̂ as [t][j]
+  __attribute__((aligned(16))) float hatT[4][3][kHead][kTP]; // B̂^T, K̂^T as [j][t]; V^T as [i][t]
+  __attribute__((aligned(16))) float gram[3][4][kCL][kTP];   // N, T_ak, T_rb, T_rk as [t][m]
+  __attribute__((aligned(16))) float gramT[3][kCL][kTP];     // N as [m][t]
+  __attribute__((aligned(16))) fq4 wt[2][64];                // D(W^T) of a chunk, lane by lane
   __attribute__((aligned(16))) float lamSink[256];           // Λ stores of lanes that hold no Λ_L
 };
 
-// One workgroup per CU (the LDS pipeline takes 150 KiB): the compiler may use every register.
+// Eight waves in two roles, two per SIMD (waves w and w + 4 share SIMD w), so that each
+// SIMD interleaves two independent instruction streams.  State waves 0-3 own the state rows
+// and run chunk c's state products.  Matrix waves 4-7 prepare the chunks ahead of it: all four
+// the hat vectors of chunk c + 3 (and the token-vector staging), waves 5-7 the L x L matrices
+// of chunk c + 2 (N and T_ak on wave 5, whose operands share Â), and wave 4 W^T of chunk c + 1
+// from its N (computed one iteration earlier), which keeps W^T's dependent chain of 24
+// products off the iteration that produces N and balances the matrix work over the SIMDs
+// (116 / 112 / 96 / 96 products per SIMD and chunk).  One barrier per chunk.  The LDS
+// pipeline (four hat buffers, three matrix buffers) takes 144 KiB: one workgroup per CU.
 template <bool kSlots>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
+__global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
   const Fp32Args& p = ra.a;
   __shared__ ChunkLds L;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int li = lane & 15, g = lane >> 4;
+  const bool state_wave = w < 4;
+  const int mtid = tid & 255;  // thread index inside its role
   const int bh = blockIdx.x, bi = bh / p.H, h = bh - bi * p.H;
   const int T = p.T, C = p.C;
   const size_t tok0 = (size_t)bi * T * C + (size_t)h * kHead;
   float* S = state_block<kSlots>(p, bi, h);
   if (S == nullptr) {
-    for (int idx = tid; idx < T * kHead; idx += 256)
+    for (int idx = tid; idx < T * kHead; idx += 512)
       p.y[tok0 + (size_t)(idx / kHead) * C + (idx % kHead)] = (_Float16)__builtin_nanf("");
     return;
   }
-  const int iw = 16 * w + li;  // this lane's state row (value index) in the accumulator layout
+  const int iw = 16 * (w & 3) + li;  // a state wave lane's state row (value index), accumulator layout
   // X^T tile q (j = 16 q .. 16 q + 15): register r holds X^T[16 q + 4 g + r][iw] = S[iw][16 q + 4 g + r]
   fq4 st[4];
+  if (state_wave) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) st[q] = *reinterpret_cast<const fq4*>(S + iw * kHead + 16 * q + 4 * g);
+    for (int q = 0; q < 4; ++q) st[q] = *reinterpret_cast<const fq4*>(S + iw * kHead + 16 * q + 4 * g);
+  }
 
-  // raw token vectors: piece c = tid + 256 u is vector c >> 7, token (c >> 3) & 15, channels
-  // 8 (c & 7) .. + 7; tokens past T re-read token T - 1 (masked out below)
+  // raw token vectors (matrix waves): piece c = mtid + 256 u is vector c >> 7, token
+  // (c >> 3) & 15, channels 8 (c & 7) .. + 7; tokens past T re-read token T - 1 (masked out below)
   const _Float16* src[6] = {p.r, p.w, p.k, p.v, p.a, p.b};
   hv8 pre[3];
   auto load_raw = [&](int t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < 3; ++u) {
-      const int c = tid + 256 * u;
+      const int c = mtid + 256 * u;
       const int t = min(t0 + ((c >> 3) & 15), T - 1);
       const _Float16* at = src[c >> 7] + tok0 + (size_t)t * C + (c & 7) * 8;
       // a global (not flat) load: a flat load would also count against the LDS counter,
-      // and every wait for the LDS reads below would wait for this prefetch
+      // and every wait for the LDS reads would wait for this prefetch
       if (ra.vec) {
         pre[u] = *(global_hv8*)at;
       } else {
@@ -621,16 +638,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto store_raw = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < 3; ++u) {
-      const int c = tid + 256 * u;
+      const int c = mtid + 256 * u;
       L.raw[buf][c >> 3][c & 7] = pre[u];  // row (vector, token) c >> 3, channels 8 (c & 7) ..
     }
   };
 
-  // hat vectors of chunk cc (raw buffer cc & 1) into hat buffer cc % 3: thread = token ht,
-  // channels j0 .. j0 + 3 (16 lanes of a row hold one quad's 16 tokens: the Λ scan).  A
-  // chunk past the end computes stale values nobody reads.  Split into the LDS reads and
-  // the arithmetic, so the reads can be issued early.
-  const int ht = lane & 15, j0 = 4 * (tid >> 4);
+  // hat vectors of chunk cc (raw buffer cc & 1) into hat buffer cc % 4 (matrix waves): thread =
+  // token ht, channels j0 .. j0 + 3 (16 lanes of a row hold one quad's 16 tokens: the Λ
+  // scan).  A chunk past the end computes stale values nobody reads.  Split into the LDS
+  // reads and the arithmetic, so the reads can be issued early.
+  const int ht = lane & 15, j0 = 4 * (mtid >> 4);
   struct RawQuad {
     hv4 r, w, k, v, a, b;
   };
@@ -642,7 +659,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     return RawQuad{rd4(0), rd4(1), rd4(2), rd4(3), rd4(4), rd4(5)};
   };
   auto hats_write = [&](int cc, const RawQuad& x) __attribute__((always_inline)) {
-    const int b = cc % 3;
+    const int b = cc & 3;
     const int n = min(kCL, T - cc * kCL);
     const float in = ht < n ? 1.0f : 0.0f;  // padded tokens: d = 1 and zero vectors (a select, no branch)
     float l1[4], l0[4];
@@ -669,96 +686,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     *reinterpret_cast<fq4*>(&L.hat[b][0][ht][j0]) = fq4{ah[0], ah[1], ah[2], ah[3]};
     *reinterpret_cast<fq4*>(&L.hat[b][1][ht][j0]) = fq4{rh[0], rh[1], rh[2], rh[3]};
-    *reinterpret_cast<fq4*>(&L.hat[b][2][ht][j0]) = fq4{bh[0], bh[1], bh[2], bh[3]};
-    *reinterpret_cast<fq4*>(&L.hat[b][3][ht][j0]) = fq4{kh[0], kh[1], kh[2], kh[3]};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       L.hatT[b][0][j0 + e][ht] = bh[e];
       L.hatT[b][1][j0 + e][ht] = kh[e];
       L.hatT[b][2][j0 + e][ht] = vv[e];
     }
-    float* lamDst = ht == kCL - 1 ? &L.lamL[b][j0] : &L.lamSink[4 * (tid >> 2) & 252];
+    float* lamDst = ht == kCL - 1 ? &L.lamL[b][j0] : &L.lamSink[4 * (mtid >> 2) & 252];
     *reinterpret_cast<fq4*>(lamDst) = fq4{l1[0], l1[1], l1[2], l1[3]};
   };
-  // wave w: the L x L matrix w of chunk cc (hat buffer cc % 3, matrix buffer cc & 1):
-  // (Â,B̂) (Â,K̂) (R̂,B̂) (R̂,K̂), masked (strictly lower for the first two)
-  const int xsel = w < 2 ? 0 : 1, ysel = (w & 1) ? 3 : 2, mlim = w < 2 ? 1 : 0;
-  struct GramOps {
-    fq4 x[4], y[4];
-  };
-  auto gram_read = [&](int cc) __attribute__((always_inline)) {
-    const int hb = cc % 3;
-    GramOps o;
+  // L x L matrix (x, y) of chunk cc into matrix buffer cc % 3, slot m: (Â,B̂) (Â,K̂) (R̂,B̂)
+  // (R̂,K̂) for m = 0..3, masked (strictly lower for the first two); N also transposed.  The x
+  // operands come from hat ([t][j], one 16-byte read per k step), the y operands from hatT.
+  auto gram_x = [&](int cc, int xsel, fq4 (&x)[4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      o.x[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][xsel][li][16 * q + 4 * g]);
-      o.y[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][ysel][li][16 * q + 4 * g]);
-    }
-    return o;
+    for (int q = 0; q < 4; ++q) x[q] = *reinterpret_cast<const fq4*>(&L.hat[cc & 3][xsel][li][16 * q + 4 * g]);
   };
-  auto gram_mfma = [&](const GramOps& o) __attribute__((always_inline)) {
+  auto gram_y = [&](int cc, int ysel, fq4 (&y)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) y[q][s2] = L.hatT[cc & 3][ysel][16 * q + 4 * g + s2][li];
+  };
+  auto gram_mfma = [&](const fq4 (&x)[4], const fq4 (&y)[4]) __attribute__((always_inline)) {
     fq4 gm = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) gm = mfma4(o.x[q][s2], o.y[q][s2], gm);
+      for (int s2 = 0; s2 < 4; ++s2) gm = mfma4(x[q][s2], y[q][s2], gm);
     return gm;
   };
-  auto gram_write = [&](int cc, const fq4& gm) __attribute__((always_inline)) {
-    const int b = cc & 1;
+  auto gram_write = [&](int cc, int m, const fq4& gm) __attribute__((always_inline)) {
+    const int b = cc % 3, mlim = m < 2 ? 1 : 0;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 4 * g + r;
       const float x = li <= t - mlim ? gm[r] : 0.0f;
-      L.gram[b][w][t][li] = x;
-      L.gramT[b][w][li][t] = x;
+      L.gram[b][m][t][li] = x;
+      if (m == 0) L.gramT[b][li][t] = x;
     }
   };
-
-  const int nchunk = (T + kCL - 1) / kCL;
-  // prologue: chunk 0's matrices and chunk 1's hats; chunk 2's raw vectors staged, chunk 3's
-  // loaded.  (Chunks past the end read token T - 1 and are never used.)
-  load_raw(0);
-  store_raw(0);
-  load_raw(kCL);
-  __syncthreads();
-  hats_write(0, hats_read(0));
-  store_raw(1);
-  load_raw(2 * kCL);
-  __syncthreads();
-  hats_write(1, hats_read(1));
-  gram_write(0, gram_mfma(gram_read(0)));
-  store_raw(0);
-  load_raw(3 * kCL);
-  __syncthreads();
-  for (int c = 0; c < nchunk; ++c) {
-    const int b = c & 1, hb = c % 3;
-    const int n = min(kCL, T - c * kCL);
-    // ---- phase 1: every LDS operand of the iteration
-    fq4 pm[4], pmt[4];  // pm[k] = D(N^(2^k)), pmt[k] = D((N^(2^k))^T)
-    pm[0] = *reinterpret_cast<const fq4*>(&L.gramT[b][0][li][4 * g]);
-    pmt[0] = *reinterpret_cast<const fq4*>(&L.gram[b][0][li][4 * g]);
-    fq4 a4[4], r4[4], k4[4], b4[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      a4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][0][li][16 * q + 4 * g]);
-      r4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][1][li][16 * q + 4 * g]);
-      k4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][1][16 * q + li][4 * g]);
+  // wave 5: N and T_ak; wave 6: T_rb; wave 7: T_rk
+  auto grams = [&](int cc) __attribute__((always_inline)) {
+    if (w == 5) {
+      fq4 x[4], yb[4], yk[4];
+      gram_x(cc, 0, x);
+      gram_y(cc, 0, yb);
+      gram_y(cc, 1, yk);
+      const fq4 gn = gram_mfma(x, yb), gk = gram_mfma(x, yk);
+      gram_write(cc, 0, gn);
+      gram_write(cc, 1, gk);
+    } else if (w >= 6) {
+      fq4 x[4], y[4];
+      gram_x(cc, 1, x);
+      gram_y(cc, w == 6 ? 0 : 1, y);
+      gram_write(cc, w == 6 ? 2 : 3, gram_mfma(x, y));
     }
-    const fq4 v4 = *reinterpret_cast<const fq4*>(&L.hatT[hb][2][iw][4 * g]);
-    const GramOps go = gram_read(c + 1);
-    const RawQuad rq = hats_read(c + 2);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) b4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][0][16 * q + li][4 * g]);
-    const fq4 tak = *reinterpret_cast<const fq4*>(&L.gram[b][1][li][4 * g]);
-    const fq4 trb = *reinterpret_cast<const fq4*>(&L.gram[b][2][li][4 * g]);
-    const fq4 trk = *reinterpret_cast<const fq4*>(&L.gram[b][3][li][4 * g]);
-    fq4 lamq[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) lamq[q] = *reinterpret_cast<const fq4*>(&L.lamL[hb][16 * q + 4 * g]);
-    __builtin_amdgcn_sched_barrier(0);
-    // ---- phase 2 (independent chains, interleaved by the scheduler): W^T of this chunk,
-    // Â X0^T, R̂ X0^T, K̂^T V, chunk c + 1's matrix, chunk c + 2's hat vectors
+  };
+  // wave 4: W^T = ((I - N)^{-1})^T of chunk cc into wt buffer cc & 1.  N is nilpotent,
+  // N^16 = 0, so (I - N)^{-1} = (I + N)(I + N^2)(I + N^4)(I + N^8); the powers in both
+  // orientations: D(M^2) = Σ_s D(M^T)[s] x D(M)[s].
+  auto w_transpose = [&](int cc) __attribute__((always_inline)) {
+    const int b = cc % 3;
+    fq4 pm[4], pmt[4];  // pm[k] = D(N^(2^k)), pmt[k] = D((N^(2^k))^T)
+    pm[0] = *reinterpret_cast<const fq4*>(&L.gramT[b][li][4 * g]);
+    pmt[0] = *reinterpret_cast<const fq4*>(&L.gram[b][0][li][4 * g]);
 #pragma unroll
     for (int k = 1; k < 4; ++k) {
       fq4 x = {0.0f, 0.0f, 0.0f, 0.0f}, y = x;
@@ -782,64 +774,126 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int s2 = 0; s2 < 4; ++s2) x = mfma4(pm[k][s2], wt[s2], x);
       wt = x;
     }
-    fq4 p1 = {0.0f, 0.0f, 0.0f, 0.0f}, y1 = p1;
+    L.wt[cc & 1][lane] = wt;
+  };
+
+  const int nchunk = (T + kCL - 1) / kCL;
+  // prologue (matrix waves): hats of chunks 0-2, matrices of chunks 0-1, W^T of chunk 0; chunk
+  // 3's raw vectors staged, chunk 4's loaded.  (Chunks past the end read token T - 1 and are
+  // never used.)
+  if (!state_wave) {
+    load_raw(0);
+    store_raw(0);
+    load_raw(kCL);
+  }
+  __syncthreads();
+  if (!state_wave) {
+    hats_write(0, hats_read(0));
+    store_raw(1);
+    load_raw(2 * kCL);
+  }
+  __syncthreads();
+  if (!state_wave) {
+    hats_write(1, hats_read(1));
+    grams(0);
+    store_raw(0);
+    load_raw(3 * kCL);
+  }
+  __syncthreads();
+  if (!state_wave) {
+    hats_write(2, hats_read(2));
+    grams(1);
+    if (w == 4) w_transpose(0);
+    store_raw(1);
+    load_raw(4 * kCL);
+  }
+  __syncthreads();
+  for (int c = 0; c < nchunk; ++c) {
+    if (state_wave) {
+      // ---- chunk c against the state:  RHS = Â X0^T + T_ak V;  Y = R̂ X0^T + T_rk V + T_rb Z
+      // with Z = W RHS;  X^T += K̂^T V + B̂^T Z;  S^T = diag(Λ_L) X^T
+      const int hb = c & 3, gb = c % 3;
+      const int n = min(kCL, T - c * kCL);
+      const fq4 wt = L.wt[c & 1][lane];
+      fq4 a4[4], r4[4], k4[4], b4[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < 4; ++q) {
+        a4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][0][li][16 * q + 4 * g]);
+        r4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][1][li][16 * q + 4 * g]);
+        k4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][1][16 * q + li][4 * g]);
+      }
+      const fq4 v4 = *reinterpret_cast<const fq4*>(&L.hatT[hb][2][iw][4 * g]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][0][16 * q + li][4 * g]);
+      const fq4 tak = *reinterpret_cast<const fq4*>(&L.gram[gb][1][li][4 * g]);
+      const fq4 trb = *reinterpret_cast<const fq4*>(&L.gram[gb][2][li][4 * g]);
+      const fq4 trk = *reinterpret_cast<const fq4*>(&L.gram[gb][3][li][4 * g]);
+      fq4 lamq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) lamq[q] = *reinterpret_cast<const fq4*>(&L.lamL[hb][16 * q + 4 * g]);
+      __builtin_amdgcn_sched_barrier(0);
+      fq4 p1 = {0.0f, 0.0f, 0.0f, 0.0f}, y1 = p1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          p1 = mfma4(a4[q][s2], st[q][s2], p1);
+          y1 = mfma4(r4[q][s2], st[q][s2], y1);
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) st[q] = mfma4(k4[q][s2], v4[s2], st[q]);
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
-        p1 = mfma4(a4[q][s2], st[q][s2], p1);
-        y1 = mfma4(r4[q][s2], st[q][s2], y1);
+        p1 = mfma4(tak[s2], v4[s2], p1);
+        y1 = mfma4(trk[s2], v4[s2], y1);
       }
+      fq4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+      for (int s2 = 0; s2 < 4; ++s2) z = mfma4(wt[s2], p1[s2], z);
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) st[q] = mfma4(k4[q][s2], v4[s2], st[q]);
-    const fq4 gm = gram_mfma(go);
-    hats_write(c + 2, rq);
-    // ---- phase 3: RHS = Â X0^T + T_ak V;  Y1 += T_rk V;  Z = W RHS;  Y = Y1 + T_rb Z;
-    // X^T += B̂^T Z;  S^T = diag(Λ_L) X^T
+      for (int s2 = 0; s2 < 4; ++s2) y1 = mfma4(trb[s2], z[s2], y1);
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      p1 = mfma4(tak[s2], v4[s2], p1);
-      y1 = mfma4(trk[s2], v4[s2], y1);
-    }
-    fq4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int q = 0; q < 4; ++q) {
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) z = mfma4(wt[s2], p1[s2], z);
+        for (int s2 = 0; s2 < 4; ++s2) st[q] = mfma4(b4[q][s2], z[s2], st[q]);
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) y1 = mfma4(trb[s2], z[s2], y1);
+        for (int r = 0; r < 4; ++r) st[q][r] *= lamq[q][r];
+      }
+      // y rows t = 4 g + r of this wave's 16 value columns
+      _Float16 yh[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+      for (int r = 0; r < 4; ++r) {
+        float yv = y1[r];
+        asm volatile("" : "+v"(yv));  // an fp32 value before the fp16 conversion
+        yh[r] = (_Float16)yv;
+      }
+      _Float16* yp = p.y + tok0 + (size_t)(c * kCL + 4 * g) * C + iw;
+      if (n == kCL) {
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) st[q] = mfma4(b4[q][s2], z[s2], st[q]);
+        for (int r = 0; r < 4; ++r) yp[(size_t)r * C] = yh[r];
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) st[q][r] *= lamq[q][r];
-    }
-    gram_write(c + 1, gm);
-    // y rows t = 4 g + r of this wave's 16 value columns
-    _Float16 yh[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float yv = y1[r];
-      asm volatile("" : "+v"(yv));  // an fp32 value before the fp16 conversion
-      yh[r] = (_Float16)yv;
-    }
-    _Float16* yp = p.y + tok0 + (size_t)(c * kCL + 4 * g) * C + iw;
-    if (n == kCL) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) yp[(size_t)r * C] = yh[r];
+        for (int r = 0; r < 4; ++r)
+          if (4 * g + r < n) yp[(size_t)r * C] = yh[r];
+      }
     } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (4 * g + r < n) yp[(size_t)r * C] = yh[r];
+      // ---- chunk c + 3's hat vectors, chunk c + 2's matrices, chunk c + 1's W^T; chunk c + 4's
+      // raw vectors into the buffer chunk c + 2's hats were read from (one iteration ago)
+      const RawQuad rq = hats_read(c + 3);
+      grams(c + 2);
+      if (w == 4) w_transpose(c + 1);
+      hats_write(c + 3, rq);
+      store_raw(c & 1);
+      load_raw((c + 5) * kCL);
     }
-    // chunk c + 3's raw vectors into the buffer chunk c + 1's hats read (one iteration ago)
-    store_raw((c + 1) & 1);
-    load_raw((c + 4) * kCL);
     __syncthreads();
   }
+  if (state_wave) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) *reinterpret_cast<fq4*>(S + iw * kHead + 16 * q + 4 * g) = st[q];
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<fq4*>(S + iw * kHead + 16 * q + 4 * g) = st[q];
+  }
 }
 
 bool rows_vec_ok(const Fp32Args& p) {
@@ -864,7 +918,7 @@ void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
   } else if (rows) {
     RowsArgs ra{p, rows_vec_ok(p) ? 1 : 0};
     if (p.T >= kChunkMinT)
-      hipLaunchKernelGGL(wkv7_fp32_chunk_kernel<kSlots>, dim3(B * p.H), dim3(256), 0, stream, ra);
+      hipLaunchKernelGGL(wkv7_fp32_chunk_kernel<kSlots>, dim3(B * p.H), dim3(512), 0, stream, ra);
     else if (ra.vec && B * p.H < 2 * device_cus())
       hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 1>), dim3(2 * B * p.H), dim3(256), 0, stream, ra);
     else
