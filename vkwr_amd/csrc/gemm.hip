@@ -499,13 +499,25 @@ template <int kEpi>
 __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv16 (&acc)[4][4], int m0, int n0,
                                               int wm, int wn, int lane) {
   const int lr = lane & 31, lh = lane >> 5, r8 = lane >> 3, c8 = 8 * (lane & 7);
+  // The problem's fields, held in SGPRs for the whole store loop (an asm output cannot be
+  // re-derived): left alone the compiler re-reads them from the kernel arguments before each
+  // store, and the wait for each such scalar load also waits for every LDS read in flight,
+  // which serialised the strips (the epilogue of a 256 x 256 tile took ~11 us).
+  // (Global address-space pointers, so the accesses stay global, not flat, ones: a flat
+  // access would count against the LDS counter too.)
+  typedef _Float16 __attribute__((address_space(1)))* gptr;
+  typedef const _Float16 __attribute__((address_space(1)))* gcptr;
+  int pm = P.m, pn = P.n;
+  gptr pcp = (gptr)P.c;
+  gcptr pvp = (gcptr)P.v, pvfp = (gcptr)P.vf, pv0p = (gcptr)P.v0;
+  asm("" : "+s"(pm), "+s"(pn), "+s"(pcp), "+s"(pvp), "+s"(pvfp), "+s"(pv0p));
   constexpr bool kVres = kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL;
   constexpr bool kCol = kVres || kEpi == VKWR_GEMM_EPI_BIAS;  // a per-column operand v0
   const int rowb = m0 + wm * 128 + r8, colb = n0 + wn * 128 + c8;
   hv8 ov0[2];
   if constexpr (kCol) {
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) ov0[jj] = *reinterpret_cast<const hv8*>(P.v0 + min(colb + jj * 64, P.n - 8));
+    for (int jj = 0; jj < 2; ++jj) ov0[jj] = *reinterpret_cast<const __attribute__((address_space(1))) hv8*>(pv0p + min(colb + jj * 64, pn - 8));
   }
   hv8 ov[2][4], ovf[2][4];
   auto load_ops = [&](int p) __attribute__((always_inline)) {
@@ -513,10 +525,10 @@ __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       const int row = rowb + (p >> 1) * 32 + 8 * h;
-      const bool in = row < P.m && col < P.n;
-      const int64_t idx = in ? (int64_t)row * P.n + col : 0;
-      ov[p & 1][h] = *reinterpret_cast<const hv8*>(P.v + idx);
-      ovf[p & 1][h] = *reinterpret_cast<const hv8*>(P.vf + idx);
+      const bool in = row < pm && col < pn;
+      const int64_t idx = in ? (int64_t)row * pn + col : 0;
+      ov[p & 1][h] = *reinterpret_cast<const __attribute__((address_space(1))) hv8*>(pvp + idx);
+      ovf[p & 1][h] = *reinterpret_cast<const __attribute__((address_space(1))) hv8*>(pvfp + idx);
     }
   };
   auto write_strip = [&](int p) __attribute__((always_inline)) {
@@ -568,7 +580,7 @@ __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv
           o[e] = (_Float16)y;
         }
       }
-      if (row < P.m && col < P.n) *reinterpret_cast<hv8*>(P.c + (int64_t)row * P.n + col) = o;
+      if (row < pm && col < pn) *reinterpret_cast<__attribute__((address_space(1))) hv8*>(pcp + (int64_t)row * pn + col) = o;
     }
   };
   if constexpr (kVres) load_ops(0);
