@@ -328,14 +328,36 @@ def _big_vs_rowmajor(gpu, shapes, epis, seed):
     ([(257, 64, 1000)], [1]),                        # one row past a tile, K of one stage, relu^2
     ([(768, 448, 1280)], [3]),                       # 15 tiles (not a multiple of the 8 XCDs), bias
     ([(600, 512, 700), (600, 512, 96), (600, 512, 256), (600, 512, 512)], [1, 0, 3, 2]),  # mixed epilogues
-    ([(2304, 4096, 4096)], [0]),                     # the 7B o-projection shape of a mixed step
-    ([(2304, 4096, 128), (2304, 4096, 512)], [4, 5]),  # 7B low-rank inputs (padded w, g): tanh, sigmoid
+    ([(2304, 4096, 4096)], [0]),                     # the 7B o-projection shape: 192-row tiles (192 of them)
     ([(2304, 128, 4096), (2304, 512, 4096)], [3, 2]),  # 7B low-rank outputs: bias, value residual
 ])
 def test_big_gemm_bitwise_equals_rowmajor_kernel(gpu, shapes, epis):
+    """Launches whose tiles all run whole (no k-parts), in 256- or 192-row tiles: the same bits as
+    the row-major kernel."""
     big, ref = _big_vs_rowmajor(gpu, shapes, epis, seed=11)
     for i, (x, y) in enumerate(zip(big, ref)):
         assert torch.equal(x, y), (shapes[i], epis[i], float((x.float() - y.float()).abs().max()))
+
+
+def test_big_gemm_split_small_batch_tanh_sigmoid(gpu):
+    """The 7B low-rank inputs alone (w1 padded to 128 columns with tanh, g1 to 512 with sigmoid):
+    36 tiles of 192 rows, each split into k-parts (fp32 partials, ordered fixup): within one fp16
+    ulp plus the fp32 re-association bound of the row-major kernel's result (the activations'
+    slopes are at most 1), and run-to-run identical."""
+    shapes, epis = [(2304, 4096, 128), (2304, 4096, 512)], [4, 5]
+    big, ref = _big_vs_rowmajor(gpu, shapes, epis, seed=11)
+    big2, _ = _big_vs_rowmajor(gpu, shapes, epis, seed=11)
+    for i, (M, K, N) in enumerate(shapes):
+        g = torch.Generator(device=gpu).manual_seed(11 + 1000 * i)
+        a = torch.randn(M, K, device=gpu, generator=g).half()
+        w = (torch.randn(N, K, device=gpu, generator=g) * 0.05).half()
+        abs_sum = (a.abs().float() @ w.abs().float().t()).double()
+        r = ref[i].double()
+        ulp = torch.exp2(torch.floor(torch.log2(r.abs().clamp_min(2.0 ** -14))) - 10)
+        err = (big[i].double() - r).abs()
+        bound = ulp + ACC * abs_sum
+        assert bool((err <= bound).all()), (shapes[i], float(err.max()), int((err > bound).sum()))
+        assert torch.equal(big[i], big2[i])
 
 
 @pytest.mark.parametrize("M,K,N", [(300, 256, 200), (2304, 512, 256)])

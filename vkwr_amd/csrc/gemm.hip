@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "vk_capi.h"
 #include "vk_common.cuh"
@@ -416,10 +417,13 @@ int reduce_wgs(const Batch& bt) {
 // Workgroup b runs on XCD b % 8; logical tiles are handed out so that each XCD holds a
 // contiguous range, walked in groups of 4 tile rows, which keeps the A row blocks and B
 // column blocks an XCD needs at once few (its own L2).
+// Tiles are BM x 256 (BM = 256, or 192 where 256-row tiles would leave many CUs idle: M =
+// 2304 gives 9 rows of 256 but 12 of 192); the LDS buffers are sized for BM = 256.
 constexpr int kBigBM = 256, kBigBK = 64, kBigTile = 256 * kBigBK;  // halves per operand tile
-constexpr int kBigTileElems = kBigBM * kBigBM;                       // floats per partial tile
+constexpr int kBigTileElems = kBigBM * kBigBM;                       // floats per partial tile (BM = 256)
 
 struct BigPlan {
+  int bm;        // tile rows: 256 or 192
   int dp_tiles;  // D: tiles computed whole
   int sk_tiles;  // R: tiles split into k-parts
   int parts;     // S: k-parts per split tile
@@ -445,6 +449,7 @@ __device__ __forceinline__ void dma16_m0(const void* base, uint32_t voff, uint32
 
 // Logical tile L of the batch -> its problem index and tile origin (groups of 4 tile rows,
 // column-major inside a group).
+template <int BM>
 __device__ __forceinline__ int big_tile(const Batch& bt, int L, int& m0, int& n0) {
   int pi = 0;
 #pragma unroll
@@ -455,7 +460,7 @@ __device__ __forceinline__ int big_tile(const Batch& bt, int L, int& m0, int& n0
   constexpr int kGroup = 4;
   const int per = kGroup * P.tiles_n, grp = lt / per, in = lt - grp * per;
   const int g0 = grp * kGroup, gs = min(kGroup, P.tiles_m - g0);
-  m0 = (g0 + in % gs) * kBigBM;
+  m0 = (g0 + in % gs) * BM;
   n0 = (in / gs) * kBigBM;
   return pi;
 }
@@ -483,9 +488,9 @@ __device__ __forceinline__ float big_epilogue(const Prob& P, float y, int row, i
   }
 }
 
-// Stores a 256x256 accumulator tile through epilogue kEpi (fp16, clipped to M x N) via LDS
-// (P.vec_out: 16-byte aligned rows, N a multiple of 8).  Wave w walks its 128 x 128 part
-// in 8 strips of 32 x 64 (two horizontally adjacent 32 x 32 accumulator blocks): strip p's
+// Stores a BM x 256 accumulator tile through epilogue kEpi (fp16, clipped to M x N) via LDS
+// (P.vec_out: 16-byte aligned rows, N a multiple of 8).  Wave w walks its (BM / 2) x 128 part
+// in BM / 32 strips of 32 x 64 (two horizontally adjacent 32 x 32 accumulator blocks): strip p's
 // fp32 sums go to one of two LDS buffers of the wave (32 rows of kBigStRow floats each)
 // while strip p - 1 is read back from the other, lane l taking 8 columns (8 (l % 8) .. + 7)
 // of rows l / 8 + 8 h, h = 0..3, so that each 16-byte store instruction writes 8 whole
@@ -495,9 +500,10 @@ __device__ __forceinline__ float big_epilogue(const Prob& P, float y, int row, i
 // (bias / v0) are loaded once; the value residual's v and v_first rows one strip ahead.
 constexpr int kBigStRow = 68;               // 64 columns + 4 floats of padding
 constexpr int kBigStBuf = 32 * kBigStRow;   // floats per strip buffer
-template <int kEpi>
-__device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv16 (&acc)[4][4], int m0, int n0,
-                                              int wm, int wn, int lane) {
+template <int BM, int kEpi>
+__device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv16 (&acc)[BM / 64][4], int m0,
+                                              int n0, int wm, int wn, int lane) {
+  constexpr int kStrips = 2 * (BM / 64);  // 32 x 64 strips of the wave's (BM / 2) x 128 part
   const int lr = lane & 31, lh = lane >> 5, r8 = lane >> 3, c8 = 8 * (lane & 7);
   // The problem's fields, held in SGPRs for the whole store loop (an asm output cannot be
   // re-derived): left alone the compiler re-reads them from the kernel arguments before each
@@ -513,7 +519,7 @@ __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv
   asm("" : "+s"(pm), "+s"(pn), "+s"(pcp), "+s"(pvp), "+s"(pvfp), "+s"(pv0p));
   constexpr bool kVres = kEpi == VKWR_GEMM_EPI_VALUE_RESIDUAL;
   constexpr bool kCol = kVres || kEpi == VKWR_GEMM_EPI_BIAS;  // a per-column operand v0
-  const int rowb = m0 + wm * 128 + r8, colb = n0 + wn * 128 + c8;
+  const int rowb = m0 + wm * (BM / 2) + r8, colb = n0 + wn * 128 + c8;
   hv8 ov0[2];
   if constexpr (kCol) {
 #pragma unroll
@@ -586,46 +592,48 @@ __device__ __forceinline__ void big_store_lds(float* st, const Prob& P, const fv
   if constexpr (kVres) load_ops(0);
   write_strip(0);
 #pragma unroll
-  for (int p = 1; p < 8; ++p) {
+  for (int p = 1; p < kStrips; ++p) {
     if constexpr (kVres) load_ops(p);
     write_strip(p);
     finish_strip(p - 1);
   }
-  finish_strip(7);
+  finish_strip(kStrips - 1);
 }
 
-// One 256x256 tile over k-stages [ks, ke): kPartial stores the fp32 sums to part in
+// One BM x 256 tile over k-stages [ks, ke): kPartial stores the fp32 sums to part in
 // register order -- element ((4 i + j) * 16 + r) * 256 + thread is accumulator r of block
 // (i, j) of that thread, so each store is one coalesced kilobyte -- otherwise the
 // epilogue's fp16 values (clipped to M x N) to P.c.
-template <bool kPartial, int kEpi>
+template <int BM, bool kPartial, int kEpi>
 __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], const Prob& P, int m0, int n0,
                                              int ks, int ke, float* part) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const int M = P.m, N = P.n, K = P.k;
+  constexpr int RB = BM / 64;          // 32-row accumulator blocks per wave
+  constexpr int NA = BM / 32, ND = NA + 8;  // DMA instructions per stage: A, A + B
   // DMA instruction j (0..7) of wave w fills slots j*256 + w*64 + lane of a tile
-  uint32_t ao[8], bo[8];
+  uint32_t ao[NA], bo[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int sl = j * 256 + w * 64 + lane, row = sl >> 3, c = (sl & 7) ^ ((row >> 1) & 7);
-    ao[j] = (uint32_t)((min(m0 + row, M - 1) * (int64_t)K + c * 8) * 2);
+    if (j < NA) ao[j] = (uint32_t)((min(m0 + row, M - 1) * (int64_t)K + c * 8) * 2);
     bo[j] = (uint32_t)((min(n0 + row, N - 1) * (int64_t)K + c * 8) * 2);
   }
   const uint32_t wl = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sm[0][0][0] + w * 64 * 16);
-  int fra[4][4], frb[4][4];
+  int fra[4][RB], frb[4][4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      fra[kk][rb] = big_slot(wm * 128 + 32 * rb + lr, 2 * kk + lh) * 8;
+      if (rb < RB) fra[kk][rb] = big_slot(wm * (BM / 2) + 32 * rb + lr, 2 * kk + lh) * 8;
       frb[kk][rb] = big_slot(wn * 128 + 32 * rb + lr, 2 * kk + lh) * 8;
     }
-  fv16 acc[4][4];
+  fv16 acc[RB][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -634,9 +642,11 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
   // read once: the DMA statements clobber memory, so P.a / P.b would be reloaded after each
   const _Float16* const pa = (const _Float16*)uniform_ptr(P.a);
   const _Float16* const pb = (const _Float16*)uniform_ptr(P.b);
-  // DMA instruction d (0..15) of a stage: A rows of instruction d / 2 for even d, B for odd
+  // DMA instruction d (0..ND-1) of a stage: A and B rows of instruction d / 2 alternating
+  // while both have some (even d: A), then the remaining B ones
   auto dma_one = [&](int d, const void* ab, const void* bb, uint32_t la) __attribute__((always_inline)) {
-    if (d & 1) dma16_m0(bb, bo[d >> 1], la + kBigTile * 2 + (d >> 1) * 256 * 16);
+    if (d >= 2 * NA) dma16_m0(bb, bo[d - NA], la + kBigTile * 2 + (d - NA) * 256 * 16);
+    else if (d & 1) dma16_m0(bb, bo[d >> 1], la + kBigTile * 2 + (d >> 1) * 256 * 16);
     else dma16_m0(ab, ao[d >> 1], la + (d >> 1) * 256 * 16);
   };
   auto stage_src = [&](int st, const void*& ab, const void*& bb) __attribute__((always_inline)) {
@@ -649,55 +659,61 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
     stage_src(st, ab, bb);
     const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2);
 #pragma unroll
-    for (int d = 0; d < 16; ++d)
+    for (int d = 0; d < ND; ++d)
       if (d >= d0 && d < d1) dma_one(d, ab, bb, la);
   };
-  hv8 fa[2][4], fb[2][4];
+  hv8 fa[2][RB], fb[2][4];
   auto fread = [&](int buf, int kk, int set) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fa[set][i] = *reinterpret_cast<const hv8*>(&sm[buf][0][fra[kk][i]]);
+      if (i < RB) fa[set][i] = *reinterpret_cast<const hv8*>(&sm[buf][0][fra[kk][i]]);
       fb[set][i] = *reinterpret_cast<const hv8*>(&sm[buf][1][frb[kk][i]]);
     }
   };
-  // 16 MFMAs with the next group's 8 fragment reads interleaved, one after each of the first 8
+  // 4 RB MFMAs with the next group's RB + 4 fragment reads interleaved, one after each of the
+  // first RB + 4
   auto mfma16 = [&](int set) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < RB + 4; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 3 * RB - 4, 0);
   };
-  // 16 MFMAs with DMA instructions d0 .. d0 + 7 of stage st (buffer buf) after every other
-  // one: a burst of DMA issues would hold up the wave's in-order issue of the MFMAs
+  // 4 RB MFMAs with DMA instructions d0 .. d0 + ND / 2 - 1 of stage st (buffer buf) after
+  // every other one (any left over after the last): a burst of DMA issues would hold up the
+  // wave's in-order issue of the MFMAs
   auto mfma16_dma = [&](int set, int buf, int st, int d0) __attribute__((always_inline)) {
     const void *ab, *bb;
     stage_src(st, ab, bb);
     const uint32_t la = wl + (uint32_t)(buf * 2 * kBigTile * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
-        if ((j & 1) == 0) dma_one(d0 + 2 * i + (j >> 1), ab, bb, la);
+        const int q = 2 * i + (j >> 1);  // the q-th DMA of this half
+        if ((j & 1) == 0 && q < ND / 2) dma_one(d0 + q, ab, bb, la);
         __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+    for (int q = 2 * RB; q < ND / 2; ++q) dma_one(d0 + q, ab, bb, la);
+    __builtin_amdgcn_sched_barrier(0);
   };
-  dma(0, ks, 0, 16);
+  dma(0, ks, 0, ND);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  dma(1, ks + 1, 0, 8);
+  dma(1, ks + 1, 0, ND / 2);
   fread(0, 0, 0);
   int cb = 0;
   for (int s = ks; s < ke; ++s) {
     const int nb = cb ^ 1;
     fread(cb, 1, 1);
-    mfma16_dma(0, nb, s + 1, 8);  // the second half of stage s + 1
+    mfma16_dma(0, nb, s + 1, ND / 2);  // the second half of stage s + 1
     __builtin_amdgcn_sched_barrier(0);
     fread(cb, 2, 0);
     mfma16(1);
@@ -719,71 +735,72 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
 
   if constexpr (kPartial) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) part[((4 * i + j) * 16 + r) * 256 + tid] = acc[i][j][r];
   } else if constexpr (kEpi >= 0) {
-    big_store_lds<kEpi>(st, P, acc, m0, n0, wm, wn, lane);
+    big_store_lds<BM, kEpi>(st, P, acc, m0, n0, wm, wn, lane);
   } else {
     // a batch of mixed epilogues: one branch per tile to a specialized store loop
     // (a per-element switch would not keep the accumulator tile in registers)
     switch (P.epi) {
-      case VKWR_GEMM_EPI_RELU_SQUARE: big_store_lds<VKWR_GEMM_EPI_RELU_SQUARE>(st, P, acc, m0, n0, wm, wn, lane); break;
+      case VKWR_GEMM_EPI_RELU_SQUARE: big_store_lds<BM, VKWR_GEMM_EPI_RELU_SQUARE>(st, P, acc, m0, n0, wm, wn, lane); break;
       case VKWR_GEMM_EPI_VALUE_RESIDUAL:
-        big_store_lds<VKWR_GEMM_EPI_VALUE_RESIDUAL>(st, P, acc, m0, n0, wm, wn, lane);
+        big_store_lds<BM, VKWR_GEMM_EPI_VALUE_RESIDUAL>(st, P, acc, m0, n0, wm, wn, lane);
         break;
-      case VKWR_GEMM_EPI_BIAS: big_store_lds<VKWR_GEMM_EPI_BIAS>(st, P, acc, m0, n0, wm, wn, lane); break;
-      case VKWR_GEMM_EPI_TANH: big_store_lds<VKWR_GEMM_EPI_TANH>(st, P, acc, m0, n0, wm, wn, lane); break;
-      case VKWR_GEMM_EPI_SIGMOID: big_store_lds<VKWR_GEMM_EPI_SIGMOID>(st, P, acc, m0, n0, wm, wn, lane); break;
-      default: big_store_lds<VKWR_GEMM_EPI_NONE>(st, P, acc, m0, n0, wm, wn, lane); break;
+      case VKWR_GEMM_EPI_BIAS: big_store_lds<BM, VKWR_GEMM_EPI_BIAS>(st, P, acc, m0, n0, wm, wn, lane); break;
+      case VKWR_GEMM_EPI_TANH: big_store_lds<BM, VKWR_GEMM_EPI_TANH>(st, P, acc, m0, n0, wm, wn, lane); break;
+      case VKWR_GEMM_EPI_SIGMOID: big_store_lds<BM, VKWR_GEMM_EPI_SIGMOID>(st, P, acc, m0, n0, wm, wn, lane); break;
+      default: big_store_lds<BM, VKWR_GEMM_EPI_NONE>(st, P, acc, m0, n0, wm, wn, lane); break;
     }
   }
 }
 
 // Whole tiles: workgroup b takes logical tile (XCD-contiguous order) of the first `tiles`.
 // kEpi >= 0: every problem of the batch has that epilogue; -1: each its own.
-template <int kEpi>
+template <int BM, int kEpi>
 __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int tiles) {
   __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];  // [buffer][A/B]: 128 KiB
   const int xb = blockIdx.x & 7, idx = blockIdx.x >> 3, q8 = tiles >> 3, r8 = tiles & 7;
   const int L = (xb < r8 ? xb * (q8 + 1) : r8 * (q8 + 1) + (xb - r8) * q8) + idx;
   int m0, n0;
-  const Prob& P = bt.p[big_tile(bt, L, m0, n0)];
-  big_tile_run<false, kEpi>(sm, P, m0, n0, 0, P.k / kBigBK, nullptr);
+  const Prob& P = bt.p[big_tile<BM>(bt, L, m0, n0)];
+  big_tile_run<BM, false, kEpi>(sm, P, m0, n0, 0, P.k / kBigBK, nullptr);
 }
 
 // Split tiles: workgroup b computes part b % S (k-stages [p nst / S, (p+1) nst / S)) of
 // split tile D + b / S into partial slot b.
+template <int BM>
 __global__ __launch_bounds__(256, 1) void gemm_big_sk_kernel(Batch bt, BigPlan pl) {
   __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];
   const int t = blockIdx.x / pl.parts, p = blockIdx.x - t * pl.parts;
   int m0, n0;
-  const Prob& P = bt.p[big_tile(bt, pl.dp_tiles + t, m0, n0)];
-  big_tile_run<true, -1>(sm, P, m0, n0, p * pl.nst / pl.parts, (p + 1) * pl.nst / pl.parts,
-                         pl.ws + (size_t)blockIdx.x * kBigTileElems);
+  const Prob& P = bt.p[big_tile<BM>(bt, pl.dp_tiles + t, m0, n0)];
+  big_tile_run<BM, true, -1>(sm, P, m0, n0, p * pl.nst / pl.parts, (p + 1) * pl.nst / pl.parts,
+                             pl.ws + (size_t)blockIdx.x * (BM * kBigBM));
 }
 
 // Fixup: blockIdx.y = split tile t, blockIdx.x = accumulator block (i, j) of the partial
 // layout; adds the tile's S partials in increasing k order, applies the epilogue, stores.
-template <int kEpi>
+template <int BM, int kEpi>
 __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan pl) {
   const int t = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
   int m0, n0;
-  const Prob& P = bt.p[big_tile(bt, pl.dp_tiles + t, m0, n0)];
+  const Prob& P = bt.p[big_tile<BM>(bt, pl.dp_tiles + t, m0, n0)];
   const int lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lh = lane >> 5;
   const int i = blk >> 2, j = blk & 3;
   const int col = n0 + wn * 128 + j * 32 + lr;
   if (col >= P.n) return;
   // The 16 values of a part are loaded together (the workspace holds whole
   // tiles, so rows past M are in bounds), then the parts are added in order.
-  const float* base = pl.ws + (size_t)t * pl.parts * kBigTileElems + (size_t)blk * 16 * 256 + tid;
+  const float* base = pl.ws + (size_t)t * pl.parts * (BM * kBigBM) + (size_t)blk * 16 * 256 + tid;
   float acc[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = base[r * 256];
   for (int q = 1; q < pl.parts; ++q) {
-    const float* bq = base + (size_t)q * kBigTileElems;
+    const float* bq = base + (size_t)q * (BM * kBigBM);
     float nx[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) nx[r] = bq[r * 256];
@@ -792,7 +809,7 @@ __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan p
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+    const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
     if (row >= P.m) continue;
     float y = big_epilogue<kEpi>(P, acc[r], row, col);
     asm volatile("" : "+v"(y));
@@ -1390,7 +1407,14 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
 }
 
 // Tiles (256x256) of a large-M batch and its stream-K split; returns the workspace bytes.
-int64_t plan_big(Batch& bt, BigPlan& pl) {
+// The plan for tile rows BM: tile fields of the batch's problems, and the split of the last
+// round; returns its estimated time (us).  Time model: a tile's k-stage ~1.7 us when every CU
+// is busy (0.86 of that for 192 rows, as measured: the operand bytes per MAC are higher), plus
+// ~2 stages of prologue and epilogue per workgroup; a split tile costs its S fp32 partials
+// written and read back at ~5 TB/s.  Batches of unequal K (the low-rank outputs: K = 512 and
+// 128, their time in the epilogue stores) are scored by how fully the last round of tiles
+// fills the CUs instead (returned as a negative fill fraction).
+double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
   int T = 0, k_all = -1;
   bool uniform_k = true;
   for (int i = 0; i < bt.n; ++i) {
@@ -1400,7 +1424,7 @@ int64_t plan_big(Batch& bt, BigPlan& pl) {
     if (P.m == 0 || P.n == 0) {
       P.tiles_m = P.tiles_n = 0;
     } else {
-      P.tiles_m = (P.m + kBigBM - 1) / kBigBM;
+      P.tiles_m = (P.m + BM - 1) / BM;
       P.tiles_n = (P.n + kBigBM - 1) / kBigBM;
       uniform_k = uniform_k && (k_all < 0 || k_all == P.k);
       k_all = P.k;
@@ -1408,29 +1432,43 @@ int64_t plan_big(Batch& bt, BigPlan& pl) {
     P.tile_begin = T;
     T += P.tiles_m * P.tiles_n;
   }
-  pl = BigPlan{T, 0, 1, 0, nullptr};
+  pl = BigPlan{BM, T, 0, 1, 0, nullptr};
   const int G = device_cus();
-  if (T < 32 || !uniform_k || T % G == 0) return 0;
-  // Time model of the last round, in microseconds: a tile's k-stage ~1.7 us when every CU
-  // is busy; a split tile costs its S fp32 partials written and read back (2 x 256 KiB
-  // each) at ~5 TB/s.  Take the S (1..8, >= 8 stages per part) with the least time.
-  const int R = T % G, nst = k_all / kBigBK;
-  double best = (double)nst * 1.7;
+  const double stage = 1.7 * (BM == 192 ? 0.86 : 1.0), over = 2.0 * stage;
+  if (!uniform_k) return -(double)T / ((double)((T + G - 1) / G) * G);
+  const int nst = k_all / kBigBK;
+  const double rounds_whole = (double)((T + G - 1) / G);
+  double best = rounds_whole * (nst * stage + over);
+  if (T < 32 || T % G == 0) return best;
+  const int R = T % G, D = T - R;
+  const double full = (double)(D / G) * (nst * stage + over);
   int best_s = 1;
   for (int S = 2; S <= 8 && nst / S >= 8; ++S) {
     const double rounds = (double)((R * S + G - 1) / G);
-    const double t = rounds * nst * 1.7 / S + (double)R * S * 2 * kBigTileElems * 4 / 5e6;
+    const double t = full + rounds * ((double)nst / S * stage + over) + (double)R * S * 2 * BM * kBigBM * 4 / 5e6;
     if (t < best) {
       best = t;
       best_s = S;
     }
   }
-  if (best_s == 1) return 0;
-  pl.dp_tiles = T - R;
-  pl.sk_tiles = R;
-  pl.parts = best_s;
-  pl.nst = nst;
-  return (int64_t)R * best_s * kBigTileElems * 4;
+  if (best_s > 1) {
+    pl.dp_tiles = D;
+    pl.sk_tiles = R;
+    pl.parts = best_s;
+    pl.nst = nst;
+  }
+  return best;
+}
+
+// Picks the tile rows (256, or 192 when its plan is estimated to be at least 5 % faster -- M =
+// 2304 fills 256 CUs with 192 row tiles far better than with 144 -- or, for unequal K, fills
+// the last round better) and plans the batch; returns the workspace bytes the plan needs.
+int64_t plan_big(Batch& bt, BigPlan& pl) {
+  BigPlan p192;
+  const double t192 = plan_big_bm(bt, p192, 192);
+  const double t256 = plan_big_bm(bt, pl, 256);
+  if (t256 < 0 ? t192 < t256 - 0.05 : t192 < 0.95 * t256) plan_big_bm(bt, pl, 192);
+  return pl.sk_tiles > 0 ? (int64_t)pl.sk_tiles * pl.parts * pl.bm * kBigBM * 4 : 0;
 }
 
 int total_wgs(const Batch& bt) {
@@ -1573,23 +1611,31 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
       if (bt.p[i].m == 0 || bt.p[i].n == 0) continue;
       epi = epi == -2 ? bt.p[i].epi : (epi == bt.p[i].epi ? epi : -1);
     }
-    auto go = [&](auto whole, auto fix) {
+    auto go = [&](auto bm_tag, auto whole, auto fix) {
+      constexpr int BM = decltype(bm_tag)::value;
       if (pl.dp_tiles > 0) hipLaunchKernelGGL(whole, dim3(pl.dp_tiles), dim3(256), 0, s, bt, pl.dp_tiles);
       if (pl.sk_tiles > 0) {
-        hipLaunchKernelGGL(gemm_big_sk_kernel, dim3(pl.sk_tiles * pl.parts), dim3(256), 0, s, bt, pl);
-        hipLaunchKernelGGL(fix, dim3(16, pl.sk_tiles), dim3(256), 0, s, bt, pl);
+        hipLaunchKernelGGL(gemm_big_sk_kernel<BM>, dim3(pl.sk_tiles * pl.parts), dim3(256), 0, s, bt, pl);
+        hipLaunchKernelGGL(fix, dim3(4 * (BM / 64), pl.sk_tiles), dim3(256), 0, s, bt, pl);
       }
     };
-    if (epi == VKWR_GEMM_EPI_NONE)
-      go(gemm_big_kernel<VKWR_GEMM_EPI_NONE>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_NONE>);
-    else if (epi == VKWR_GEMM_EPI_RELU_SQUARE)
-      go(gemm_big_kernel<VKWR_GEMM_EPI_RELU_SQUARE>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_RELU_SQUARE>);
-    else if (epi == VKWR_GEMM_EPI_BIAS)
-      go(gemm_big_kernel<VKWR_GEMM_EPI_BIAS>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_BIAS>);
-    else if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL)
-      go(gemm_big_kernel<VKWR_GEMM_EPI_VALUE_RESIDUAL>, gemm_big_fixup_kernel<VKWR_GEMM_EPI_VALUE_RESIDUAL>);
-    else
-      go(gemm_big_kernel<-1>, gemm_big_fixup_kernel<-1>);
+    auto go_bm = [&](auto bm_tag) {
+      constexpr int BM = decltype(bm_tag)::value;
+      if (epi == VKWR_GEMM_EPI_NONE)
+        go(bm_tag, gemm_big_kernel<BM, VKWR_GEMM_EPI_NONE>, gemm_big_fixup_kernel<BM, VKWR_GEMM_EPI_NONE>);
+      else if (epi == VKWR_GEMM_EPI_RELU_SQUARE)
+        go(bm_tag, gemm_big_kernel<BM, VKWR_GEMM_EPI_RELU_SQUARE>,
+           gemm_big_fixup_kernel<BM, VKWR_GEMM_EPI_RELU_SQUARE>);
+      else if (epi == VKWR_GEMM_EPI_BIAS)
+        go(bm_tag, gemm_big_kernel<BM, VKWR_GEMM_EPI_BIAS>, gemm_big_fixup_kernel<BM, VKWR_GEMM_EPI_BIAS>);
+      else if (epi == VKWR_GEMM_EPI_VALUE_RESIDUAL)
+        go(bm_tag, gemm_big_kernel<BM, VKWR_GEMM_EPI_VALUE_RESIDUAL>,
+           gemm_big_fixup_kernel<BM, VKWR_GEMM_EPI_VALUE_RESIDUAL>);
+      else
+        go(bm_tag, gemm_big_kernel<BM, -1>, gemm_big_fixup_kernel<BM, -1>);
+    };
+    if (pl.bm == 192) go_bm(std::integral_constant<int, 192>{});
+    else go_bm(std::integral_constant<int, 256>{});
     return check_launch(fn);
   }
   if (cfg.bm == 32) hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 4>), dim3(wgs), dim3(256), 0, s, bt);
