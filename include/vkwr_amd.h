@@ -389,6 +389,33 @@ VKWR_EXPORT int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, cons
                                                        uint16_t* x_out, uint16_t* const* out,
                                                        const int32_t* shift_slots, int64_t n_shift,
                                                        void* stream);
+
+/* A group of rows of a mixed prefill + decode batch: B sequences of T consecutive rows each,
+ * starting at row row0, sequence b's shift row at shift_state[slots[b]]. */
+typedef struct vkwr_ln_shift_group {
+  int64_t row0;
+  int32_t B, T;
+  const int32_t* slots;
+} vkwr_ln_shift_group;
+
+/* Residual add + LayerNorm + token-shift lerp over the row groups of a mixed batch, in one
+ * launch: x_out = fp16(x + residual) (residual may be NULL), y = LN(x + residual), and for
+ * row t of a sequence out[i] = lerp(y, prev, mix[i]) with prev the y of row t - 1, or for
+ * t = 0 the sequence's shift row, which then takes the y of the sequence's last row.  The
+ * same bits as vkwr_layer_norm_f16 followed, per group, by vkwr_token_shift_mix_slots_f16
+ * (the reference's add_layer_norm_f16 and tmix_mix6 / cmix_mix, csrc/v1/norm/norm_ops.cu
+ * and csrc/v1/mix/mix_ops.cu:42-160, run back to back).  The groups cover rows 0 .. rows-1 in
+ * order (1..8 of them); C % 8 == 0, C <= 4096; n_mix 1 or 6; every tensor 16-byte aligned;
+ * slots distinct across the call.  A slot outside 0 .. n_shift-1 makes its rows' x_out and
+ * outputs NaN and leaves the pool untouched.  No counterpart in the reference: it is the
+ * mixed step's fusion of those two ops. */
+VKWR_EXPORT int vkwr_add_layer_norm_shift_rows_f16(int64_t rows, int C, const uint16_t* x,
+                                                   const uint16_t* residual, const uint16_t* weight,
+                                                   const uint16_t* bias, float eps, uint16_t* x_out,
+                                                   int n_mix, const uint16_t* const* mix,
+                                                   uint16_t* const* out, uint16_t* shift_state,
+                                                   int64_t n_shift, int n_groups,
+                                                   const vkwr_ln_shift_group* groups, void* stream);
 VKWR_EXPORT int vkwr_add_last_layer_norm_frag_f16(int B, int T, int C, const uint16_t* x,
                                                   const uint16_t* residual, const uint16_t* weight,
                                                   const uint16_t* bias, float eps, uint16_t* y,

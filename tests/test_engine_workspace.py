@@ -38,8 +38,8 @@ def _host_model(cfg, n_layer=2):
 def test_mixed_engine_workspace_covers_every_row_count_7b():
     """Config 4 (7B shape, 256 decode rows + 4 x 512 chunks = 2304 rows): every GEMM launch the
     step can issue, at every row count 1..2304 (and the head at 1..260 sequences), fits the
-    engine's workspace.  Sampling only powers of two and the maximum falls short (the FFN value
-    GEMM at 1281..1536 rows splits its last round into more k-parts)."""
+    engine's workspace (the split of a GEMM's last round into k-parts, and so its workspace,
+    is not monotone in the row count, so every count is checked)."""
     cfg = RWKV7Config.preset("7b")
     eng = MixedEngine(_host_model(cfg), 2304, max_seqs=260)
     have = eng.ws.numel()
@@ -52,9 +52,6 @@ def test_mixed_engine_workspace_covers_every_row_count_7b():
     for S in range(1, 261):
         assert capi.gemm_workspace_bytes(eng._head_problem(S)) <= have
     assert worst == have or capi.gemm_workspace_bytes_upto(eng._head_problem(260)) == have
-    sampled = max(capi.gemm_workspace_bytes(ps) for m in [1 << i for i in range(12)] + [2304]
-                  for ps in eng._gemm_batches(m, 2))
-    assert sampled < have
 
 
 def test_decode_engine_rowmajor_workspace_covers_every_batch_1p5b():

@@ -445,3 +445,83 @@ def test_ln_mix_slots_and_rows_bounds(gpu, frag):
     want = before.clone()
     want.index_copy_(0, sel, shift)
     assert torch.equal(pool, want)
+
+
+def _ln_shift_rows_case(gpu, C, n_mix, with_res, shapes, P=16, bad_group=None):
+    """Fused LayerNorm + token shift over row groups against vkwr_layer_norm_f16 followed by
+    vkwr_token_shift_mix_slots_f16 per group: bit-equal outputs, x_out and shift pool."""
+    from vkwr_amd import capi
+    f16 = dict(dtype=torch.float16, device=gpu)
+    rows = sum(B * T for B, T in shapes)
+    x, res = dev(h(rows, C), gpu), dev(h(rows, C), gpu) if with_res else None
+    wt, bs = dev(h(C, scale=0.5) + 1, gpu), dev(h(C, scale=0.1), gpu)
+    mixes = [dev(rng.random(C).astype(np.float16), gpu) for _ in range(n_mix)]
+    pool0 = dev(h(P, C), gpu)
+    perm = rng.permutation(P)
+    groups, r0, k = [], 0, 0
+    for gi, (B, T) in enumerate(shapes):
+        sl = [int(s) for s in perm[k:k + B]]
+        if gi == bad_group:
+            sl[0] = P  # one slot past the pool: that sequence's rows are NaN
+        groups.append((r0, B, T, torch.tensor(sl, dtype=torch.int32, device=gpu)))
+        r0, k = r0 + B * T, k + B
+    pool = pool0.clone()
+    x_out, outs = torch.empty(rows, C, **f16), [torch.empty(rows, C, **f16) for _ in range(n_mix)]
+    capi.layer_norm_shift_rows(x, wt, bs, x_out, mixes, outs, pool, groups, residual=res)
+
+    y, xo_ref = torch.empty(rows, C, **f16), torch.empty(rows, C, **f16)
+    capi.layer_norm(x, wt, bs, y, residual=res, x_out=xo_ref)
+    pool_ref = pool0.clone()
+    refs = [torch.full((rows, C), float("nan"), **f16) for _ in range(n_mix)]
+    for gi, (g0, B, T, sl) in enumerate(groups):
+        if gi == bad_group:
+            sl = sl[1:]
+            g0, B = g0 + T, B - 1
+            if B == 0:
+                continue
+        n = B * T
+        capi.token_shift(B, T, C, y[g0:g0 + n], pool_ref, mixes, [o[g0:g0 + n] for o in refs], shift_slots=sl)
+    torch.cuda.synchronize()
+    bad_rows = torch.zeros(rows, dtype=torch.bool, device=gpu)
+    if bad_group is not None:
+        g0, _, T, _ = groups[bad_group]
+        bad_rows[g0:g0 + T] = True
+    ok = ~bad_rows
+    assert torch.equal(x_out[ok], xo_ref[ok])
+    assert torch.isnan(x_out[bad_rows]).all()
+    for o, r in zip(outs, refs):
+        assert torch.equal(o[ok], r[ok])
+        assert torch.isnan(o[bad_rows]).all()
+    assert torch.equal(pool, pool_ref), "shift pool := LN of each sequence's last row"
+
+
+@pytest.mark.parametrize("C", [2048, 4096, 64])
+@pytest.mark.parametrize("n_mix", [6, 1])
+@pytest.mark.parametrize("with_res", [True, False])
+def test_layer_norm_shift_rows_matches_ln_then_shift(gpu, C, n_mix, with_res):
+    """Decode rows (T = 1) and prefill sequences (T > 1, including T = 2) in one launch."""
+    _ln_shift_rows_case(gpu, C, n_mix, with_res, [(5, 1), (2, 7), (1, 2), (1, 1), (3, 4)])
+
+
+def test_layer_norm_shift_rows_bad_slot(gpu):
+    """A slot outside the pool: that sequence's rows are NaN, its shift row untouched, the rest exact."""
+    _ln_shift_rows_case(gpu, 2048, 6, True, [(4, 1), (2, 5), (1, 3)], bad_group=1)
+    _ln_shift_rows_case(gpu, 2048, 1, True, [(4, 1), (1, 3)], bad_group=0)
+
+
+def test_layer_norm_shift_rows_errors(gpu):
+    from vkwr_amd import capi
+    C = 256
+    x = torch.zeros(6, C, dtype=torch.float16, device=gpu)
+    wt, bs = torch.ones(C, dtype=torch.float16, device=gpu), torch.zeros(C, dtype=torch.float16, device=gpu)
+    pool = torch.zeros(8, C, dtype=torch.float16, device=gpu)
+    sl = torch.arange(3, dtype=torch.int32, device=gpu)
+    xo, out = torch.empty_like(x), [torch.empty_like(x)]
+    with pytest.raises(RuntimeError, match="cover"):  # groups cover 3 of 6 rows
+        capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(0, 3, 1, sl)])
+    with pytest.raises(RuntimeError, match="starts at row"):
+        capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(0, 3, 1, sl), (4, 3, 1, sl)])
+    with pytest.raises(RuntimeError, match="groups"):
+        capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(r, 1, 1, sl) for r in range(6)] * 2)
+    with pytest.raises(RuntimeError, match="n_mix"):
+        capi.layer_norm_shift_rows(x, wt, bs, xo, [wt, wt], out * 2, pool, [(0, 3, 2, sl)])

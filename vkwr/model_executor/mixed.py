@@ -9,16 +9,17 @@ and matrix-core bound -- while the per-sequence recurrent parts run per group:
           group with T = 1, each prefill chunk length another.
 
 Per layer (x: previous block output, res: residual stream, rows = all rows):
-  res, xx = add + LN1 over rows
-  xr..xg  = token-shift lerps per group (slot-indexed att shift pool)
-  r, k, v, w1, a1, g1, v1 = projections over rows            (one GEMM launch)
+  res, xr..xg = add + LN1 + token-shift lerps per group (slot-indexed att shift
+          pool; one launch over all groups, the LN output never leaves the CUs)
+  r, k, v, tanh(w1), a1, sigmoid(g1), v1 = projections over rows (one GEMM launch,
+          the activations in its epilogue)
   w, a12, g, v = low-rank outputs (tanh / - / sigmoid / value residual) (one launch;
           the adapter ranks padded to multiples of 64 with zeros, so the launch runs on
           the large-M kernel)
   k', -kk, kk*a = kk/a gate over rows
   y   = WKV-7 per group on the slot pool (T = 1 decode kernel, T > 1 prefill kernel)
   o   = (GroupNorm(y) + bonus) * g  W_o^T over rows
-  res, xx = add + LN2; xk = token shift per group (ffn shift pool)
+  res, xk = add + LN2 + token shift per group (ffn shift pool; one launch)
   x   = relu(xk K^T)^2 V^T over rows
 logits of the last row of every group's sequences = LN_out(x + res) Head^T.
 
@@ -69,7 +70,6 @@ class MixedEngine:
         self.tok = torch.empty(R, dtype=torch.int32, device=dev)
         self.x0 = buf(R, C)
         self.res = [buf(R, C), buf(R, C)]
-        self.xx = buf(R, C)
         self.mix = [buf(R, C) for _ in range(6)]
         self.r, self.k, self.v, self.v_first, self.v_new = (buf(R, C) for _ in range(5))
         # Low-rank adapters with the rank padded to a multiple of 64 (96 -> 128, 480 -> 512 at
@@ -103,17 +103,17 @@ class MixedEngine:
         s, gp = self, capi.gemm_problem
         ps = [gp(s.mix[0][:R], L["Wr"], s.r[:R]), gp(s.mix[2][:R], L["Wk"], s.k[:R]),
               gp(s.mix[3][:R], L["Wv"], (s.v_first if first else s.v)[:R]),
-              gp(s.mix[1][:R], W["w1"], s.w1[:R]), gp(s.mix[4][:R], W["a1"], s.a1[:R]),
-              gp(s.mix[5][:R], W["g1"], s.g1[:R])]
+              gp(s.mix[1][:R], W["w1"], s.w1[:R], epilogue=capi.EPI_TANH), gp(s.mix[4][:R], W["a1"], s.a1[:R]),
+              gp(s.mix[5][:R], W["g1"], s.g1[:R], epilogue=capi.EPI_SIGMOID)]
         if not first:
             ps.append(gp(s.mix[3][:R], W["v1"], s.v1[:R]))
         return ps
 
     def _rank_out(self, L, W, R, first):
-        """The low-rank output GEMMs; tanh(w1) and sigmoid(g1) are applied by
-        _rank_act first (once per element: as an A-operand activation every
-        column tile of the GEMM recomputed them, 56 of the 103 us of g2 at the 7B
-        shape).  Same fp16 values as the A-operand form."""
+        """The low-rank output GEMMs.  Their inputs tanh(w1) and sigmoid(g1) come activated
+        from the projection batch's epilogue (once per element, on the fp32 sum, as in the
+        decode engine's frag GEMM; as an A-operand activation every column tile of this GEMM
+        recomputed them, 56 of the 103 us of g2 at the 7B shape)."""
         s, gp = self, capi.gemm_problem
         # g2 (the longest K) first: its tiles start in the first round and the short ones
         # fill in behind them
@@ -124,10 +124,6 @@ class MixedEngine:
             ps.append(gp(s.v1[:R], W["v2"], s.v_new[:R], epilogue=capi.EPI_VALUE_RESIDUAL, v=s.v[:R],
                          v_first=s.v_first[:R], v0=L["v0"]))
         return ps
-
-    def _rank_act(self, R):
-        capi.activation(capi.ACT_EW_TANH, self.w1[:R], self.w1[:R])
-        capi.activation(capi.ACT_EW_SIGMOID, self.g1[:R], self.g1[:R])
 
     def _gemm_batches(self, R, nl):
         m, s, gp = self.model, self, capi.gemm_problem
@@ -170,19 +166,15 @@ class MixedEngine:
         assert 0 < R <= self.max_rows and S <= self.max_seqs
         ws = self.ws
         torch.index_select(m.emb, 0, s.tok[:R], out=s.x0[:R])
+        shift_groups = [(r0, B, T, slots) for B, T, r0, slots, _ in groups]
         x, res_in = s.x0[:R], None
         for l, L in enumerate(m.layers):
             first = l == 0
             res = s.res[l % 2][:R]
-            # ---- time mix
-            capi.layer_norm(x, L["ln1_w"], L["ln1_b"], s.xx[:R], residual=res_in, x_out=res)  # res = x + res_in
-            mixes = [L[k] for k in TMIX_MIX]
-            for B, T, r0, slots, _ in groups:
-                n = B * T
-                capi.token_shift(B, T, C, s.xx[r0:r0 + n], state.att_shift[l], mixes,
-                                 [t[r0:r0 + n] for t in s.mix], shift_slots=slots)
+            # ---- time mix: res = x + res_in, LN1 and the six lerps against the shift pool
+            capi.layer_norm_shift_rows(x, L["ln1_w"], L["ln1_b"], res, [L[k] for k in TMIX_MIX],
+                                       [t[:R] for t in s.mix], state.att_shift[l], shift_groups, residual=res_in)
             capi.gemm(self._proj(L, s.lw[l], R, first), ws)
-            self._rank_act(R)
             capi.gemm(self._rank_out(L, s.lw[l], R, first), ws)
             v = (s.v_first if first else s.v_new)[:R]
             capi.kk_a_gate(R, 1, C, H, s.k[:R], L["k_k"], L["a0"], s.a12[:R], L["k_a"], s.new_k[:R],
@@ -197,11 +189,8 @@ class MixedEngine:
             capi.gemm([capi.gemm_problem(s.o_in[:R], L["Wo"], s.o[:R])], ws)
             # ---- channel mix
             res2 = s.res[(l + 1) % 2][:R]
-            capi.layer_norm(s.o[:R], L["ln2_w"], L["ln2_b"], s.xx[:R], residual=res, x_out=res2)
-            for B, T, r0, slots, _ in groups:
-                n = B * T
-                capi.token_shift(B, T, C, s.xx[r0:r0 + n], state.ffn_shift[l], [L["x_k_ffn"]],
-                                 [s.xk[r0:r0 + n]], shift_slots=slots)
+            capi.layer_norm_shift_rows(s.o[:R], L["ln2_w"], L["ln2_b"], res2, [L["x_k_ffn"]], [s.xk[:R]],
+                                       state.ffn_shift[l], shift_groups, residual=res)
             capi.gemm([capi.gemm_problem(s.xk[:R], L["key"], s.act[:R], epilogue=capi.EPI_RELU_SQUARE)], ws)
             capi.gemm([capi.gemm_problem(s.act[:R], L["value"], s.ffn[:R])], ws)
             x, res_in = s.ffn[:R], res2

@@ -54,6 +54,10 @@ class FragProblem(ctypes.Structure):
                 ("epilogue", _i), ("c_frag", _i), ("v", _p), ("v_first", _p), ("v0", _p)]
 
 
+class LnShiftGroup(ctypes.Structure):
+    _fields_ = [("row0", _i64), ("B", ctypes.c_int32), ("T", ctypes.c_int32), ("slots", _p)]
+
+
 def _sig(name, args, res=_i):
     fn = getattr(_LIB, name)
     fn.argtypes = args
@@ -92,6 +96,9 @@ _gn_frag = _sig("vkwr_tmix_groupnorm_bonus_gate_frag_f16", [_i, _i, _i, _i, _p, 
 _wkv_fused = _sig("vkwr_wkv7_decode_fused_f16", [_i, _i, _i, _p, _i, _i, _p] + [_p] * 13 + [_i, _p])
 _wkv_layout = _sig("vkwr_wkv7_state_layout_f32", [_i64, _p, _p, _i, _p])
 WKV_STATE_STD, WKV_STATE_ILV = 0, 1
+_ln_shift_rows = _sig("vkwr_add_layer_norm_shift_rows_f16",
+                      [_i64, _i, _p, _p, _p, _p, _f, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _p, _i64, _i,
+                       ctypes.POINTER(LnShiftGroup), _p])
 _shift = _sig("vkwr_token_shift_mix_f16", [_i, _i, _i, _p, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
 _shift_slots = _sig("vkwr_token_shift_mix_slots_f16",
                     [_i, _i, _i, _p, _p, _i64, _p, _i, ctypes.POINTER(_p), ctypes.POINTER(_p), _i, _p])
@@ -300,6 +307,20 @@ def wkv_state_layout(src, dst, to_layout):
     """Copies fp32 state blocks (src, dst: [..., 64, 64] views of the same shape) into layout to_layout."""
     assert src.shape == dst.shape and src.dtype == dst.dtype == torch.float32 and src.numel() % 4096 == 0
     _check(_wkv_layout(src.numel() // 4096, _ptr(src), _ptr(dst), to_layout, _stream()), "vkwr_wkv7_state_layout_f32")
+
+
+def layer_norm_shift_rows(x, weight, bias, x_out, mixes, outs, shift_state, groups, residual=None, eps=1e-5):
+    """x_out = x + residual, y = LN(x_out), and per group (row0, B, T, slots [B] int32) the
+    token-shift lerps of y into outs against the shift pool shift_state [P, C]: one launch
+    of vkwr_add_layer_norm_shift_rows_f16.  x, residual, x_out, outs [rows, C]."""
+    C = x.shape[-1]
+    rows = x.numel() // C
+    mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
+    op = (_p * len(outs))(*[o.data_ptr() for o in outs])
+    gs = (LnShiftGroup * len(groups))(*[LnShiftGroup(r0, B, T, sl.data_ptr()) for r0, B, T, sl in groups])
+    _check(_ln_shift_rows(rows, C, _ptr(x), _ptr(residual), _ptr(weight), _ptr(bias), eps, _ptr(x_out), len(mixes),
+                          mp, op, _ptr(shift_state), shift_state.numel() // C, len(groups), gs, _stream()),
+           "vkwr_add_layer_norm_shift_rows_f16")
 
 
 def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False, shift_slots=None):

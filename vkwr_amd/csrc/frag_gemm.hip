@@ -142,7 +142,7 @@ __device__ __forceinline__ void store_cols(const float (&s)[W], int row, int col
     for (int e = 0; e < W; ++e) {
       const float x = (float)vv.v[e];
       const float gate = sigmoidf((float)v0.v[e] + s[e]);
-      o.v[e] = (_Float16)__builtin_fmaf((float)vf.v[e] - x, gate, x);
+      o.v[e] = f16_of(__builtin_fmaf((float)vf.v[e] - x, gate, x));
     }
   } else if (epi == VKWR_GEMM_EPI_BIAS) {
     const hw v0 = *reinterpret_cast<const hw*>(pv0 + col);

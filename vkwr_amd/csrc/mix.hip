@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void token_shift_kernel(ShiftArgs p) {
           o[e] = (_Float16)__builtin_fmaf16(dx, mu[i][e], cur[e]);
         } else {
           const float cf = (float)cur[e];
-          o[e] = (_Float16)__builtin_fmaf((float)prev[e] - cf, (float)mu[i][e], cf);
+          o[e] = f16_of(__builtin_fmaf((float)prev[e] - cf, (float)mu[i][e], cf));
         }
       }
       _Float16* dst = p.out[i] + ((int64_t)b * p.T + t) * p.C + c0;
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void vres_gate_kernel(int64_t n, int C, const 
   const int c = (int)(i % C);
   const float vv = (float)v[i];
   const float gate = sigmoidf((float)v0[c] + (float)v12[i]);
-  out[i] = (_Float16)__builtin_fmaf((float)vf[i] - vv, gate, vv);
+  out[i] = f16_of(__builtin_fmaf((float)vf[i] - vv, gate, vv));
 }
 
 template <int ACT>

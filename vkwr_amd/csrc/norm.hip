@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
       const float t = (v[n][e] - mean) * rstd;
       const float wt = kVec ? (float)wpre[n % kPre].v[e] : ld_in<kBf16>(p.weight, c0 + e);
       const float bs = kVec ? (float)bpre[n % kPre].v[e] : ld_in<kBf16>(p.bias, c0 + e);
-      yh[e] = (_Float16)__builtin_fmaf(t, wt, bs);
+      yh[e] = f16_of(__builtin_fmaf(t, wt, bs));
       xo[e] = (_Float16)v[n][e];
     }
     const int64_t odst = p.out_frag ? frag_index(row, c0, C) : dst + c0;  // y / out[] element offset
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(LnArgs p) {
         for (int e = 0; e < VW; ++e) {
           const float yv = (float)yh[e];
           const float mv = kVec ? (float)mpre[n % kPre][i % (NMIX > 0 ? NMIX : 1)].v[e] : (float)p.mix[i][c0 + e];
-          o[e] = (_Float16)__builtin_fmaf((float)prev[e] - yv, mv, yv);
+          o[e] = f16_of(__builtin_fmaf((float)prev[e] - yv, mv, yv));
         }
         if constexpr (VW == 8) {
           st8(p.out[i] + odst, *reinterpret_cast<const h8*>(o));
@@ -423,6 +423,191 @@ int launch_ln(const char* fn, const LnArgs& p, bool vec_ok, hipStream_t stream) 
   }
 #undef VK_LN_GO
   return check_launch(fn);
+}
+
+// ---- mixed-batch fusion: residual add + LayerNorm + token-shift lerp over row groups.
+//
+// Rows are laid out group by group (a decode group: B sequences of one row; a prefill
+// chunk group: B sequences of T consecutive rows).  For row t of a sequence the lerp's
+// "previous token" is the LayerNorm output of row t - 1, or for t = 0 the sequence's shift
+// row in the slot pool, which then receives the output of the sequence's last row.  One
+// 256-lane workgroup per row computes the LayerNorm of its row and of one more: row t - 1
+// (t > 0), or the sequence's last row (t = 0, T > 1; the t = 0 workgroup is the only reader
+// and the only writer of the shift row, so no other workgroup races it).  The two rows'
+// reductions share their barriers.  The results are the bits of vkwr_layer_norm_f16 (with
+// the residual) followed by vkwr_token_shift_mix_slots_f16 per group, without the LayerNorm
+// output's trip through HBM and the second launch.  Algorithmic bytes per row: 2C (x) +
+// 2C (residual) + 2C (x_out) + 2nC (n lerp outputs), plus the shift row of each sequence.
+// Measured at 2304 rows x 4096 (256 decode rows + 4 chunks of 512): 34 us with 6 lerps
+// (5.5 TB/s of algorithmic bytes), 21 us with 1, where the launches it replaces took 13 us
+// (the LayerNorm) plus 37 us (6 lerps) or 17 us (1 lerp) for the two token-shift launches.
+constexpr int kMaxShiftGroups = 8;
+
+struct LnShiftGroup {
+  int64_t r0;
+  int B, T;
+  const int32_t* slots;
+};
+
+struct LnShiftArgs {
+  int C, n_groups;
+  const _Float16* x;
+  const _Float16* residual;  // may be null
+  const _Float16* weight;
+  const _Float16* bias;
+  float eps;
+  _Float16* x_out;
+  _Float16* shift;
+  int64_t n_shift;
+  const _Float16* mix[6];
+  _Float16* out[6];
+  LnShiftGroup g[kMaxShiftGroups];
+};
+
+// Two workgroup sums with one barrier: each is block_sum_ln's value, in its order.
+template <int NW>
+__device__ __forceinline__ void block_sum2_ln(float& a, float& b, float* red) {
+  a = wave_sum_dpp(a);
+  b = wave_sum_dpp(b);
+  if ((threadIdx.x & 63) == 0) {
+    red[threadIdx.x >> 6] = a;
+    red[NW + (threadIdx.x >> 6)] = b;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float ta = red[0], tb = red[NW];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    ta += red[w];
+    tb += red[NW + w];
+  }
+  a = ta;
+  b = tb;
+}
+
+template <int NV, int NMIX>
+__global__ __launch_bounds__(kThreads) void ln_shift_rows_kernel(LnShiftArgs p) {
+  __shared__ float red[2][2 * kWaves];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, C = p.C;
+  int gi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxShiftGroups; ++i)
+    if (i < p.n_groups && row >= p.g[i].r0) gi = i;
+  const int64_t r0 = p.g[gi].r0;
+  const int T = p.g[gi].T;
+  const int64_t local = row - r0;
+  const int b = (int)(local / T), t = (int)(local - (int64_t)b * T);
+  const int64_t slot = p.g[gi].slots[b];
+  const int64_t dst = row * (int64_t)C;
+  if (slot < 0 || slot >= p.n_shift) {
+    // A slot outside the pool: the row's outputs are NaN and no shift row is touched.
+    const _Float16 nan = (_Float16)__builtin_nanf("");
+    for (int c = tid; c < C; c += kThreads) {
+      p.x_out[dst + c] = nan;
+#pragma unroll
+      for (int i = 0; i < NMIX; ++i) p.out[i][dst + c] = nan;
+    }
+    return;
+  }
+  const bool has_sec = t > 0 || T > 1;
+  // the second row: the previous one, or (t = 0) the sequence's last one; itself if none
+  const int64_t srow2 = t > 0 ? row - 1 : (T > 1 ? row + (T - 1) : row);
+  const int64_t sec = srow2 * (int64_t)C;
+  const int64_t sdst = slot * (int64_t)C;
+  auto col = [&](int n) {
+    const int c = (tid + n * kThreads) * 8;
+    return c < C ? c : C - 8;
+  };
+  // every load first (the shift row only where it is read), then the arithmetic
+  h8 xc[NV], rc[NV], xs[NV], rs[NV], wp[NV], bp[NV], mp[NV][NMIX], old[NV];
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int cl = col(n);
+    xc[n] = ld8(p.x + dst + cl);
+    xs[n] = ld8(p.x + sec + cl);
+    wp[n] = ld8(p.weight + cl);
+    bp[n] = ld8(p.bias + cl);
+#pragma unroll
+    for (int i = 0; i < NMIX; ++i) mp[n][i] = ld8(p.mix[i] + cl);
+  }
+  if (p.residual) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      rc[n] = ld8(p.residual + dst + col(n));
+      rs[n] = ld8(p.residual + sec + col(n));
+    }
+  }
+  if (t == 0) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) old[n] = ld8(p.shift + sdst + col(n));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float vc[NV][8], vs[NV][8], sc = 0.0f, ss = 0.0f;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const bool in = (tid + n * kThreads) * 8 < C;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vc[n][e] = (float)xc[n].v[e];
+      vs[n][e] = (float)xs[n].v[e];
+    }
+    if (p.residual) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vc[n][e] = vc[n][e] + (float)rc[n].v[e];
+        vs[n][e] = vs[n][e] + (float)rs[n].v[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sc += in ? vc[n][e] : 0.0f;
+      ss += in ? vs[n][e] : 0.0f;
+    }
+  }
+  block_sum2_ln<kWaves>(sc, ss, red[0]);
+  const float mc = sc / (float)C, ms = ss / (float)C;
+  float qc = 0.0f, qs = 0.0f;
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    if ((tid + n * kThreads) * 8 < C) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float dc = vc[n][e] - mc, ds = vs[n][e] - ms;
+        qc = __builtin_fmaf(dc, dc, qc);
+        qs = __builtin_fmaf(ds, ds, qs);
+      }
+    }
+  }
+  block_sum2_ln<kWaves>(qc, qs, red[1]);
+  const float rc_std = rsqrtf(qc / (float)C + p.eps), rs_std = rsqrtf(qs / (float)C + p.eps);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    const int c0 = (tid + n * kThreads) * 8;
+    if (c0 >= C) continue;
+    // (element-wise selects: a select of whole h8 values goes through scratch memory)
+    h8 yc, xo, prev, snew;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float wt = (float)wp[n].v[e], bs = (float)bp[n].v[e];
+      yc.v[e] = f16_of(__builtin_fmaf((vc[n][e] - mc) * rc_std, wt, bs));
+      const _Float16 ys = f16_of(__builtin_fmaf((vs[n][e] - ms) * rs_std, wt, bs));
+      xo.v[e] = (_Float16)vc[n][e];
+      prev.v[e] = t > 0 ? ys : old[n].v[e];
+      snew.v[e] = has_sec ? ys : yc.v[e];
+    }
+    st8(p.x_out + dst + c0, xo);
+#pragma unroll
+    for (int i = 0; i < NMIX; ++i) {
+      h8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float yv = (float)yc.v[e];
+        o.v[e] = f16_of(__builtin_fmaf((float)prev.v[e] - yv, (float)mp[n][i].v[e], yv));
+      }
+      st8(p.out[i] + dst + c0, o);
+    }
+    if (t == 0) st8(p.shift + sdst + c0, snew);
+  }
 }
 
 }  // namespace
@@ -590,6 +775,65 @@ extern "C" int vkwr_add_layer_norm_mix_parts_frag_f16(int64_t rows, int C, const
   VK_REQUIRE(part_stride >= rows * (int64_t)C, "%s: part_stride below rows * C", fn);
   return add_ln_mix(fn, rows, C, nullptr, residual, shift_state, weight, bias, n_mix, mix, eps, x_out, out, nullptr,
                     shift_slots, 0, n_shift, 1, stream, x_parts, n_parts, part_stride);
+}
+
+extern "C" int vkwr_add_layer_norm_shift_rows_f16(int64_t rows, int C, const uint16_t* x,
+                                                  const uint16_t* residual, const uint16_t* weight,
+                                                  const uint16_t* bias, float eps, uint16_t* x_out, int n_mix,
+                                                  const uint16_t* const* mix, uint16_t* const* out,
+                                                  uint16_t* shift_state, int64_t n_shift, int n_groups,
+                                                  const vkwr_ln_shift_group* groups, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_add_layer_norm_shift_rows_f16";
+  VK_REQUIRE(n_mix == 1 || n_mix == 6, "%s: n_mix must be 1 or 6 (got %d)", fn, n_mix);
+  VK_REQUIRE(n_groups >= 1 && n_groups <= kMaxShiftGroups, "%s: 1..%d groups (got %d)", fn, kMaxShiftGroups,
+             n_groups);
+  VK_REQUIRE(groups && mix && out, "%s: null pointer", fn);
+  VK_REQUIRE(rows >= 0 && rows <= 0x7fffffff, "%s: bad rows", fn);
+  VK_REQUIRE(C > 0 && C % 8 == 0 && C <= 4096, "%s: C must be a multiple of 8 in 8..4096 (got %d)", fn, C);
+  VK_REQUIRE(n_shift >= 0, "%s: negative n_shift", fn);
+  LnShiftArgs p{};
+  p.C = C;
+  p.n_groups = n_groups;
+  int64_t r = 0;
+  for (int i = 0; i < n_groups; ++i) {
+    const vkwr_ln_shift_group& g = groups[i];
+    VK_REQUIRE(g.row0 == r, "%s: group %d starts at row %lld, expected %lld", fn, i, (long long)g.row0,
+               (long long)r);
+    VK_REQUIRE(g.B >= 1 && g.T >= 1 && g.slots, "%s: group %d needs B >= 1, T >= 1 and slots", fn, i);
+    p.g[i] = LnShiftGroup{g.row0, g.B, g.T, g.slots};
+    r += (int64_t)g.B * g.T;
+  }
+  VK_REQUIRE(r == rows, "%s: the groups cover %lld rows, not %lld", fn, (long long)r, (long long)rows);
+  if (rows == 0) return VKWR_OK;
+  VK_REQUIRE(x && weight && bias && x_out && shift_state, "%s: null pointer", fn);
+  bool vec = aligned16(x) && (!residual || aligned16(residual)) && aligned16(weight) && aligned16(bias) &&
+             aligned16(x_out) && aligned16(shift_state);
+  p.x = reinterpret_cast<const _Float16*>(x);
+  p.residual = reinterpret_cast<const _Float16*>(residual);
+  p.weight = reinterpret_cast<const _Float16*>(weight);
+  p.bias = reinterpret_cast<const _Float16*>(bias);
+  p.eps = eps;
+  p.x_out = reinterpret_cast<_Float16*>(x_out);
+  p.shift = reinterpret_cast<_Float16*>(shift_state);
+  p.n_shift = n_shift;
+  for (int i = 0; i < n_mix; ++i) {
+    VK_REQUIRE(mix[i] && out[i], "%s: null pointer", fn);
+    p.mix[i] = reinterpret_cast<const _Float16*>(mix[i]);
+    p.out[i] = reinterpret_cast<_Float16*>(out[i]);
+    vec = vec && aligned16(mix[i]) && aligned16(out[i]);
+  }
+  VK_REQUIRE(vec, "%s: every tensor must be 16-byte aligned", fn);
+  const dim3 grid((unsigned)rows), block(kThreads);
+  const bool one = C <= 8 * kThreads;
+  if (n_mix == 1) {
+    if (one) hipLaunchKernelGGL((ln_shift_rows_kernel<1, 1>), grid, block, 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((ln_shift_rows_kernel<2, 1>), grid, block, 0, (hipStream_t)stream, p);
+  } else {
+    if (one) hipLaunchKernelGGL((ln_shift_rows_kernel<1, 6>), grid, block, 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((ln_shift_rows_kernel<2, 6>), grid, block, 0, (hipStream_t)stream, p);
+  }
+  return check_launch(fn);
 }
 
 extern "C" int vkwr_add_f16(int64_t n, const uint16_t* x, const uint16_t* y, uint16_t* out,
