@@ -400,11 +400,14 @@ def test_big_gemm_batch_with_empty_problem_and_oracle(gpu):
 
 @pytest.mark.parametrize("M,K,N", [
     (1024, 16384, 2048),   # 32 tiles, long K: every tile split into 8 k-parts
-    (2304, 16384, 4096),   # the 7B FFN value shape: 144 tiles split into 3 k-parts
+    (2304, 16384, 4096),   # the 7B FFN value shape: 144 tiles of 256 stages, layered split
+                           # (144 stages per CU: [0, 144) of every tile, [144, 256) of 112 tiles
+                           # whole, the other 32 in 16-stage pieces)
+    (2304, 8192, 4096),    # 144 tiles of 128 stages: per 72, layered with 8-stage pieces
     (2304, 4096, 16384),   # the 7B FFN key shape: 2 whole rounds + a 64-tile tail split in 4
 ])
 def test_big_gemm_split_tail(gpu, M, K, N):
-    """Tail tiles split into k-parts (fp32 partials, ordered fixup): against the row-major
+    """Tail tiles split into k-parts or balanced pieces (fp32 partials, ordered fixup): against the row-major
     kernel on the transposed weight within the fp32 re-association bound, and run-to-run
     bitwise identical (also through the relu^2 epilogue)."""
     from vkwr_amd import capi

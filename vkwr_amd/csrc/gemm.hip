@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <numeric>
 #include <type_traits>
 
 #include "vk_capi.h"
@@ -412,7 +413,12 @@ int reduce_wgs(const Batch& bt) {
 // and the split pays for its traffic, each of them is cut into S equal k-parts, one per
 // workgroup of gemm_big_sk_kernel, which store fp32 partial tiles; gemm_big_fixup_kernel
 // adds each tile's S partials in increasing k order (deterministic) and applies the
-// epilogue.  S is chosen by a time model (plan_big).
+// epilogue.  Where R tiles divide unevenly over the CUs (the 7B FFN value GEMM: 144 tiles
+// of 256 stages on 256 CUs) a layered split gives every CU the same number of stages
+// instead (Layers below; 293 -> 275 us for that GEMM's split kernel, fixup 24 -> 29 us).
+// A split that hands each CU one contiguous range of the tiles laid end to end balances
+// the work as well, but its CUs then sit at unrelated k offsets and share no operand
+// panels in the L2 (measured 349 us).  The split is chosen by a time model (plan_big).
 //
 // Workgroup b runs on XCD b % 8; logical tiles are handed out so that each XCD holds a
 // contiguous range, walked in groups of 4 tile rows, which keeps the A row blocks and B
@@ -426,10 +432,44 @@ struct BigPlan {
   int bm;        // tile rows: 256 or 192
   int dp_tiles;  // D: tiles computed whole
   int sk_tiles;  // R: tiles split into k-parts
-  int parts;     // S: k-parts per split tile
+  int parts;     // S: k-parts per split tile (equal split)
   int nst;       // k-stages per tile (all problems, when sk_tiles > 0)
-  float* ws;     // one partial tile per part: [R][S]
+  int wgs;       // W > 0: layered split over W workgroups (below); 0: equal split
+  int per;       // layered split: k-stages per workgroup (R nst / W)
+  int gran;      // layered split: k-stages per third-layer piece
+  float* ws;     // partial tiles: [R][S] (equal split) or one per piece (layered split)
 };
+
+// Position of workgroup b among W when the blocks of each XCD (b % 8) take a contiguous
+// range of positions (the order gemm_big_kernel hands out tiles in).
+__device__ __forceinline__ int xcd_contiguous(int b, int W) {
+  const int xb = b & 7, idx = b >> 3, q8 = W >> 3, r8 = W & 7;
+  return (xb < r8 ? xb * (q8 + 1) : r8 * (q8 + 1) + (xb - r8) * q8) + idx;
+}
+
+// Layered split of R tiles of nst k-stages over W workgroups (R <= W < 2R), each doing
+// per = R nst / W stages (per >= nst / 2), so that every CU gets the same work although the
+// tiles do not divide evenly over the CUs.  Every piece of one layer covers the same k range,
+// so workgroups that share A or B panels stream them through the L2 together:
+//   layer 1: workgroup t < R takes stages [0, per) of tile t;
+//   layer 2: workgroup R + j (j < W' = W - R) takes [per, nst) of tile j (L = nst - per stages);
+//   layer 3: the other R'' = R - W' tiles' [per, nst) ranges, cut into L / g pieces of
+//            g = gran stages, in k-major order (piece q: k class q / R'', tile W' + q % R''),
+//            b / g consecutive pieces to each layer-2 workgroup (b = per - L).
+// Partial slot of a piece: layer 1 t, layer 2 R + j, layer 3 R + W' + q.
+struct Layers {
+  int R, W2, L, R3, npc, bpw;  // R, W', L, R'', pieces per tile, pieces per workgroup (layer 3)
+};
+__device__ __host__ inline Layers layers_of(const BigPlan& pl) {
+  Layers y;
+  y.R = pl.sk_tiles;
+  y.W2 = pl.wgs - pl.sk_tiles;
+  y.L = pl.nst - pl.per;
+  y.R3 = y.R - y.W2;
+  y.npc = y.L / pl.gran;
+  y.bpw = (pl.per - y.L) / pl.gran;
+  return y;
+}
 
 __device__ __forceinline__ int big_slot(int row, int c) { return row * 8 + (c ^ ((row >> 1) & 7)); }
 
@@ -763,18 +803,41 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
 template <int BM, int kEpi>
 __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int tiles) {
   __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];  // [buffer][A/B]: 128 KiB
-  const int xb = blockIdx.x & 7, idx = blockIdx.x >> 3, q8 = tiles >> 3, r8 = tiles & 7;
-  const int L = (xb < r8 ? xb * (q8 + 1) : r8 * (q8 + 1) + (xb - r8) * q8) + idx;
+  const int L = xcd_contiguous(blockIdx.x, tiles);
   int m0, n0;
   const Prob& P = bt.p[big_tile<BM>(bt, L, m0, n0)];
   big_tile_run<BM, false, kEpi>(sm, P, m0, n0, 0, P.k / kBigBK, nullptr);
 }
 
-// Split tiles: workgroup b computes part b % S (k-stages [p nst / S, (p+1) nst / S)) of
-// split tile D + b / S into partial slot b.
+// Split tiles.  Equal split: workgroup b computes part b % S (k-stages [p nst / S, (p+1) nst / S))
+// of split tile D + b / S into partial slot b.  Balanced split: the workgroup at position lw
+// (XCD-contiguous) computes its stage range, one piece per tile it touches, the piece of tile
+// t into slot lw pmax + (t - its first tile); so every CU gets the same number of stages
+// even when the split tiles do not divide evenly over the CUs.
 template <int BM>
 __global__ __launch_bounds__(256, 1) void gemm_big_sk_kernel(Batch bt, BigPlan pl) {
   __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];
+  if (pl.wgs > 0) {
+    const Layers y = layers_of(pl);
+    const size_t tile = (size_t)BM * kBigBM;
+    auto piece = [&](int t, int ks, int ke, int slot) __attribute__((always_inline)) {
+      int m0, n0;
+      const Prob& P = bt.p[big_tile<BM>(bt, pl.dp_tiles + t, m0, n0)];
+      big_tile_run<BM, true, -1>(sm, P, m0, n0, ks, ke, pl.ws + (size_t)slot * tile);
+    };
+    if ((int)blockIdx.x < y.R) {
+      const int t = xcd_contiguous(blockIdx.x, y.R);
+      piece(t, 0, pl.per, t);
+      return;
+    }
+    const int j = xcd_contiguous(blockIdx.x - y.R, y.W2);
+    piece(j, pl.per, pl.nst, y.R + j);
+    for (int q = j * y.bpw; q < (j + 1) * y.bpw; ++q) {
+      const int ks = pl.per + (q / y.R3) * pl.gran;
+      piece(y.W2 + q % y.R3, ks, ks + pl.gran, y.R + y.W2 + q);
+    }
+    return;
+  }
   const int t = blockIdx.x / pl.parts, p = blockIdx.x - t * pl.parts;
   int m0, n0;
   const Prob& P = bt.p[big_tile<BM>(bt, pl.dp_tiles + t, m0, n0)];
@@ -783,7 +846,9 @@ __global__ __launch_bounds__(256, 1) void gemm_big_sk_kernel(Batch bt, BigPlan p
 }
 
 // Fixup: blockIdx.y = split tile t, blockIdx.x = accumulator block (i, j) of the partial
-// layout; adds the tile's S partials in increasing k order, applies the epilogue, stores.
+// layout; adds the tile's partials in increasing k order (equal split: its S parts; layered
+// split: its layer-1 piece, then its layer-2 piece or its layer-3 pieces in k order), applies
+// the epilogue, stores.
 template <int BM, int kEpi>
 __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan pl) {
   const int t = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
@@ -795,17 +860,38 @@ __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan p
   if (col >= P.n) return;
   // The 16 values of a part are loaded together (the workspace holds whole
   // tiles, so rows past M are in bounds), then the parts are added in order.
-  const float* base = pl.ws + (size_t)t * pl.parts * (BM * kBigBM) + (size_t)blk * 16 * 256 + tid;
+  const size_t in_tile = (size_t)blk * 16 * 256 + tid;
   float acc[16];
+  if (pl.wgs > 0) {
+    const Layers y = layers_of(pl);
+    auto slot = [&](int q) { return pl.ws + (size_t)q * (BM * kBigBM) + in_tile; };
+    auto add = [&](const float* bq) __attribute__((always_inline)) {
+      float nx[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = base[r * 256];
-  for (int q = 1; q < pl.parts; ++q) {
-    const float* bq = base + (size_t)q * (BM * kBigBM);
-    float nx[16];
+      for (int r = 0; r < 16; ++r) nx[r] = bq[r * 256];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) nx[r] = bq[r * 256];
+      for (int r = 0; r < 16; ++r) acc[r] += nx[r];
+    };
+    const float* b0 = slot(t);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] += nx[r];
+    for (int r = 0; r < 16; ++r) acc[r] = b0[r * 256];
+    if (t < y.W2) {
+      add(slot(y.R + t));
+    } else {
+      for (int i = 0; i < y.npc; ++i) add(slot(y.R + y.W2 + i * y.R3 + (t - y.W2)));
+    }
+  } else {
+    const float* base = pl.ws + (size_t)t * pl.parts * (BM * kBigBM) + in_tile;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = base[r * 256];
+    for (int q = 1; q < pl.parts; ++q) {
+      const float* bq = base + (size_t)q * (BM * kBigBM);
+      float nx[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) nx[r] = bq[r * 256];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += nx[r];
+    }
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -1432,7 +1518,7 @@ double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
     P.tile_begin = T;
     T += P.tiles_m * P.tiles_n;
   }
-  pl = BigPlan{BM, T, 0, 1, 0, nullptr};
+  pl = BigPlan{BM, T, 0, 1, 0, 0, 0, 0, nullptr};
   const int G = device_cus();
   const double stage = 1.7 * (BM == 192 ? 0.86 : 1.0), over = 2.0 * stage;
   if (!uniform_k) return -(double)T / ((double)((T + G - 1) / G) * G);
@@ -1451,11 +1537,30 @@ double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
       best_s = S;
     }
   }
-  if (best_s > 1) {
+  // Layered split of the R tiles over all G CUs (when its shape conditions hold): R nst / G
+  // stages on every CU, in 1 + 1 + b / g pieces at most.
+  int lay_per = 0, lay_g = 0;
+  if (R <= G && G < 2 * R && ((int64_t)R * nst) % G == 0) {
+    const int per = (int)((int64_t)R * nst / G), L = nst - per, b = per - L;
+    int g = std::gcd(b, L);
+    if (L > 0 && b > 0 && g >= 8) {
+      const int R3 = R - (G - R), pieces = R + (G - R) + R3 * (L / g);
+      const double t = full + per * stage + (2 + b / g) * over + (double)pieces * 2 * BM * kBigBM * 4 / 5e6;
+      if (t < best) {
+        best = t;
+        lay_per = per;
+        lay_g = g;
+      }
+    }
+  }
+  if (lay_per > 0 || best_s > 1) {
     pl.dp_tiles = D;
     pl.sk_tiles = R;
-    pl.parts = best_s;
+    pl.parts = lay_per > 0 ? 0 : best_s;
     pl.nst = nst;
+    pl.wgs = lay_per > 0 ? G : 0;
+    pl.per = lay_per;
+    pl.gran = lay_g;
   }
   return best;
 }
@@ -1468,7 +1573,13 @@ int64_t plan_big(Batch& bt, BigPlan& pl) {
   const double t192 = plan_big_bm(bt, p192, 192);
   const double t256 = plan_big_bm(bt, pl, 256);
   if (t256 < 0 ? t192 < t256 - 0.05 : t192 < 0.95 * t256) plan_big_bm(bt, pl, 192);
-  return pl.sk_tiles > 0 ? (int64_t)pl.sk_tiles * pl.parts * pl.bm * kBigBM * 4 : 0;
+  if (pl.sk_tiles == 0) return 0;
+  int64_t slots = (int64_t)pl.sk_tiles * pl.parts;
+  if (pl.wgs > 0) {
+    const Layers y = layers_of(pl);
+    slots = (int64_t)y.R + y.W2 + (int64_t)y.R3 * y.npc;
+  }
+  return slots * pl.bm * kBigBM * 4;
 }
 
 int total_wgs(const Batch& bt) {
@@ -1615,7 +1726,8 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
       constexpr int BM = decltype(bm_tag)::value;
       if (pl.dp_tiles > 0) hipLaunchKernelGGL(whole, dim3(pl.dp_tiles), dim3(256), 0, s, bt, pl.dp_tiles);
       if (pl.sk_tiles > 0) {
-        hipLaunchKernelGGL(gemm_big_sk_kernel<BM>, dim3(pl.sk_tiles * pl.parts), dim3(256), 0, s, bt, pl);
+        const int sk_wgs = pl.wgs > 0 ? pl.wgs : pl.sk_tiles * pl.parts;
+        hipLaunchKernelGGL(gemm_big_sk_kernel<BM>, dim3(sk_wgs), dim3(256), 0, s, bt, pl);
         hipLaunchKernelGGL(fix, dim3(4 * (BM / 64), pl.sk_tiles), dim3(256), 0, s, bt, pl);
       }
     };
