@@ -73,6 +73,19 @@ VKWR_EXPORT int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* 
                                  const uint16_t* a, const uint16_t* b, uint16_t* y,
                                  void* stream);
 
+/* One decode step (T = 1) of vkwr_wkv7_fp32_forward_slots with the dot products in the
+ * row-split order of the prefill kernels (eight 8-term FMA chains per state row, combined
+ * pairwise) instead of one 64-term chain, and no LDS: it can run on a second stream beside
+ * the chunked prefill kernel, which holds most of each CU's LDS.  Same arguments and slot
+ * semantics (out-of-range slot: NaN y rows, pool untouched); pool and v 16-byte aligned,
+ * r, w, k, a, b 8-byte aligned.  No counterpart in the reference (its T = 1 op is
+ * wkv_forward_fp32, csrc/v1/wkv/torch_bindings.cpp:179-188, in one-chain order); for
+ * mixed prefill + decode batches. */
+VKWR_EXPORT int vkwr_wkv7_fp32_step_rows_slots(int B, int C, int H, float* pool, int n_slots,
+                                               const int32_t* slots, const uint16_t* r, const uint16_t* w,
+                                               const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                               const uint16_t* b, uint16_t* y, void* stream);
+
 /* Layouts of an fp32 64x64 WKV state block (16 KiB) in a pool.
  *   VKWR_WKV_STATE_STD: row-major S[i][j] at float 64 i + j (the reference's
  *     [.., H, 64, 64] layout; every other entry point uses it).

@@ -172,9 +172,9 @@ def _mixed_vs_oracle(gpu, cfg, P, Bd, Bp, T, seed, state_tol):
     oracle/model_ref: decode rows against one reference decode step, each chunk's
     last-token logits and final states against T sequential reference decode steps, and
     the last layer's WKV of both groups against the C oracle on the engine's own WKV
-    inputs: bit for bit for the decode rows (the one-chain order of the T = 1 kernel) and
-    chunks under 16 tokens (the row-split order), at tolerance for longer chunks (the
-    chunked kernel, against the reference order).  Untouched slots stay bitwise unchanged.
+    inputs: bit for bit for the decode rows and chunks under 16 tokens (both in the row-split
+    order: the mixed step's T = 1 kernel and the row-split prefill kernel), at tolerance for
+    longer chunks (the chunked kernel, against the reference order).  Untouched slots stay bitwise unchanged.
     End to end the states drift from the float32 model's by the fp16 rounding of the
     intermediates, compounded over the chunk's T tokens; state_tol bounds that drift
     relative to the largest state value."""
@@ -207,7 +207,7 @@ def _mixed_vs_oracle(gpu, cfg, P, Bd, Bp, T, seed, state_tol):
     ins = [t.cpu().numpy() for t in (eng.r, eng.w, eng.new_k, v_last, eng.neg_kk, eng.kka)]
     y_eng = eng.y.cpu().numpy()
     chunked = T >= 16
-    for (B, TT, r0, order, sl, base) in ((Bd, 1, 0, "seq", sd, 0),
+    for (B, TT, r0, order, sl, base) in ((Bd, 1, 0, "rows", sd, 0),
                                          (Bp, T, Bd, "seq" if chunked else "rows", sp, Bd)):
         n = B * TT
         pool = wkv0[L, base:base + B].cpu().numpy().copy()

@@ -626,3 +626,41 @@ def test_slots_large_pool_nontemporal_path_same_bits(gpu):
     others = torch.ones(P_big, dtype=torch.bool, device=gpu)
     others[slots_big.long()] = False
     assert torch.equal(big[others], before[others])
+
+
+@pytest.mark.parametrize("P,B,H", [(512, 128, 32), (520, 5, 32), (40, 9, 4)])
+def test_step_rows_slots_match_rows_oracle(gpu, P, B, H):
+    """vkwr_wkv7_fp32_step_rows_slots: y and the pool bit-exact against the oracle's row-split
+    order (order="rows") at T = 1, two steps, untouched slots unchanged.  P = 520 at H = 32 is
+    a 260 MiB pool: the non-temporal state path."""
+    from vkwr_amd import capi
+    C = H * 64
+    pool_np = make_state(P, H, seed=P + B)
+    slots_np = np.random.default_rng(P + B).permutation(P)[:B].astype(np.int32)
+    pool = torch.from_numpy(pool_np).to(gpu)
+    slots = torch.from_numpy(slots_np).to(gpu)
+    for step in range(2):
+        ins = make_wkv_inputs(B, 1, H, seed=2000 + step)
+        y_ref = orc.wkv_fp32_slots(B, 1, C, H, pool_np, slots_np.astype(np.int64), *ins, order="rows")
+        y = torch.empty(B, C, dtype=torch.float16, device=gpu)
+        capi.wkv_step_rows_slots(B, C, H, pool, slots, *_dev([x.reshape(B, C) for x in ins], gpu), y)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), y_ref.reshape(B, C).view(np.uint16)), step
+    assert np.array_equal(pool.cpu().numpy(), pool_np)
+
+
+def test_step_rows_slots_out_of_range_is_skipped(gpu):
+    """A slot outside [0, P): NaN y rows for that sequence, pool bitwise unchanged there."""
+    from vkwr_amd import capi
+    P, B, H = 8, 3, 2
+    C = H * 64
+    pool = torch.from_numpy(make_state(P, H, seed=5)).to(gpu)
+    before = pool.clone()
+    slots = torch.tensor([1, P + 5, 4], dtype=torch.int32, device=gpu)
+    ins = _dev([x.reshape(B, C) for x in make_wkv_inputs(B, 1, H, seed=5)], gpu)
+    y = torch.empty(B, C, dtype=torch.float16, device=gpu)
+    capi.wkv_step_rows_slots(B, C, H, pool, slots, *ins, y)
+    torch.cuda.synchronize()
+    assert torch.isnan(y[1]).all() and not torch.isnan(y[0]).any() and not torch.isnan(y[2]).any()
+    untouched = [0, 2, 3, 5, 6, 7]
+    assert torch.equal(pool[untouched], before[untouched])

@@ -17,7 +17,8 @@ Per layer (x: previous block output, res: residual stream, rows = all rows):
           the adapter ranks padded to multiples of 64 with zeros, so the launch runs on
           the large-M kernel)
   k', -kk, kk*a = kk/a gate over rows
-  y   = WKV-7 per group on the slot pool (T = 1 decode kernel, T > 1 prefill kernel)
+  y   = WKV-7 per group on the slot pool (T > 1: the chunked prefill kernel; the T = 1
+        decode group in the row-split order, on a second stream beside the prefill)
   o   = (GroupNorm(y) + bonus) * g  W_o^T over rows
   res, xk = add + LN2 + token shift per group (ffn shift pool; one launch)
   x   = relu(xk K^T)^2 V^T over rows
@@ -97,6 +98,11 @@ class MixedEngine:
         need = max(capi.gemm_workspace_bytes_upto(ps) for ps in self._gemm_batches(max_rows, 1))
         need = max(need, capi.gemm_workspace_bytes_upto(self._head_problem(self.max_seqs)))
         self.ws = torch.empty(max(need, 0), dtype=torch.uint8, device=dev)
+        # The decode rows' WKV step runs on a second stream beside the prefill chunks' (its
+        # kernel uses no LDS, so it fits on the CUs the chunk kernel holds); default priority.
+        self.side = torch.cuda.Stream(device=dev) if dev.type == "cuda" else None
+        self.fork = torch.cuda.Event() if dev.type == "cuda" else None
+        self.join = torch.cuda.Event() if dev.type == "cuda" else None
 
     # -- GEMM batches (shared by planning and execution)
     def _proj(self, L, W, R, first):
@@ -135,6 +141,29 @@ class MixedEngine:
                 [gp(s.xk[:R], L["key"], s.act[:R], epilogue=capi.EPI_RELU_SQUARE)],
                 [gp(s.act[:R], L["value"], s.ffn[:R])]]
         return out
+
+    def _wkv(self, groups, pool, v):
+        """WKV-7 of every group on the slot pool: prefill groups (T > 1) on the current stream,
+        then the decode group (T = 1, row-split order, no LDS) on the side stream, forked after
+        the gate and joined before the GroupNorm, so the decode rows' HBM-bound state traffic
+        runs while the prefill chunks occupy the matrix cores."""
+        C, H = self.cfg.n_embd, self.cfg.n_head
+        s = self
+        args = lambda r0, n: (s.r[r0:r0 + n], s.w[r0:r0 + n], s.new_k[r0:r0 + n], v[r0:r0 + n],  # noqa: E731
+                              s.neg_kk[r0:r0 + n], s.kka[r0:r0 + n], s.y[r0:r0 + n])
+        dec = [g for g in groups if g[1] == 1]
+        main = torch.cuda.current_stream()
+        if dec:
+            s.fork.record(main)
+        for B, T, r0, slots, _ in groups:
+            if T > 1:
+                capi.wkv_slots(B, T, C, H, pool, slots, *args(r0, B * T))
+        for B, _, r0, slots, _ in dec:
+            s.side.wait_event(s.fork)
+            with torch.cuda.stream(s.side):
+                capi.wkv_step_rows_slots(B, C, H, pool, slots, *args(r0, B))
+            s.join.record(s.side)
+            main.wait_event(s.join)
 
     def _head_problem(self, S):
         return [capi.gemm_problem(self.h[:S], self.model.head, self.logits[:S])]
@@ -179,11 +208,7 @@ class MixedEngine:
             v = (s.v_first if first else s.v_new)[:R]
             capi.kk_a_gate(R, 1, C, H, s.k[:R], L["k_k"], L["a0"], s.a12[:R], L["k_a"], s.new_k[:R],
                            s.neg_kk[:R], s.kka[:R])
-            for B, T, r0, slots, _ in groups:
-                n = B * T
-                sl = slice(r0, r0 + n)
-                capi.wkv_slots(B, T, C, H, state.wkv[l], slots, s.r[sl], s.w[sl], s.new_k[sl], v[sl],
-                               s.neg_kk[sl], s.kka[sl], s.y[sl])
+            self._wkv(groups, state.wkv[l], v)
             capi.groupnorm_bonus_gate(R, 1, C, H, s.y[:R], s.r[:R], s.new_k[:R], v, L["r_k"], L["lnx_w"],
                                       L["lnx_b"], s.g[:R], s.o_in[:R])
             capi.gemm([capi.gemm_problem(s.o_in[:R], L["Wo"], s.o[:R])], ws)

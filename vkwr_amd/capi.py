@@ -77,6 +77,7 @@ _gate = _sig("vkwr_tmix_kk_a_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p,
 _gn = _sig("vkwr_tmix_groupnorm_bonus_gate_f16", [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _wkv_slots = _sig("vkwr_wkv7_fp32_forward_slots",
                   [_i, _i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p])
+_wkv_step_rows = _sig("vkwr_wkv7_fp32_step_rows_slots", [_i, _i, _i, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p])
 _frag_gemm = _sig("vkwr_frag_gemm_f16", [_i, ctypes.POINTER(FragProblem), _p])
 _act = _sig("vkwr_activation_f16", [_i, _i64, _p, _p, _p])
 ACT_EW_TANH, ACT_EW_SIGMOID = 1, 2  # vkwr_activation_f16 codes
@@ -293,6 +294,13 @@ def _arr_frag(problems):
 def wkv_slots(B, T, C, H, pool, slots, r, w, k, v, a, b, y):
     _check(_wkv_slots(B, T, C, H, _ptr(pool), pool.shape[0], _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
                       _ptr(a), _ptr(b), _ptr(y), _stream()), "vkwr_wkv7_fp32_forward_slots")
+
+
+def wkv_step_rows_slots(B, C, H, pool, slots, r, w, k, v, a, b, y):
+    """One decode step on the slot pool in the row-split dot-product order, without LDS
+    (vkwr_wkv7_fp32_step_rows_slots)."""
+    _check(_wkv_step_rows(B, C, H, _ptr(pool), pool.shape[0], _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
+                          _ptr(a), _ptr(b), _ptr(y), _stream()), "vkwr_wkv7_fp32_step_rows_slots")
 
 
 def wkv_decode_fused(B, C, H, pool, slots, r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_w, ln_b, out, frag=False,

@@ -278,6 +278,95 @@ __device__ __forceinline__ float sum8(float x) {
 // compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// ---- decode step (T == 1) in the row-split order, without LDS.
+//
+// One wave per (sequence, head); lane (g = lane & 7, q = lane >> 3) holds rows 8q..8q+7 of the
+// state at columns 4g..4g+3 and 32+4g..32+4g+3 (64 values in VGPRs) -- the row-split kernel's
+// column ownership, so each dot product is its eight 8-term FMA chains and sum8 butterfly and
+// the results are the bits of the row-split order.  Each state load or store instruction covers
+// 8 rows x 128 contiguous bytes (8 whole lines), so the state moves straight between HBM and
+// registers with no staging tile and no barrier.  Using no LDS, the kernel fits beside the
+// chunked prefill kernel (144 KiB of LDS per CU) on the same CUs: a mixed batch runs its
+// decode rows on a second stream while the prefill chunks run, the HBM-bound state traffic of
+// one hidden under the matrix-core work of the other.  kNT: non-temporal state accesses
+// (state tables larger than the memory-side cache).
+template <bool kNT>
+__global__ __launch_bounds__(64) void wkv7_fp32_step_rows_kernel(Fp32Args p) {
+  const int lane = threadIdx.x, g = lane & 7, q = lane >> 3;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const size_t tok = (size_t)bi * p.C + (size_t)h * kHead;
+  float* S = state_block<true>(p, bi, h);
+  if (S == nullptr) {
+    p.y[tok + lane] = (_Float16)__builtin_nanf("");
+    return;
+  }
+  // token vectors: the lane's 8 columns (4 + 4 fp16, 8-byte loads) and its 8 rows of v
+  typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+  const int c0 = 4 * g, c1 = 32 + 4 * g;
+  auto ld4 = [&](const _Float16* x, int c) { return *reinterpret_cast<const hv4*>(x + tok + c); };
+  const hv4 r0 = ld4(p.r, c0), r1 = ld4(p.r, c1), w0 = ld4(p.w, c0), w1 = ld4(p.w, c1);
+  const hv4 k0 = ld4(p.k, c0), k1 = ld4(p.k, c1), a0 = ld4(p.a, c0), a1 = ld4(p.a, c1);
+  const hv4 b0 = ld4(p.b, c0), b1 = ld4(p.b, c1);
+  const hv8 vv = *reinterpret_cast<const hv8*>(p.v + tok + 8 * q);
+  f4 st[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const f4* src = reinterpret_cast<const f4*>(S + (8 * q + i) * kHead + (hf ? c1 : c0));
+      st[i][hf] = kNT ? __builtin_nontemporal_load(src) : *src;
+    }
+  float rr[8], dd[8], kk[8], aa[8], bb[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    rr[e] = (float)r0[e];
+    rr[4 + e] = (float)r1[e];
+    dd[e] = decay((float)w0[e]);
+    dd[4 + e] = decay((float)w1[e]);
+    kk[e] = (float)k0[e];
+    kk[4 + e] = (float)k1[e];
+    aa[e] = (float)a0[e];
+    aa[4 + e] = (float)a1[e];
+    bb[e] = (float)b0[e];
+    bb[4 + e] = (float)b1[e];
+  }
+  float yv = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float s[8] = {st[i][0].x, st[i][0].y, st[i][0].z, st[i][0].w,
+                  st[i][1].x, st[i][1].y, st[i][1].z, st[i][1].w};
+    float sa = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sa = __builtin_fmaf(s[e], aa[e], sa);
+    sa = sum8(sa);
+    const float vi = (float)vv[i];
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = s[e] * dd[e];
+      x = __builtin_fmaf(sa, bb[e], x);
+      x = __builtin_fmaf(kk[e], vi, x);
+      s[e] = x;
+      acc = __builtin_fmaf(x, rr[e], acc);
+    }
+    acc = sum8(acc);
+    yv = g == i ? acc : yv;  // lane g keeps row 8q + g
+    st[i][0] = f4{s[0], s[1], s[2], s[3]};
+    st[i][1] = f4{s[4], s[5], s[6], s[7]};
+  }
+  p.y[tok + 8 * q + g] = f16_of(yv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      f4* dst = reinterpret_cast<f4*>(S + (8 * q + i) * kHead + (hf ? c1 : c0));
+      if constexpr (kNT) __builtin_nontemporal_store(st[i][hf], dst);
+      else *dst = st[i][hf];
+    }
+}
+
 struct RowsArgs {
   Fp32Args a;
   int vec;  // 16-byte aligned r..b and 8-byte aligned y: vector loads/stores
@@ -1249,6 +1338,32 @@ extern "C" int vkwr_wkv7_fp32_forward_slots(int B, int T, int C, int H, float* p
              reinterpret_cast<_Float16*>(y)};
   launch_fp32<true>(p, B, (hipStream_t)stream, true);
   return check_launch("vkwr_wkv7_fp32_forward_slots");
+}
+
+extern "C" int vkwr_wkv7_fp32_step_rows_slots(int B, int C, int H, float* pool, int n_slots,
+                                              const int32_t* slots, const uint16_t* r, const uint16_t* w,
+                                              const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                              const uint16_t* b, uint16_t* y, void* stream) {
+  clear_error();
+  const char* fn = "vkwr_wkv7_fp32_step_rows_slots";
+  if (int e = check_wkv_dims(fn, B, 1, C, H)) return e;
+  VK_REQUIRE(n_slots >= 0, "%s: negative pool size", fn);
+  if (B == 0 || H == 0) return VKWR_OK;
+  VK_REQUIRE(pool && slots && r && w && k && v && a && b && y, "%s: null pointer", fn);
+  VK_REQUIRE(((uintptr_t)pool | (uintptr_t)v) % 16 == 0 &&
+                 ((uintptr_t)r | (uintptr_t)w | (uintptr_t)k | (uintptr_t)a | (uintptr_t)b) % 8 == 0,
+             "%s: pool and v must be 16-byte aligned, r, w, k, a, b 8-byte aligned", fn);
+  Fp32Args p{1, C, H, n_slots, pool, slots,
+             reinterpret_cast<const _Float16*>(r), reinterpret_cast<const _Float16*>(w),
+             reinterpret_cast<const _Float16*>(k), reinterpret_cast<const _Float16*>(v),
+             reinterpret_cast<const _Float16*>(a), reinterpret_cast<const _Float16*>(b),
+             reinterpret_cast<_Float16*>(y)};
+  const int64_t table = (int64_t)n_slots * H * kHead * kHead * 4;
+  if (table > kMallBytes)
+    hipLaunchKernelGGL(wkv7_fp32_step_rows_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(wkv7_fp32_step_rows_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+  return check_launch(fn);
 }
 
 extern "C" int vkwr_wkv7_decode_fused_f16(int B, int C, int H, float* pool, int n_slots, int state_layout,
