@@ -431,9 +431,12 @@ def serve_mixed_7b(dev, steps, warmup=1):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4),
                      "flops_per_step": gemm_flops(cfg, rows, Bd + Bp)},
-        "gemm_path": "vkwr_gemm_f16 large-M path (256x256x64 MFMA tiles, LDS DMA, split last round), "
-                     "rank-out adapters included (ranks zero-padded to multiples of 64)",
-        "timing": "eager launches, HIP events around the timed steps",
+        "gemm_path": "vkwr_gemm_f16 large-M path (256x256 or 192x256 tiles, k 64 per LDS-DMA stage; last round "
+                     "split in equal k-parts or layered), rank-out adapters included (ranks zero-padded to "
+                     "multiples of 64)",
+        "wkv_path": "prefill chunks: chunked MFMA kernel; decode rows: LDS-free step kernel on a second stream "
+                    "beside it",
+        "timing": "eager launches, HIP events around the timed steps (the side stream joins the timed one)",
     }
 
 
