@@ -503,6 +503,12 @@ def test_layer_norm_shift_rows_matches_ln_then_shift(gpu, C, n_mix, with_res):
     _ln_shift_rows_case(gpu, C, n_mix, with_res, [(5, 1), (2, 7), (1, 2), (1, 1), (3, 4)])
 
 
+def test_layer_norm_shift_rows_more_groups_than_one_launch_takes(gpu):
+    """11 groups: the wrapper splits them over two launches (8 + 3 groups), same bits."""
+    _ln_shift_rows_case(gpu, 256, 6, True, [(2, 1), (1, 3), (1, 2), (2, 2), (1, 5), (3, 1), (1, 4), (1, 6),
+                                            (2, 3), (1, 1), (1, 7)], P=32)
+
+
 def test_layer_norm_shift_rows_bad_slot(gpu):
     """A slot outside the pool: that sequence's rows are NaN, its shift row untouched, the rest exact."""
     _ln_shift_rows_case(gpu, 2048, 6, True, [(4, 1), (2, 5), (1, 3)], bad_group=1)
@@ -521,7 +527,7 @@ def test_layer_norm_shift_rows_errors(gpu):
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(0, 3, 1, sl)])
     with pytest.raises(RuntimeError, match="starts at row"):
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(0, 3, 1, sl), (4, 3, 1, sl)])
-    with pytest.raises(RuntimeError, match="groups"):
+    with pytest.raises(RuntimeError, match="starts at row"):  # split over two launches, still checked
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(r, 1, 1, sl) for r in range(6)] * 2)
     with pytest.raises(RuntimeError, match="n_mix"):
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt, wt], out * 2, pool, [(0, 3, 2, sl)])

@@ -317,12 +317,26 @@ def wkv_state_layout(src, dst, to_layout):
     _check(_wkv_layout(src.numel() // 4096, _ptr(src), _ptr(dst), to_layout, _stream()), "vkwr_wkv7_state_layout_f32")
 
 
+LN_SHIFT_MAX_GROUPS = 8  # groups per vkwr_add_layer_norm_shift_rows_f16 launch
+
+
 def layer_norm_shift_rows(x, weight, bias, x_out, mixes, outs, shift_state, groups, residual=None, eps=1e-5):
     """x_out = x + residual, y = LN(x_out), and per group (row0, B, T, slots [B] int32) the
     token-shift lerps of y into outs against the shift pool shift_state [P, C]: one launch
-    of vkwr_add_layer_norm_shift_rows_f16.  x, residual, x_out, outs [rows, C]."""
+    of vkwr_add_layer_norm_shift_rows_f16 per 8 groups.  x, residual, x_out, outs [rows, C];
+    the groups cover rows 0 .. rows - 1 in order."""
     C = x.shape[-1]
     rows = x.numel() // C
+    if len(groups) > LN_SHIFT_MAX_GROUPS:
+        # one launch per run of 8 groups, on the rows they cover (groups never share a row)
+        for i in range(0, len(groups), LN_SHIFT_MAX_GROUPS):
+            part = groups[i:i + LN_SHIFT_MAX_GROUPS]
+            a = part[0][0]
+            e = part[-1][0] + part[-1][1] * part[-1][2]
+            rb = lambda t: None if t is None else t.view(rows, C)[a:e]  # noqa: E731
+            layer_norm_shift_rows(rb(x), weight, bias, rb(x_out), mixes, [rb(o) for o in outs], shift_state,
+                                  [(r0 - a, B, T, sl) for r0, B, T, sl in part], residual=rb(residual), eps=eps)
+        return
     mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
     gs = (LnShiftGroup * len(groups))(*[LnShiftGroup(r0, B, T, sl.data_ptr()) for r0, B, T, sl in groups])
