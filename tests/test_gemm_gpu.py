@@ -404,6 +404,7 @@ def test_big_gemm_batch_with_empty_problem_and_oracle(gpu):
                            # (144 stages per CU: [0, 144) of every tile, [144, 256) of 112 tiles
                            # whole, the other 32 in 16-stage pieces)
     (2304, 8192, 4096),    # 144 tiles of 128 stages: per 72, layered with 8-stage pieces
+    (4096, 16384, 6400),   # 400 tiles: 256 whole, the other 144 layered (tile indices offset by 256)
     (2304, 4096, 16384),   # the 7B FFN key shape: 2 whole rounds + a 64-tile tail split in 4
 ])
 def test_big_gemm_split_tail(gpu, M, K, N):
