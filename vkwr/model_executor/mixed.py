@@ -142,15 +142,22 @@ class MixedEngine:
                 [gp(s.act[:R], L["value"], s.ffn[:R])]]
         return out
 
-    def _wkv(self, groups, pool, v):
-        """WKV-7 of every group on the slot pool: prefill groups (T > 1) on the current stream,
-        then the decode group (T = 1, row-split order, no LDS) on the side stream, forked after
-        the gate and joined before the GroupNorm, so the decode rows' HBM-bound state traffic
-        runs while the prefill chunks occupy the matrix cores."""
+    def _wkv_gn(self, groups, pool, v, L):
+        """WKV-7 of every group on the slot pool, then the GroupNorm + bonus + gate of its rows:
+        prefill groups (T > 1) on the current stream, the decode group (T = 1, row-split order,
+        no LDS) on the side stream, forked after the gate and joined before the o projection.
+        The decode rows' HBM-bound state traffic runs while the prefill chunks occupy the
+        matrix cores, and each side's GroupNorm runs as soon as its own WKV is done."""
         C, H = self.cfg.n_embd, self.cfg.n_head
         s = self
         args = lambda r0, n: (s.r[r0:r0 + n], s.w[r0:r0 + n], s.new_k[r0:r0 + n], v[r0:r0 + n],  # noqa: E731
                               s.neg_kk[r0:r0 + n], s.kka[r0:r0 + n], s.y[r0:r0 + n])
+
+        def gn(r0, n):
+            sl = slice(r0, r0 + n)
+            capi.groupnorm_bonus_gate(n, 1, C, H, s.y[sl], s.r[sl], s.new_k[sl], v[sl], L["r_k"], L["lnx_w"],
+                                      L["lnx_b"], s.g[sl], s.o_in[sl])
+
         dec = [g for g in groups if g[1] == 1]
         main = torch.cuda.current_stream()
         if dec:
@@ -158,10 +165,12 @@ class MixedEngine:
         for B, T, r0, slots, _ in groups:
             if T > 1:
                 capi.wkv_slots(B, T, C, H, pool, slots, *args(r0, B * T))
+                gn(r0, B * T)
         for B, _, r0, slots, _ in dec:
             s.side.wait_event(s.fork)
             with torch.cuda.stream(s.side):
                 capi.wkv_step_rows_slots(B, C, H, pool, slots, *args(r0, B))
+                gn(r0, B)
             s.join.record(s.side)
             main.wait_event(s.join)
 
@@ -208,9 +217,7 @@ class MixedEngine:
             v = (s.v_first if first else s.v_new)[:R]
             capi.kk_a_gate(R, 1, C, H, s.k[:R], L["k_k"], L["a0"], s.a12[:R], L["k_a"], s.new_k[:R],
                            s.neg_kk[:R], s.kka[:R])
-            self._wkv(groups, state.wkv[l], v)
-            capi.groupnorm_bonus_gate(R, 1, C, H, s.y[:R], s.r[:R], s.new_k[:R], v, L["r_k"], L["lnx_w"],
-                                      L["lnx_b"], s.g[:R], s.o_in[:R])
+            self._wkv_gn(groups, state.wkv[l], v, L)
             capi.gemm([capi.gemm_problem(s.o_in[:R], L["Wo"], s.o[:R])], ws)
             # ---- channel mix
             res2 = s.res[(l + 1) % 2][:R]
