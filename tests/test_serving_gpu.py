@@ -100,6 +100,30 @@ def test_mixed_groups_equal_separate_steps(gpu):
     assert (sa.wkv - sb.wkv).abs().max().item() <= 2e-2
 
 
+def test_mixed_step_with_more_groups_than_one_ln_launch_takes(gpu):
+    """Decode rows plus 9 prefill groups of distinct lengths (10 row groups: the LayerNorm +
+    token-shift launches split at 8 groups) equal the groups stepped one at a time."""
+    from vkwr.model_executor import MixedEngine
+    cfg, model, state = _tiny(gpu, 32)
+    g = torch.Generator().manual_seed(12)
+    dec = (torch.randint(0, cfg.vocab, (3,), generator=g).to(torch.int32).to(gpu), _i32([0, 1, 2], gpu))
+    pre, slot = [], 3
+    for T in (2, 3, 4, 5, 6, 7, 9, 17, 20):
+        B = 1 + T % 2
+        pre.append((torch.randint(0, cfg.vocab, (B, T), generator=g).to(torch.int32).to(gpu),
+                    _i32(list(range(slot, slot + B)), gpu)))
+        slot += B
+    eng = MixedEngine(model, 160, max_seqs=32)
+    sa = _clone(state)
+    both = eng.step(sa, decode=dec, prefill=pre).float().clone()
+    sb = _clone(state)
+    parts = [eng.step(sb, decode=dec).float().clone()] + [eng.step(sb, prefill=[p]).float().clone() for p in pre]
+    assert (both - torch.cat(parts)).abs().max().item() <= TOL
+    assert (sa.wkv - sb.wkv).abs().max().item() <= 2e-2
+    for got, ref in ((sa.att_shift, sb.att_shift), (sa.ffn_shift, sb.ffn_shift)):
+        assert ((got.float() - ref.float()).abs() <= torch.clamp(_ulp16(ref), min=2e-3) * 4).all()
+
+
 def test_scheduler_matches_teacher_forced_replay(gpu):
     """12 requests, prompts 1..23 tokens (chunk 8, so up to three chunks), budgets 1..6 tokens,
     only 5 slots: admission waits for slots, slots are recycled and reset."""
