@@ -419,7 +419,8 @@ typedef struct vkwr_ln_shift_group {
  * (the reference's add_layer_norm_f16 and tmix_mix6 / cmix_mix, csrc/v1/norm/norm_ops.cu
  * and csrc/v1/mix/mix_ops.cu:42-160, run back to back).  The groups cover rows 0 .. rows-1 in
  * order (1..8 of them); C % 8 == 0, C <= 4096; n_mix 1 or 6; every tensor 16-byte aligned;
- * slots distinct across the call.  A slot outside 0 .. n_shift-1 makes its rows' x_out and
+ * slots distinct across the call; x_out and out[] must not overlap x or residual (a row's
+ * lerp reads the previous row, so no update in place; an overlap is rejected).  A slot outside 0 .. n_shift-1 makes its rows' x_out and
  * outputs NaN and leaves the pool untouched.  No counterpart in the reference: it is the
  * mixed step's fusion of those two ops. */
 VKWR_EXPORT int vkwr_add_layer_norm_shift_rows_f16(int64_t rows, int C, const uint16_t* x,

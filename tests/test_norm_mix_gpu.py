@@ -529,5 +529,9 @@ def test_layer_norm_shift_rows_errors(gpu):
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(0, 3, 1, sl), (4, 3, 1, sl)])
     with pytest.raises(RuntimeError, match="starts at row"):  # split over two launches, still checked
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(r, 1, 1, sl) for r in range(6)] * 2)
+    with pytest.raises(RuntimeError, match="must not overlap"):  # in place on the residual
+        capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], out, pool, [(0, 3, 2, sl)], residual=xo)
+    with pytest.raises(RuntimeError, match="must not overlap"):  # an output over x
+        capi.layer_norm_shift_rows(x, wt, bs, xo, [wt], [x], pool, [(0, 3, 2, sl)])
     with pytest.raises(RuntimeError, match="n_mix"):
         capi.layer_norm_shift_rows(x, wt, bs, xo, [wt, wt], out * 2, pool, [(0, 3, 2, sl)])

@@ -208,7 +208,9 @@ class MixedEngine:
         x, res_in = s.x0[:R], None
         for l, L in enumerate(m.layers):
             first = l == 0
-            res = s.res[l % 2][:R]
+            # the LN launches read neighbouring rows of their inputs, so each writes the residual
+            # stream into the buffer it does not read: LN1 into res[1], LN2 into res[0]
+            res = s.res[1][:R]
             # ---- time mix: res = x + res_in, LN1 and the six lerps against the shift pool
             capi.layer_norm_shift_rows(x, L["ln1_w"], L["ln1_b"], res, [L[k] for k in TMIX_MIX],
                                        [t[:R] for t in s.mix], state.att_shift[l], shift_groups, residual=res_in)
@@ -220,7 +222,7 @@ class MixedEngine:
             self._wkv_gn(groups, state.wkv[l], v, L)
             capi.gemm([capi.gemm_problem(s.o_in[:R], L["Wo"], s.o[:R])], ws)
             # ---- channel mix
-            res2 = s.res[(l + 1) % 2][:R]
+            res2 = s.res[0][:R]
             capi.layer_norm_shift_rows(s.o[:R], L["ln2_w"], L["ln2_b"], res2, [L["x_k_ffn"]], [s.xk[:R]],
                                        state.ffn_shift[l], shift_groups, residual=res)
             capi.gemm([capi.gemm_problem(s.xk[:R], L["key"], s.act[:R], epilogue=capi.EPI_RELU_SQUARE)], ws)

@@ -447,6 +447,8 @@ struct LnShiftGroup {
   int64_t r0;
   int B, T;
   const int32_t* slots;
+  int64_t run0;  // runs kernel: the group's first run
+  int rps;       // runs kernel: runs per sequence, ceil(T / kLnRun)
 };
 
 struct LnShiftArgs {
@@ -607,6 +609,168 @@ __global__ __launch_bounds__(kThreads) void ln_shift_rows_kernel(LnShiftArgs p) 
       st8(p.out[i] + dst + c0, o);
     }
     if (t == 0) st8(p.shift + sdst + c0, snew);
+  }
+}
+
+// The same operation over runs of up to kLnRun consecutive rows of one sequence per
+// workgroup (runs never cross a sequence): the LayerNorm weight, bias and mix vectors are
+// loaded once per run instead of once per row, and each row's LayerNorm output is the next
+// row's "previous token" straight from registers, so a run of n rows normalises n + 1 rows
+// (the row before the run, or for the sequence's first run its last row, which goes to the
+// shift pool) instead of 2n.  Each row's arithmetic is the row kernel's, in the same order.
+// Measured at 2304 rows x 4096 (256 decode rows + 4 chunks of 512): 31.1 us with 6 lerps and
+// 16.9 us with 1 (6.1 / 5.6 TB/s), against 34.1 / 20.9 us for the row kernel above (runs of
+// 8 rows: 31.1 / 18.3 us).
+constexpr int kLnRun = 4;
+
+template <int NV, int NMIX>
+__global__ __launch_bounds__(kThreads) void ln_shift_runs_kernel(LnShiftArgs p) {
+  __shared__ float red[2][2][kWaves];  // [row parity][statistics pass]
+  const int64_t run = blockIdx.x;
+  const int tid = threadIdx.x, C = p.C;
+  int gi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxShiftGroups; ++i)
+    if (i < p.n_groups && run >= p.g[i].run0) gi = i;
+  const LnShiftGroup& G = p.g[gi];
+  const int T = G.T;
+  const int64_t local = run - G.run0;
+  const int b = (int)(local / G.rps);
+  const int t0 = (int)(local - (int64_t)b * G.rps) * kLnRun, t1 = min(T, t0 + kLnRun);
+  const int64_t seq0 = G.r0 + (int64_t)b * T;  // the sequence's row 0
+  const int64_t slot = G.slots[b];
+  auto col = [&](int n) {
+    const int c = (tid + n * kThreads) * 8;
+    return c < C ? c : C - 8;
+  };
+  if (slot < 0 || slot >= p.n_shift) {
+    // A slot outside the pool: the run's outputs are NaN and no shift row is touched.
+    const _Float16 nan = (_Float16)__builtin_nanf("");
+    for (int t = t0; t < t1; ++t)
+      for (int c = tid; c < C; c += kThreads) {
+        const int64_t o = (seq0 + t) * (int64_t)C + c;
+        p.x_out[o] = nan;
+#pragma unroll
+        for (int i = 0; i < NMIX; ++i) p.out[i][o] = nan;
+      }
+    return;
+  }
+  const int64_t sdst = slot * (int64_t)C;
+  h8 wp[NV], bp[NV], mp[NV][NMIX], prev[NV];
+  h8 xa[NV], ra[NV];  // raw x / residual of the row being loaded
+  auto load_row = [&](int64_t row) __attribute__((always_inline)) {
+    const int64_t o = row * (int64_t)C;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      xa[n] = ld8(p.x + o + col(n));
+      if (p.residual) ra[n] = ld8(p.residual + o + col(n));
+    }
+  };
+  // LayerNorm of the loaded row (the row kernel's arithmetic and order): y and x + residual
+  auto ln_row = [&](float* rd, h8 (&y)[NV], h8 (&xo)[NV]) __attribute__((always_inline)) {
+    float v[NV][8], sum = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const bool in = (tid + n * kThreads) * 8 < C;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[n][e] = (float)xa[n].v[e];
+      if (p.residual) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[n][e] = v[n][e] + (float)ra[n].v[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += in ? v[n][e] : 0.0f;
+    }
+    const float mean = block_sum_ln<kWaves>(sum, rd) / (float)C;
+    float ss = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      if ((tid + n * kThreads) * 8 < C) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[n][e] - mean;
+          ss = __builtin_fmaf(d, d, ss);
+        }
+      }
+    }
+    const float rstd = rsqrtf(block_sum_ln<kWaves>(ss, rd + kWaves) / (float)C + p.eps);
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[n].v[e] = f16_of(__builtin_fmaf((v[n][e] - mean) * rstd, (float)wp[n].v[e], (float)bp[n].v[e]));
+        xo[n].v[e] = (_Float16)v[n][e];
+      }
+  };
+  // parameters, and the first row's (or the row before the run's) inputs
+  const bool first = t0 == 0;
+  load_row(first ? seq0 : seq0 + t0 - 1);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    wp[n] = ld8(p.weight + col(n));
+    bp[n] = ld8(p.bias + col(n));
+#pragma unroll
+    for (int i = 0; i < NMIX; ++i) mp[n][i] = ld8(p.mix[i] + col(n));
+    if (first) prev[n] = ld8(p.shift + sdst + col(n));
+  }
+  h8 y[NV], xo[NV];
+  int par = 0;
+  if (!first) {
+    ln_row(&red[par][0][0], prev, xo);  // the row before the run: only its y is used
+    par ^= 1;
+    load_row(seq0 + t0);
+  }
+#pragma unroll 1
+  for (int t = t0; t < t1; ++t) {
+    // keep the parameters in fp16 registers: converted once outside the loop they would
+    // double their register count
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      u4 wu = __builtin_bit_cast(u4, wp[n]), bu = __builtin_bit_cast(u4, bp[n]);
+      asm volatile("" : "+v"(wu), "+v"(bu));
+      wp[n] = __builtin_bit_cast(h8, wu);
+      bp[n] = __builtin_bit_cast(h8, bu);
+#pragma unroll
+      for (int i = 0; i < NMIX; ++i) {
+        u4 mu = __builtin_bit_cast(u4, mp[n][i]);
+        asm volatile("" : "+v"(mu));
+        mp[n][i] = __builtin_bit_cast(h8, mu);
+      }
+    }
+    ln_row(&red[par][0][0], y, xo);
+    par ^= 1;
+    if (t + 1 < t1) load_row(seq0 + t + 1);  // the next row's loads go out before this row's stores
+    const int64_t dst = (seq0 + t) * (int64_t)C;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int c0 = (tid + n * kThreads) * 8;
+      if (c0 >= C) continue;
+      st8(p.x_out + dst + c0, xo[n]);
+#pragma unroll
+      for (int i = 0; i < NMIX; ++i) {
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float yv = (float)y[n].v[e];
+          o.v[e] = f16_of(__builtin_fmaf((float)prev[n].v[e] - yv, (float)mp[n][i].v[e], yv));
+        }
+        st8(p.out[i] + dst + c0, o);
+      }
+      prev[n] = y[n];
+    }
+  }
+  if (first) {
+    // the sequence's last row to the shift pool (this workgroup read the old value above)
+    if (t1 < T) {
+      load_row(seq0 + T - 1);
+      ln_row(&red[par][0][0], y, xo);
+    }
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int c0 = (tid + n * kThreads) * 8;
+      if (c0 < C) st8(p.shift + sdst + c0, y[n]);
+    }
   }
 }
 
@@ -795,14 +959,16 @@ extern "C" int vkwr_add_layer_norm_shift_rows_f16(int64_t rows, int C, const uin
   LnShiftArgs p{};
   p.C = C;
   p.n_groups = n_groups;
-  int64_t r = 0;
+  int64_t r = 0, runs = 0;
   for (int i = 0; i < n_groups; ++i) {
     const vkwr_ln_shift_group& g = groups[i];
     VK_REQUIRE(g.row0 == r, "%s: group %d starts at row %lld, expected %lld", fn, i, (long long)g.row0,
                (long long)r);
     VK_REQUIRE(g.B >= 1 && g.T >= 1 && g.slots, "%s: group %d needs B >= 1, T >= 1 and slots", fn, i);
-    p.g[i] = LnShiftGroup{g.row0, g.B, g.T, g.slots};
+    const int rps = (g.T + kLnRun - 1) / kLnRun;
+    p.g[i] = LnShiftGroup{g.row0, g.B, g.T, g.slots, runs, rps};
     r += (int64_t)g.B * g.T;
+    runs += (int64_t)g.B * rps;
   }
   VK_REQUIRE(r == rows, "%s: the groups cover %lld rows, not %lld", fn, (long long)r, (long long)rows);
   if (rows == 0) return VKWR_OK;
@@ -824,14 +990,23 @@ extern "C" int vkwr_add_layer_norm_shift_rows_f16(int64_t rows, int C, const uin
     vec = vec && aligned16(mix[i]) && aligned16(out[i]);
   }
   VK_REQUIRE(vec, "%s: every tensor must be 16-byte aligned", fn);
-  const dim3 grid((unsigned)rows), block(kThreads);
+  // a workgroup reads rows of x and residual that other workgroups own: no output may overlap them
+  const int64_t span = rows * (int64_t)C * 2;
+  auto overlap = [&](const void* o, const void* i) {
+    const uintptr_t a = (uintptr_t)o, b = (uintptr_t)i;
+    return i != nullptr && a < b + span && b < a + span;
+  };
+  bool alias = overlap(x_out, x) || overlap(x_out, residual);
+  for (int i = 0; i < n_mix; ++i) alias = alias || overlap(out[i], x) || overlap(out[i], residual);
+  VK_REQUIRE(!alias, "%s: x_out and out[] must not overlap x or residual (rows are read across workgroups)", fn);
+  const dim3 grid((unsigned)runs), block(kThreads);
   const bool one = C <= 8 * kThreads;
   if (n_mix == 1) {
-    if (one) hipLaunchKernelGGL((ln_shift_rows_kernel<1, 1>), grid, block, 0, (hipStream_t)stream, p);
-    else hipLaunchKernelGGL((ln_shift_rows_kernel<2, 1>), grid, block, 0, (hipStream_t)stream, p);
+    if (one) hipLaunchKernelGGL((ln_shift_runs_kernel<1, 1>), grid, block, 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((ln_shift_runs_kernel<2, 1>), grid, block, 0, (hipStream_t)stream, p);
   } else {
-    if (one) hipLaunchKernelGGL((ln_shift_rows_kernel<1, 6>), grid, block, 0, (hipStream_t)stream, p);
-    else hipLaunchKernelGGL((ln_shift_rows_kernel<2, 6>), grid, block, 0, (hipStream_t)stream, p);
+    if (one) hipLaunchKernelGGL((ln_shift_runs_kernel<1, 6>), grid, block, 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((ln_shift_runs_kernel<2, 6>), grid, block, 0, (hipStream_t)stream, p);
   }
   return check_launch(fn);
 }
