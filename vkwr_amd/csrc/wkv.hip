@@ -622,14 +622,17 @@ __global__ __launch_bounds__(256) void wkv7_fp32_rows_kernel(RowsArgs ra) {
 // multiplicative DPP scan over the 16 lanes that hold one channel quad's tokens), chunk
 // c + 2's four L x L matrices and chunk c + 1's W^T from its N (described at the kernel).
 // Per chunk: 80 MFMAs on each state wave, 116 / 112 / 96 / 96 on the four SIMDs.  Measured
-// at config 2: 0.20 ms per call against 0.24 ms for the form with four waves, each running
-// all three stages for its own rows (132 MFMAs per wave, W^T computed four times).  The
-// matrix core and the vector ALU of a SIMD do not overlap across its two waves on gfx950
-// (a loop of MFMAs on one wave beside a loop of FMAs on the other takes the sum of both
-// times), so the split gains from moving the redundant W^T work out and from the second
-// wave filling dependency stalls, not from concurrent execution.  (W^T by forward
-// substitution on the vector ALU measured 5 % slower; back substitution of Z on the state
-// waves 25 % slower.)
+// at config 2: 0.174 ms per call (0.24 ms for the form with four waves, each running all
+// three stages for its own rows: 132 MFMAs per wave, W^T computed four times).  The matrix
+// core and the vector ALU of a SIMD do not overlap across its two waves on gfx950 (a loop of
+// MFMAs on one wave beside a loop of FMAs on the other takes the sum of both times), so the
+// split gains from moving the redundant W^T work out and from the second wave filling
+// dependency stalls, not from concurrent execution.  To let it fill them the state waves
+// read their next chunk's operands before the barrier (their chain then starts at once and
+// runs without stalls) and the matrix waves, whose work is dependent chains, issue at a
+// higher priority (0.201 -> 0.174 ms; at equal priority the state wave held the SIMD for its
+// whole chain).  (W^T by forward substitution on the vector ALU measured 5 % slower; back
+// substitution of Z on the state waves 25 % slower.)
 constexpr int kCL = 16;          // tokens per chunk
 constexpr int kChunkMinT = 16;   // shorter prefills take the row-split kernel
 constexpr int kHP = kHead + 4;   // padded LDS row of a [t][j] hat vector (floats)
@@ -702,6 +705,10 @@ __global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
   if (state_wave) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) st[q] = *reinterpret_cast<const fq4*>(S + iw * kHead + 16 * q + 4 * g);
+    // the loads are waited for here: otherwise the loop keeps their waits, which in every
+    // later iteration wait for the previous chunk's y stores before its first products
+#pragma unroll
+    for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(st[q]));
   }
 
   // raw token vectors (matrix waves): piece c = mtid + 256 u is vector c >> 7, token
@@ -815,13 +822,16 @@ __global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
       if (m == 0) L.gramT[b][li][t] = x;
     }
   };
-  // wave 5: N and T_ak; wave 6: T_rb; wave 7: T_rk
+  // wave 5: N and T_ak; wave 6: T_rb; wave 7: T_rk.  Every operand read is issued before the
+  // first product (a scheduling barrier): left to itself the compiler interleaves each pair of
+  // reads with two products and a wait for it, one LDS round trip per two products.
   auto grams = [&](int cc) __attribute__((always_inline)) {
     if (w == 5) {
       fq4 x[4], yb[4], yk[4];
       gram_x(cc, 0, x);
       gram_y(cc, 0, yb);
       gram_y(cc, 1, yk);
+      __builtin_amdgcn_sched_barrier(0);
       const fq4 gn = gram_mfma(x, yb), gk = gram_mfma(x, yk);
       gram_write(cc, 0, gn);
       gram_write(cc, 1, gk);
@@ -829,6 +839,7 @@ __global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
       fq4 x[4], y[4];
       gram_x(cc, 1, x);
       gram_y(cc, w == 6 ? 0 : 1, y);
+      __builtin_amdgcn_sched_barrier(0);
       gram_write(cc, w == 6 ? 2 : 3, gram_mfma(x, y));
     }
   };
@@ -897,29 +908,40 @@ __global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
     load_raw(4 * kCL);
   }
   __syncthreads();
-  for (int c = 0; c < nchunk; ++c) {
-    if (state_wave) {
+  // The state waves' operands of chunk c other than W^T (hat vectors, L x L matrices, Λ_L) are
+  // complete from the start of iteration c - 1 on (hats three chunks ahead, matrices two), so
+  // each iteration reads the next chunk's right after its own products, while the state waves
+  // wait at the barrier for the matrix waves; after the barrier only W^T is read.  (Read at
+  // the start of the iteration, these reads queued up ~100 KiB of LDS traffic in front of the
+  // first product and of the matrix waves' reads.)
+  fq4 a4[4], r4[4], k4[4], b4[4], lamq[4], v4, tak, trb, trk;
+  auto state_operands = [&](int cc) __attribute__((always_inline)) {
+    const int hb = cc & 3, gb = cc % 3;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][0][li][16 * q + 4 * g]);
+      r4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][1][li][16 * q + 4 * g]);
+      k4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][1][16 * q + li][4 * g]);
+    }
+    v4 = *reinterpret_cast<const fq4*>(&L.hatT[hb][2][iw][4 * g]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) b4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][0][16 * q + li][4 * g]);
+    tak = *reinterpret_cast<const fq4*>(&L.gram[gb][1][li][4 * g]);
+    trb = *reinterpret_cast<const fq4*>(&L.gram[gb][2][li][4 * g]);
+    trk = *reinterpret_cast<const fq4*>(&L.gram[gb][3][li][4 * g]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lamq[q] = *reinterpret_cast<const fq4*>(&L.lamL[hb][16 * q + 4 * g]);
+  };
+  // One loop per role, each with the one barrier per chunk (the role is uniform over a wave, so
+  // the two loops' barriers pair up): in a shared loop the state operands, live across the
+  // back edge, also counted against the matrix branch's registers (252 VGPRs instead of 190).
+  if (state_wave) {
+    state_operands(0);
+    for (int c = 0; c < nchunk; ++c) {
       // ---- chunk c against the state:  RHS = Â X0^T + T_ak V;  Y = R̂ X0^T + T_rk V + T_rb Z
       // with Z = W RHS;  X^T += K̂^T V + B̂^T Z;  S^T = diag(Λ_L) X^T
-      const int hb = c & 3, gb = c % 3;
       const int n = min(kCL, T - c * kCL);
       const fq4 wt = L.wt[c & 1][lane];
-      fq4 a4[4], r4[4], k4[4], b4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][0][li][16 * q + 4 * g]);
-        r4[q] = *reinterpret_cast<const fq4*>(&L.hat[hb][1][li][16 * q + 4 * g]);
-        k4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][1][16 * q + li][4 * g]);
-      }
-      const fq4 v4 = *reinterpret_cast<const fq4*>(&L.hatT[hb][2][iw][4 * g]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) b4[q] = *reinterpret_cast<const fq4*>(&L.hatT[hb][0][16 * q + li][4 * g]);
-      const fq4 tak = *reinterpret_cast<const fq4*>(&L.gram[gb][1][li][4 * g]);
-      const fq4 trb = *reinterpret_cast<const fq4*>(&L.gram[gb][2][li][4 * g]);
-      const fq4 trk = *reinterpret_cast<const fq4*>(&L.gram[gb][3][li][4 * g]);
-      fq4 lamq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) lamq[q] = *reinterpret_cast<const fq4*>(&L.lamL[hb][16 * q + 4 * g]);
       __builtin_amdgcn_sched_barrier(0);
       fq4 p1 = {0.0f, 0.0f, 0.0f, 0.0f}, y1 = p1;
 #pragma unroll
@@ -967,7 +989,21 @@ __global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
         for (int r = 0; r < 4; ++r)
           if (4 * g + r < n) yp[(size_t)r * C] = yh[r];
       }
-    } else {
+      // chunk c + 1's operands (past the last chunk: stale buffers, in bounds, never used)
+      __builtin_amdgcn_sched_barrier(0);
+      state_operands(c + 1);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<fq4*>(S + iw * kHead + 16 * q + 4 * g) = st[q];
+  } else {
+    // The matrix waves' work is dependent chains (W^T's powers, LDS round trips, the Λ scans);
+    // at a higher issue priority they go first whenever they can, and the state wave's
+    // products fill their stalls (a SIMD issues one wave's matrix products and the other's
+    // vector instructions in turn, not at once, and at equal priority the older state wave
+    // held the SIMD for its whole chain).
+    __builtin_amdgcn_s_setprio(1);
+    for (int c = 0; c < nchunk; ++c) {
       // ---- chunk c + 3's hat vectors, chunk c + 2's matrices, chunk c + 1's W^T; chunk c + 4's
       // raw vectors into the buffer chunk c + 2's hats were read from (one iteration ago)
       const RawQuad rq = hats_read(c + 3);
@@ -976,12 +1012,8 @@ __global__ __launch_bounds__(512) void wkv7_fp32_chunk_kernel(RowsArgs ra) {
       hats_write(c + 3, rq);
       store_raw(c & 1);
       load_raw((c + 5) * kCL);
+      __syncthreads();
     }
-    __syncthreads();
-  }
-  if (state_wave) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<fq4*>(S + iw * kHead + 16 * q + 4 * g) = st[q];
   }
 }
 
