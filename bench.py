@@ -180,12 +180,14 @@ def model_decode(dev, steps, warmup=3, frag=True, eager=False):
     }
 
 
-def prefill_c2(dev, steps, warmup=2):
+def prefill_c2(dev, steps, warmup=100):
     """WKV-7 prefill, B=8 sequences x T=1024 tokens, H=32, fp32 state
     gathered from / scattered back to random slots of the 512-slot pool in the same call
     (vkwr_v1_wkv::wkv_forward_slots_fp32 -> the chunked prefill kernel).  Inputs drawn as
     in config 0, resident in HBM; eager calls (each is hundreds of microseconds) bracketed
-    by HIP events on the current stream."""
+    by HIP events on the current stream.  100 untimed calls first (~17 ms): the chip's clock
+    ramps over the first ~150 calls from idle (the first 20 took ~12 % longer each than the
+    steady state), which a short warm-up left inside the timed calls."""
     from vkwr._ops.v1 import v1_wkv_ops as ops
 
     Bp, Tp = 8, 1024
