@@ -35,6 +35,14 @@ COLD_SLOTS = 2048  # cold-cache variant: 1 GiB pool
 PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "wkv7_fp32_step_kernel_decode_c1.md")
 
 
+_T0 = time.perf_counter()
+
+
+def log(msg):
+    """Progress on stderr (stdout carries only the JSON line)."""
+    print(f"bench [{time.perf_counter() - _T0:6.1f} s] {msg}", file=sys.stderr, flush=True)
+
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -57,7 +65,9 @@ def parse_args():
                          "skips the cache variants")
     ap.add_argument("--ops-calls", type=int, default=30,
                     help="timed calls per shape of the op-surface GEMMs at M=1 and M=128 (0: skip)")
-    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling", "ops"],
+    ap.add_argument("--fp16-steps", type=int, default=200,
+                    help="steps of the fp16-state WKV decode op at the config-1 shape (0: skip the fp16 section)")
+    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling", "ops", "fp16", "c1"],
                     help="run one section alone and print its JSON object (for profiler runs); with --eager "
                          "the decode steps are launched directly")
     return ap.parse_args()
@@ -117,7 +127,7 @@ def capture(step_fn, n_steps, stream):
     return g
 
 
-def model_decode(dev, steps, warmup=3, frag=True, eager=False):
+def model_decode(dev, steps, warmup=3, frag=True, eager=False, keep_cpu_model=None):
     """the RWKV-7 1.5B-shape decode step (L=24, C=2048, random fp16
     weights) for 128 sequences at T=1 from a 160-slot state pool.  One step is captured
     into a HIP graph and replayed `steps` times (the recurrent state advances every
@@ -161,6 +171,8 @@ def model_decode(dev, steps, warmup=3, frag=True, eager=False):
         torch.cuda.synchronize()
         del graph
     ms = ev0.elapsed_time(ev1) / steps
+    if keep_cpu_model is not None:
+        keep_cpu_model.append(cpu_model_copy(model))
     nbytes = gbytes_per_step(cfg, B)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {
@@ -215,25 +227,135 @@ def prefill_c2(dev, steps, warmup=100):
     ms = ev0.elapsed_time(ev1) / steps
     nbytes = 7 * Bp * Tp * C * 2 + 2 * Bp * H * HEAD * HEAD * 4 + Bp * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    # matrix-core work the chunked kernel issues per 16-token chunk and head: 4 state waves x 80
-    # v_mfma_f32_16x16x4_f32 (2048 flops each), 4 x 16 for the chunk matrices, 36 for W^T
+    # algorithmic flops of the recurrence: per token, head and state element 9 -- the decay
+    # multiply, the two multiply-adds of the update (s*d + sa*b + k*v) and one multiply-add
+    # in each of the two dot products (sa = S a, y = S' r)
+    alg_flops = Bp * Tp * H * HEAD * HEAD * 9
+    # matrix-core work the chunked kernel actually issues per 16-token chunk and head: 4 state
+    # waves x 80 v_mfma_f32_16x16x4_f32 (2048 flops each), 4 x 16 for the chunk matrices, 36 for
+    # W^T (includes the W^T power series and padded tokens, so it is not a roofline numerator)
     mfma_flops = Bp * H * ((Tp + 15) // 16) * (4 * 80 + 4 * 16 + 36) * 2048
     del r, w, k, v, a, b, pool, y
     torch.cuda.empty_cache()
+    tflops = alg_flops / (ms * 1e-3) / 1e12
     return {
         "workload": "WKV-7 prefill (BASELINE config 2): B=8, T=1024, H=32, fp32 state in a 512-slot pool "
                     "(gather + scatter in the call), fp16 inputs drawn as in config 0",
+        "tokens_per_s": round(Bp * Tp / (ms * 1e-3), 1),
+        "hbm_GBps": round(gbs, 2),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_call": nbytes,
         "ms_per_call": round(ms, 4),
         "calls": steps,
-        "tokens_per_s": round(Bp * Tp / (ms * 1e-3), 1),
         "ns_per_token_step": round(ms * 1e6 / Tp, 1),
-        "roofline": {"bound": "mfma (fp32: 16-token chunks, one dependent chain of chunk products per head)",
-                     "achieved": round(mfma_flops / (ms * 1e-3) / 1e12, 2), "peak": 157.3, "unit": "TFLOP/s",
-                     "frac": round(mfma_flops / (ms * 1e-3) / 1e12 / 157.3, 4), "flops_per_call": mfma_flops,
+        "roofline": {"bound": "mfma (fp32 matrix cores: 16-token chunks, one dependent chain of chunk "
+                              "products per head)",
+                     "achieved": round(tflops, 2), "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(tflops / 157.3, 4), "flops_per_call": alg_flops,
+                     "flops": "algorithmic: 9 per token, head and state element",
                      "hbm_GBps": round(gbs, 2), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes},
+        "issued_mfma_util": {"issued_flops_per_call": mfma_flops,
+                             "TFLOP/s": round(mfma_flops / (ms * 1e-3) / 1e12, 2),
+                             "frac_of_fp32_matrix_peak": round(mfma_flops / (ms * 1e-3) / 1e12 / 157.3, 4),
+                             "note": "how busy the chunked form keeps the matrix cores (its own products, "
+                                     "padded tokens and the W^T power series included); not a roofline"},
         "kernel": "wkv7_fp32_chunk_kernel (one 512-lane workgroup per (sequence, head): 4 state waves + 4 "
                   "waves preparing later chunks; 16-token chunks on v_mfma_f32_16x16x4_f32)",
     }
+
+
+def wkv_fp16_family(dev, steps, seq_calls=20, warmup=5):
+    """The fp16-state WKV ops (vkwr_v1_wkv::wkv_one_fp16 / wkv_seq_fp16, fp16 state [B,H,64,64],
+    8 KiB per head; reference csrc/v1/wkv/wkv_fp16_v2.cu).  (1) wkv_one_fp16 at the config-1
+    shape: 128 sequences x 32 heads, T=1, fresh r/w/k/v/a/b per step (config-0
+    distributions), `steps` steps captured into one HIP graph and replayed; also over 32
+    state tables cycled (1 GiB: the state comes from HBM, not the Infinity Cache).
+    (2) wkv_seq_fp16 at the config-2 shape (B=8, T=1024, H=32), eager calls after 100
+    untimed ones.  HIP events on the launch stream."""
+    Bd = B_ACTIVE
+    n = steps + warmup
+    inputs = make_inputs(n, dev, seed=9)
+    g = torch.Generator(device=dev).manual_seed(9)
+    state = (torch.randn(Bd, H, HEAD, HEAD, device=dev, generator=g) * 0.1).half()
+    y = torch.empty(Bd, C, dtype=torch.float16, device=dev)
+    el = torch.zeros(Bd, dtype=torch.int32, device=dev)
+    op = torch.ops.vkwr_v1_wkv.wkv_one_fp16
+
+    def step(i, st=state):
+        x = inputs[i]
+        op(Bd, C, H, st, x[0].view(Bd, C), x[1].view(Bd, C), x[2].view(Bd, C), x[3].view(Bd, C),
+           x[4].view(Bd, C), x[5].view(Bd, C), y, el)
+
+    for i in range(warmup):
+        step(steps + i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed_graph(fn, k):
+        gr = capture(fn, k, stream)
+        gr.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            gr.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        del gr
+        return ev0.elapsed_time(ev1) / k
+
+    ms_hot = timed_graph(step, steps)
+    tables = torch.empty(32, Bd, H, HEAD, HEAD, dtype=torch.float16, device=dev).normal_(0.0, 0.1)
+    ms_cold = timed_graph(lambda i: step(i, tables[i % 32]), steps)
+    del tables, inputs
+    one_bytes = 2 * Bd * H * HEAD * HEAD * 2 + 7 * Bd * C * 2 + Bd * 4
+    out = {"wkv_one_fp16_c1_shape": {
+        "ms_per_step": round(ms_hot, 5), "tokens_per_s": round(Bd / (ms_hot * 1e-3), 1),
+        "GB/s": round(one_bytes / (ms_hot * 1e-3) / 1e9, 2),
+        "hbm_frac": round(one_bytes / (ms_hot * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_step": one_bytes,
+        "cold_32_tables": {"ms_per_step": round(ms_cold, 5),
+                           "GB/s": round(one_bytes / (ms_cold * 1e-3) / 1e9, 2),
+                           "hbm_frac": round(one_bytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "workload": "128 sequences x 32 heads, T=1, fp16 state 32 MiB (read + written), fresh fp16 inputs "
+                    "per step; cold: 32 state tables (1 GiB) cycled"}}
+    # (2) prefill at the config-2 shape
+    Bp, Tp = 8, 1024
+    shp = (Bp, Tp, C)
+    r, k, v = (torch.randn(shp, device=dev, generator=g).half() for _ in range(3))
+    w = torch.exp(-0.6065 * torch.sigmoid(torch.randn(shp, device=dev, generator=g))).half()
+    kk = torch.nn.functional.normalize(k.float().view(Bp, Tp, H, HEAD), dim=-1)
+    a = (-kk).reshape(shp).half()
+    b = (kk * torch.sigmoid(torch.randn(Bp, Tp, H, HEAD, device=dev, generator=g))).reshape(shp).half()
+    st = (torch.randn(Bp, H, HEAD, HEAD, device=dev, generator=g) * 0.1).half()
+    yp = torch.empty(shp, dtype=torch.float16, device=dev)
+    elp = torch.zeros(Bp, dtype=torch.int32, device=dev)
+    call = lambda: torch.ops.vkwr_v1_wkv.wkv_seq_fp16(Bp, Tp, C, H, st, r, w, k, v, a, b, yp, elp)  # noqa: E731
+    for _ in range(100):
+        call()
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(seq_calls):
+        call()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / seq_calls
+    seq_bytes = 7 * Bp * Tp * C * 2 + 2 * Bp * H * HEAD * HEAD * 2 + Bp * 4
+    flops = Bp * Tp * H * HEAD * HEAD * 9
+    out["wkv_seq_fp16_c2_shape"] = {
+        "ms_per_call": round(ms, 4), "tokens_per_s": round(Bp * Tp / (ms * 1e-3), 1),
+        "ns_per_token_step": round(ms * 1e6 / Tp, 1),
+        "GB/s": round(seq_bytes / (ms * 1e-3) / 1e9, 2),
+        "hbm_frac": round(seq_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "fp16_TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+        "calls": seq_calls,
+        "workload": "B=8, T=1024, H=32, fp16 state, inputs drawn as in config 0; 256 (sequence, head) "
+                    "chains of 1024 dependent tokens (latency-bound: 256 waves on 256 CUs)"}
+    del r, w, k, v, a, b, st, yp
+    torch.cuda.empty_cache()
+    out["kernel"] = "wkv7_fp16_kernel<false> (vkwr_amd/csrc/wkv.hip): one wave64 per (sequence, head)"
+    out["timing"] = "decode: HIP graph of the steps, HIP events on the replay stream; prefill: eager calls"
+    return out
 
 
 def sampling_bs128(dev, calls, warmup=3):
@@ -443,7 +565,7 @@ def serve_mixed_7b(dev, steps, warmup=1):
 
 
 def cpu_baseline(target_s):
-    """Oracle (C restatement, OpenMP over heads) on the host cores, bounded sample."""
+    """Config 1 on the host cores: the oracle (C restatement, OpenMP over heads), bounded sample."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -473,6 +595,88 @@ def cpu_baseline(target_s):
     }
 
 
+def cpu_baseline_prefill(reps=5):
+    """Config 2 on the host cores: the C oracle (OpenMP over the 256 (sequence, head) chains),
+    B=8 x T=1024 x H=32 through the slot-pool entry (gather, 1024 tokens, scatter) on a
+    512-slot pool, inputs drawn as in config 0; one untimed call, then the median of `reps`."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    from tests.wkv_inputs import make_state, make_wkv_inputs
+
+    Bp, Tp = 8, 1024
+    cores = len(os.sched_getaffinity(0))
+    orc.set_threads(cores)
+    pool = make_state(P_SLOTS, H, seed=2)
+    slots = np.random.default_rng(2).permutation(P_SLOTS)[:Bp]
+    ins = make_wkv_inputs(Bp, Tp, H, seed=2)
+    orc.wkv_fp32_slots(Bp, Tp, C, H, pool, slots, *ins)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        orc.wkv_fp32_slots(Bp, Tp, C, H, pool, slots, *ins)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    nbytes = 7 * Bp * Tp * C * 2 + 2 * Bp * H * HEAD * HEAD * 4 + Bp * 4
+    return {
+        "value": round(Bp * Tp / t, 1),
+        "unit": "tokens/s",
+        "GB/s": round(nbytes / t / 1e9, 3),
+        "cores": cores,
+        "kind": "port",
+        "sample": f"config 2 whole (B=8, T=1024, H=32, one call = 8192 tokens), median of {reps} calls "
+                  f"after one untimed: {t * 1e3:.1f} ms/call",
+    }
+
+
+def cpu_model_copy(model):
+    """The decode model's weights as float32 host tensors, in the shape the float32
+    composition (oracle.model_ref.decode_step) reads."""
+    import types
+
+    f = lambda t: t.float().cpu()  # noqa: E731
+    return types.SimpleNamespace(cfg=model.cfg, layers=[{k: f(v) for k, v in L.items()} for L in model.layers],
+                                 emb=f(model.emb), ln_out_w=f(model.ln_out_w), ln_out_b=f(model.ln_out_b),
+                                 head=f(model.head))
+
+
+def cpu_baseline_decode(cpu_model, steps=3):
+    """Config 3 on the host cores: the float32 torch composition of the restated ops
+    (oracle.model_ref.decode_step, round_fp16=False) for 128 sequences at T=1, weights and
+    states in host memory, torch.set_num_threads(cores); one untimed step, then the median
+    of `steps`."""
+    from oracle import model_ref
+
+    cfg = cpu_model.cfg
+    B = 128
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(7)
+    wkv = torch.randn(cfg.n_layer, B, cfg.n_head, HEAD, HEAD, generator=g) * 0.1
+    att = torch.zeros(cfg.n_layer, B, cfg.n_embd)
+    ffn = torch.zeros(cfg.n_layer, B, cfg.n_embd)
+    tokens = torch.randint(0, cfg.vocab, (B,), generator=g)
+    slots = torch.arange(B)
+    times = []
+    with torch.no_grad():
+        for i in range(steps + 1):
+            t0 = time.perf_counter()
+            model_ref.decode_step(cpu_model, wkv, att, ffn, tokens, slots, round_fp16=False)
+            if i:
+                times.append(time.perf_counter() - t0)
+    torch.set_num_threads(prev)
+    t = sorted(times)[len(times) // 2]
+    return {
+        "value": round(B / t, 1),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"config 3 (1.5B shape, bs=128, T=1): {steps} float32 decode steps on the host after one "
+                  f"untimed, median {t * 1e3:.0f} ms/step (torch CPU, {cores} threads)",
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -485,12 +689,18 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.only:
-        copy_calibration(dev)  # a reference dispatch of known size for counter runs
         run = {"decode": lambda: model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm, eager=args.eager),
                "prefill": lambda: prefill_c2(dev, args.prefill_calls),
                "serve": lambda: serve_mixed_7b(dev, args.serve_steps),
                "sampling": lambda: sampling_bs128(dev, args.sampling_calls),
-               "ops": lambda: ops_small_m(dev, args.ops_calls)}[args.only]
+               "ops": lambda: ops_small_m(dev, args.ops_calls),
+               "fp16": lambda: wkv_fp16_family(dev, args.fp16_steps)}.get(args.only)
+        if run is None:  # "c1": the config-1 step alone (the sections below are skipped)
+            args.model_steps = args.prefill_calls = args.serve_steps = 0
+            args.sampling_calls = args.ops_calls = args.fp16_steps = 0
+            args.no_cpu_baseline = True
+    if args.only and args.only != "c1":
+        copy_calibration(dev)  # a reference dispatch of known size for counter runs
         print(json.dumps({args.only: run()}), flush=True)
         return
     K, W = args.steps, args.warmup
@@ -592,9 +802,11 @@ def main():
                                       "cycled (torch copy_ / mul_)"}
         del src, dst
     variants["wall_s_timed_region"] = round(wall, 4)
+    log("config 1 decode step done")
     gbs = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
 
     traffic = read_traffic()
+    cold = variants.get("cold_1GiB_pool")
     result = {
         "metric": "WKV-7 decode HBM GB/s (% peak); decode tokens/s at 1.5B-shape bs=128",
         "value": round(gbs, 2),
@@ -614,25 +826,51 @@ def main():
         "tokens_per_s": round(B_ACTIVE / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": STEP_BYTES},
+                     "bytes_per_launch": STEP_BYTES,
+                     "frac_cold_1GiB_pool": cold["frac_of_peak"] if cold else None,
+                     "note": "frac: the config as specified, whose 64 MiB of active state stays in the 256 MB "
+                             "Infinity Cache between steps; frac_cold_1GiB_pool: the same step over a 1 GiB pool "
+                             "whose every step's state comes from HBM. traffic: FETCH_SIZE + WRITE_SIZE bytes per "
+                             "launch (rocprofv3, scaled by a plain copy of known size); these count L2-to-fabric "
+                             "requests, Infinity Cache hits included, so they show no re-reads, not HBM bytes"},
         "variants": variants,
         "cpu_baseline": None,
     }
+    keep = [] if not args.no_cpu_baseline else None
     if args.model_steps > 0 and not args.eager:
         del inputs
         torch.cuda.empty_cache()
-        result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm)
+        result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm,
+                                                   keep_cpu_model=keep)
         torch.cuda.empty_cache()
+        log("config 3 decode step done")
     if args.prefill_calls > 0 and not args.eager:
         result["prefill_c2"] = prefill_c2(dev, args.prefill_calls)
+        log("config 2 prefill done")
+    if args.fp16_steps > 0 and not args.eager:
+        result["wkv_fp16_family"] = wkv_fp16_family(dev, args.fp16_steps)
+        log("fp16-state WKV done")
     if args.serve_steps > 0 and not args.eager:
         result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
+        log("config 4 mixed step done")
     if args.sampling_calls > 0 and not args.eager:
         result["sampling_bs128"] = sampling_bs128(dev, args.sampling_calls)
+        log("sampling done")
     if args.ops_calls > 0 and not args.eager:
         result["ops_small_m"] = ops_small_m(dev, args.ops_calls)
+        log("op-surface GEMMs done")
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        cb = cpu_baseline(args.cpu_seconds)
+        log("CPU baseline, config 1 done")
+        per = {"config1_decode_step": dict(cb)}
+        if "prefill_c2" in result:
+            per["config2_prefill"] = result["prefill_c2"]["cpu_baseline"] = cpu_baseline_prefill()
+            log("CPU baseline, config 2 done")
+        if keep:
+            per["config3_decode_1p5b"] = result["decode_1p5b_bs128"]["cpu_baseline"] = \
+                cpu_baseline_decode(keep.pop())
+        cb["per_config"] = per
+        result["cpu_baseline"] = cb
     print(json.dumps(result), flush=True)
 
 

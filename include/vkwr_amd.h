@@ -362,7 +362,10 @@ VKWR_EXPORT int vkwr_gemm_f16(int n_problems, const vkwr_gemm_problem* problems,
  * that is rejected with VKWR_ERR_INVALID before any GPU work; every GEMM batch of the
  * 1.5B-shape decode step (C = 2048) at up to 256 rows fits.  It calls no hipMalloc / hipFree.  Calls that overlap on
  * one device (concurrent streams, or host threads) share that device's scratch and race:
- * serialise them.  The first call on a device looks the array's device address up once.
+ * serialise them.  The first call on a device looks the array's device address up once
+ * (hipGetSymbolAddress): make one call on each device before capturing it into a HIP graph
+ * -- any call does, even a batch of one empty problem (m = 0); captured calls then only
+ * enqueue kernels.
  * No counterpart in the reference: it is for callers that cannot allocate device memory,
  * e.g. code under HIP graph capture, tight serving loops, or harnesses that forbid it. */
 VKWR_EXPORT int vkwr_gemm_f16_noalloc(int n_problems, const vkwr_gemm_problem* problems, void* stream);

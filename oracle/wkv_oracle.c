@@ -272,8 +272,11 @@ void oracle_wkv_fp32(int B, int T, int C, int H, float* state,
   wkv_fp32_impl(B, T, C, H, state, r, w, k, v, a, b, y, 0);
 }
 
-/* Row-split order (row_dot order 1): this build's prefill path (mode 0 and the
- * slot-pool entry point at T > 1). */
+/* Row-split order (row_dot order 1): this build's row-split kernels -- mode 0 and
+ * the slot-pool entry point at 1 < T < 16, and the mixed step's LDS-free decode
+ * kernel.  At T >= 16 mode 0 and the slot-pool entry point take the chunked
+ * (16-token block) kernel, which no order here reproduces bit for bit: its
+ * tests compare it with the row-per-thread order within a stated tolerance. */
 void oracle_wkv_fp32_rows(int B, int T, int C, int H, float* state,
                           const uint16_t* r, const uint16_t* w, const uint16_t* k,
                           const uint16_t* v, const uint16_t* a, const uint16_t* b,

@@ -343,12 +343,16 @@ def test_fp32_orders_agree_within_tolerance_and_differ_in_bits():
 
 def test_fp32_orders_at_config0_meet_north_star_bounds():
     """BASELINE config 0 exactly (B=2, T=128, H=12, zero state, seed 0): the row-split order
-    that wkv_forward_fp32 (mode 0) takes at T > 1, against the row-per-lane order of the
-    reference's mode-0 kernel at this size (wkv_fp32_v2.cu:79-124, chosen by use_small_auto
-    :212-226): y within max-abs 2e-2 / mean-rel 5e-3, final state within 1e-3.  Measured:
-    max-abs 0.015625 (one ulp at |y| in [16, 32)), mean-rel 1.6e-7, 223 of 196608 outputs
-    differ, state max-abs 9.5e-7.  (Where y is small through cancellation the two fp32 sums
-    can be several fp16 ulps of y apart; the bound is absolute.)"""
+    (the order of wkv_forward_fp32, mode 0, at 1 < T < 16, and of the mixed step's decode
+    kernel) against the row-per-lane order of the reference's mode-0 kernel at this size
+    (wkv_fp32_v2.cu:79-124, chosen by use_small_auto :212-226), both in the oracle: y within
+    max-abs 2e-2 / mean-rel 5e-3, final state within 1e-3.  Measured: max-abs 0.015625 (one
+    ulp at |y| in [16, 32)), mean-rel 1.6e-7, 223 of 196608 outputs differ, state max-abs
+    9.5e-7.  (Where y is small through cancellation the two fp32 sums can be several fp16
+    ulps of y apart; the bound is absolute.)  At config 0's T = 128 the GPU's mode 0 takes
+    the chunked kernel, not the row-split one: that kernel's y is within 2e-2 where |y| < 32
+    and within one fp16 ulp above (0.03125 at config 0: 281 of 196608 values off, mean-rel
+    1.9e-7), checked on the GPU in tests/test_wkv_gpu.py."""
     B, T, H = 2, 128, 12
     C = H * 64
     ins = make_wkv_inputs(B, T, H, seed=0, dist="baseline")

@@ -6,9 +6,12 @@ The token-by-token kernels perform the oracle's IEEE operations in the oracle's
 order, so their tests demand (and report) bit equality, which implies those
 tolerances.  The chunked prefill kernel (T >= 16 through mode 0 and the slot op)
 computes the same recurrence as products of 16-token blocks on the matrix cores:
-its results are checked against the reference-order oracle at the stated
-tolerances, plus a much tighter one that a wrong term would break (the two
-agree to fp32 rounding: mean-relative y error ~1e-7).
+its results are checked against the reference-order oracle: y within max-abs
+2e-2 wherever |y| < 32 and within one fp16 ulp where |y| >= 32 (there one ulp,
+2^-5 or more, exceeds 2e-2 -- a stated departure from the literal bound for
+those values), mean-rel <= 2e-6, at most 0.3 % of values off at all, and the
+state within 1e-3 and 2e-5 of its largest value (the two agree to fp32
+rounding).  wkv_forward_seq_fp32 is the bit-exact path in the reference order.
 Also restated: the reference's own WKV unit tests
 (reference tests/ops/test_v1_wkv_ops.py:161-466).
 """
@@ -53,22 +56,36 @@ def _check_state(s_gpu, s_ref, what):
 
 
 CHUNK_MIN_T = 16           # mode 0 / slot op prefills of at least this many tokens run chunked
-CHUNK_Y_MEAN_REL = 2e-6    # chunked vs reference order: fp32 rounding only (measured ~1e-7)
+CHUNK_Y_MEAN_REL = 2e-6    # chunked vs reference order: fp32 rounding only (measured ~2e-7)
 CHUNK_STATE_REL = 2e-5     # ... max |dS| / max |S|
+CHUNK_ULP_FRAC = 3e-3      # ... at most this fraction of y values one fp16 ulp or more off
+BIG_Y = 32.0               # |y| from which one fp16 ulp (2^-5) exceeds the 2e-2 max-abs bound
 
 
 def _check_y_chunked(y_gpu, y_ref, what):
-    """north_star tolerances (max-abs 2e-2, or one fp16 ulp where |y| >= 32 and one ulp exceeds
-    it; mean-rel 5e-3) and the chunked form's own bound (mean-rel CHUNK_Y_MEAN_REL).  Returns
-    (max-abs, mean-rel, number of y values that differ by >= 1 fp16 ulp)."""
+    """The chunked kernel's y contract against the reference-order oracle.
+
+    Every y with |y_ref| < 32 is within north_star's literal max-abs 2e-2.  Where |y_ref| >= 32
+    one fp16 ulp (2^-5 or more) is itself larger than 2e-2, and any kernel whose fp32 sums are
+    not in the reference's order may round such a y to the neighbouring fp16 value: there the
+    bound is one ulp.  This is a deliberate departure from the literal north_star bound for
+    those values only; wkv_forward_seq_fp32 (and modes 2-3) keep the reference order and are
+    bit-exact.  Mean-relative error <= 2e-6 (north_star: 5e-3), and at most 0.3 % of the
+    values may differ from the oracle at all (measured: 0.14 % at config 0, 0.16 % at config 2).
+    Returns (max-abs, mean-rel, number of y values that differ by >= 1 fp16 ulp)."""
     yg = y_gpu.detach().cpu().numpy().astype(np.float64)
     yr = y_ref.astype(np.float64)
     err = np.abs(yg - yr)
+    big = np.abs(yr) >= BIG_Y
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(yr), 2.0 ** -14))) - 10)
     mean_rel = err.sum() / max(np.abs(yr).sum(), 1e-30)
-    assert (err <= np.maximum(ulp, Y_MAX_ABS)).all() and mean_rel <= Y_MEAN_REL, (what, err.max(), mean_rel)
+    small_err = float(err[~big].max()) if (~big).any() else 0.0
+    assert small_err <= Y_MAX_ABS, (what, "|y| < 32 beyond 2e-2", small_err)
+    assert (err[big] <= ulp[big]).all(), (what, "|y| >= 32 beyond one fp16 ulp", float(err[big].max()))
     assert mean_rel <= CHUNK_Y_MEAN_REL, (what, "chunked y off the recurrence", mean_rel)
-    return float(err.max()), float(mean_rel), int((yg != yr).sum())
+    n_off = int((yg != yr).sum())
+    assert n_off <= CHUNK_ULP_FRAC * yr.size, (what, "too many y values off the oracle", n_off, yr.size)
+    return float(err.max()), float(mean_rel), n_off
 
 
 def _check_state_chunked(s_gpu, s_ref, what):
@@ -275,6 +292,33 @@ def test_prefill_config2_reduced_matches_oracle(gpu):
     _check_state_chunked(pool[slots_np.tolist()], pool_np[slots_np], "prefill pool")
     others = [i for i in range(P) if i not in slots_np.tolist()]
     assert np.array_equal(pool[others].cpu().numpy(), pool_np[others])
+
+
+def test_prefill_config2_full_matches_oracle(gpu):
+    """BASELINE config 2 at full size (B=8, T=1024, H=32, inputs drawn as in config 0, state
+    ~ N(0, 0.1) gathered from 8 random slots of a 512-slot pool and scattered back) through
+    the slot op (the chunked kernel) against the C oracle in the reference order, at the
+    chunked kernel's contract; the 504 slots no sequence names stay bitwise."""
+    from vkwr._ops.v1 import v1_wkv_ops as ops
+
+    P, B, T, H = 512, 8, 1024, 32
+    C = H * 64
+    pool_np = make_state(P, H, seed=7)
+    slots_np = np.random.default_rng(7).permutation(P)[:B].astype(np.int32)
+    ins = make_wkv_inputs(B, T, H, seed=7)
+    pool = torch.from_numpy(pool_np).to(gpu)
+    y = ops.wkv_forward_slots_fp32(B, T, C, H, pool, torch.from_numpy(slots_np).to(gpu), *_dev(ins, gpu))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    y_ref = orc.wkv_fp32_slots(B, T, C, H, pool_np, slots_np.astype(np.int64), *ins, order="seq")
+    t_or = time.perf_counter() - t0
+    mx, mr, nulp = _check_y_chunked(y, y_ref, "config 2 full")
+    print(f"config 2 full (oracle {t_or:.1f} s): y max-abs {mx:.3g} mean-rel {mr:.3g} "
+          f">=1-ulp {nulp}/{y_ref.size}", flush=True)
+    got = pool.cpu().numpy()
+    _check_state_chunked(torch.from_numpy(got[slots_np]), pool_np[slots_np], "config 2 pool")
+    others = np.setdiff1d(np.arange(P), slots_np)
+    assert np.array_equal(got[others], pool_np[others])
 
 
 def _config2_inputs(gpu, B, T, H, seed=5):

@@ -78,3 +78,39 @@ def test_noalloc_rejects_batches_beyond_its_scratch(gpu):
         _run_noalloc(probs)
     torch.cuda.synchronize()
     assert torch.isnan(outs[0]).all()
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """The use the header names: one uncaptured call first (a batch of one empty problem,
+    which performs the per-device address lookup), then a K-split batch captured into a
+    HIP graph and replayed three times, with eager work and synchronisation between the
+    replays; every replay must equal vkwr_gemm_f16 with a workspace bit for bit."""
+    empty = capi.gemm_problem(torch.empty(0, 64, dtype=torch.float16, device=gpu),
+                              torch.empty(64, 64, dtype=torch.float16, device=gpu),
+                              torch.empty(0, 64, dtype=torch.float16, device=gpu))
+    _run_noalloc([empty])
+    probs, outs, keep = _batch(gpu, 128, 1024, 8192, seed=21, nprob=2)
+    assert 0 < capi.gemm_workspace_bytes(probs) <= _max()
+    _run_ws(probs, gpu)
+    torch.cuda.synchronize()
+    want = [o.clone() for o in outs]
+    for o in outs:
+        o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            _run_noalloc(probs)
+    torch.cuda.synchronize()
+    other, other_outs, keep2 = _batch(gpu, 64, 1024, 4096, seed=22)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        _run_ws(other, gpu)  # eager work on the same device between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for g_, w_ in zip(outs, want):
+            assert torch.equal(g_, w_), rep
+    del graph

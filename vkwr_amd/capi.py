@@ -125,6 +125,19 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def _idx(t, n, what):
+    """Pointer of an index tensor the kernels read as n int32 values (slot tables, row
+    gathers): int32, on the GPU, contiguous, at least n entries.  An int64 tensor would be
+    read as pairs of 32-bit words -- wrong and duplicated slots that still pass the
+    kernels' range checks -- so anything else is refused here."""
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous() or t.numel() < n:
+        raise TypeError(f"{what}: expected a contiguous int32 CUDA tensor of >= {n} entries, got "
+                        f"{t.dtype} {t.device} shape {tuple(t.shape)} contiguous={t.is_contiguous()}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
 def gemm_problem(a, b, c, b_layout=GEMM_B_NK, a_act=ACT_NONE, epilogue=EPI_NONE, v=None, v_first=None, v0=None):
     """c[m,n] = epilogue(act(a)[m,k] . B): a [m,k], c [m,n]; b [n,k] (NK) or [k,n] (KN)."""
     k = a.shape[-1]
@@ -186,7 +199,8 @@ def add_layer_norm_mix(x, residual, shift_state, weight, bias, mixes, x_out, out
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
     fn = _ln_mix_frag if frag else _ln_mix
     _check(fn(rows, C, _ptr(x), _ptr(residual), _ptr(shift_state), _ptr(weight), _ptr(bias), len(mixes),
-              mp, eps, _ptr(x_out), op, _ptr(x_rows), _ptr(shift_slots), x.numel() // C,
+              mp, eps, _ptr(x_out), op, _idx(x_rows, rows, "x_rows"), _idx(shift_slots, rows, "shift_slots"),
+              x.numel() // C,
               shift_state.numel() // C, _stream()),
            "vkwr_add_layer_norm_mix%s_f16" % ("_frag" if frag else ""))
 
@@ -282,7 +296,8 @@ def add_layer_norm_mix_parts(x_parts, n_parts, part_stride, residual, shift_stat
     mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
     _check(_ln_mix_parts(rows, C, _ptr(x_parts), n_parts, part_stride, _ptr(residual), _ptr(shift_state),
-                         _ptr(weight), _ptr(bias), len(mixes), mp, eps, _ptr(x_out), op, _ptr(shift_slots),
+                         _ptr(weight), _ptr(bias), len(mixes), mp, eps, _ptr(x_out), op,
+                         _idx(shift_slots, rows, "shift_slots"),
                          shift_state.numel() // C, _stream()), "vkwr_add_layer_norm_mix_parts_frag_f16")
 
 
@@ -292,21 +307,24 @@ def _arr_frag(problems):
 
 
 def wkv_slots(B, T, C, H, pool, slots, r, w, k, v, a, b, y):
-    _check(_wkv_slots(B, T, C, H, _ptr(pool), pool.shape[0], _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
+    _check(_wkv_slots(B, T, C, H, _ptr(pool), pool.shape[0], _idx(slots, B, "slots"), _ptr(r), _ptr(w), _ptr(k),
+                      _ptr(v),
                       _ptr(a), _ptr(b), _ptr(y), _stream()), "vkwr_wkv7_fp32_forward_slots")
 
 
 def wkv_step_rows_slots(B, C, H, pool, slots, r, w, k, v, a, b, y):
     """One decode step on the slot pool in the row-split dot-product order, without LDS
     (vkwr_wkv7_fp32_step_rows_slots)."""
-    _check(_wkv_step_rows(B, C, H, _ptr(pool), pool.shape[0], _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
+    _check(_wkv_step_rows(B, C, H, _ptr(pool), pool.shape[0], _idx(slots, B, "slots"), _ptr(r), _ptr(w), _ptr(k),
+                          _ptr(v),
                           _ptr(a), _ptr(b), _ptr(y), _stream()), "vkwr_wkv7_fp32_step_rows_slots")
 
 
 def wkv_decode_fused(B, C, H, pool, slots, r, w, k, v, a12, g, k_k, a0, k_a, r_k, ln_w, ln_b, out, frag=False,
                      state_layout=WKV_STATE_STD):
     """gate -> WKV-7 (slot pool, T = 1) -> GroupNorm + bonus + gate in one launch."""
-    _check(_wkv_fused(B, C, H, _ptr(pool), pool.shape[0], state_layout, _ptr(slots), _ptr(r), _ptr(w), _ptr(k), _ptr(v),
+    _check(_wkv_fused(B, C, H, _ptr(pool), pool.shape[0], state_layout, _idx(slots, B, "slots"), _ptr(r), _ptr(w),
+                      _ptr(k), _ptr(v),
                       _ptr(a12), _ptr(g), _ptr(k_k), _ptr(a0), _ptr(k_a), _ptr(r_k), _ptr(ln_w), _ptr(ln_b),
                       _ptr(out), 1 if frag else 0, _stream()), "vkwr_wkv7_decode_fused_f16")
 
@@ -339,7 +357,8 @@ def layer_norm_shift_rows(x, weight, bias, x_out, mixes, outs, shift_state, grou
         return
     mp = (_p * len(mixes))(*[m.data_ptr() for m in mixes])
     op = (_p * len(outs))(*[o.data_ptr() for o in outs])
-    gs = (LnShiftGroup * len(groups))(*[LnShiftGroup(r0, B, T, sl.data_ptr()) for r0, B, T, sl in groups])
+    gs = (LnShiftGroup * len(groups))(*[LnShiftGroup(r0, B, T, _idx(sl, B, "group slots"))
+                                        for r0, B, T, sl in groups])
     _check(_ln_shift_rows(rows, C, _ptr(x), _ptr(residual), _ptr(weight), _ptr(bias), eps, _ptr(x_out), len(mixes),
                           mp, op, _ptr(shift_state), shift_state.numel() // C, len(groups), gs, _stream()),
            "vkwr_add_layer_norm_shift_rows_f16")
@@ -353,7 +372,8 @@ def token_shift(B, T, C, x, shift_state, mixes, outs, half_math=False, shift_slo
         _check(_shift(B, T, C, _ptr(x), _ptr(shift_state), len(mixes), mp, op, 1 if half_math else 0, _stream()),
                "vkwr_token_shift_mix_f16")
     else:
-        _check(_shift_slots(B, T, C, _ptr(x), _ptr(shift_state), shift_state.numel() // C, _ptr(shift_slots),
+        _check(_shift_slots(B, T, C, _ptr(x), _ptr(shift_state), shift_state.numel() // C,
+                            _idx(shift_slots, B, "shift_slots"),
                             len(mixes), mp, op, 1 if half_math else 0, _stream()), "vkwr_token_shift_mix_slots_f16")
 
 

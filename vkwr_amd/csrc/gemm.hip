@@ -1806,6 +1806,10 @@ extern "C" int64_t vkwr_gemm_f16_noalloc_max_bytes(void) { return kNoAllocScratc
 extern "C" int vkwr_gemm_f16_noalloc(int n_problems, const vkwr_gemm_problem* problems, void* stream) {
   clear_error();
   const char* fn = "vkwr_gemm_f16_noalloc";
+  // The scratch address is looked up on every call's device before anything else, so that
+  // any first call -- an empty or even an invalid batch -- does it outside a graph capture.
+  void* ws = nullptr;
+  if (int e = scratch_ptr(fn, &ws)) return e;
   Batch bt;
   Config cfg;
   if (int e = build_batch(fn, n_problems, problems, bt, cfg)) return e;
@@ -1814,9 +1818,5 @@ extern "C" int vkwr_gemm_f16_noalloc(int n_problems, const vkwr_gemm_problem* pr
              "%s: this batch needs %lld bytes of scratch; the allocation-free entry point holds at most "
              "%lld (use vkwr_gemm_f16 with a workspace)",
              fn, (long long)need, (long long)kNoAllocScratchBytes);
-  void* ws = nullptr;
-  if (need > 0) {
-    if (int e = scratch_ptr(fn, &ws)) return e;
-  }
-  return gemm_run(fn, bt, cfg, ws, stream);
+  return gemm_run(fn, bt, cfg, need > 0 ? ws : nullptr, stream);
 }

@@ -466,160 +466,14 @@ struct LnShiftArgs {
   LnShiftGroup g[kMaxShiftGroups];
 };
 
-// Two workgroup sums with one barrier: each is block_sum_ln's value, in its order.
-template <int NW>
-__device__ __forceinline__ void block_sum2_ln(float& a, float& b, float* red) {
-  a = wave_sum_dpp(a);
-  b = wave_sum_dpp(b);
-  if ((threadIdx.x & 63) == 0) {
-    red[threadIdx.x >> 6] = a;
-    red[NW + (threadIdx.x >> 6)] = b;
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  float ta = red[0], tb = red[NW];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) {
-    ta += red[w];
-    tb += red[NW + w];
-  }
-  a = ta;
-  b = tb;
-}
-
-template <int NV, int NMIX>
-__global__ __launch_bounds__(kThreads) void ln_shift_rows_kernel(LnShiftArgs p) {
-  __shared__ float red[2][2 * kWaves];
-  const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x, C = p.C;
-  int gi = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxShiftGroups; ++i)
-    if (i < p.n_groups && row >= p.g[i].r0) gi = i;
-  const int64_t r0 = p.g[gi].r0;
-  const int T = p.g[gi].T;
-  const int64_t local = row - r0;
-  const int b = (int)(local / T), t = (int)(local - (int64_t)b * T);
-  const int64_t slot = p.g[gi].slots[b];
-  const int64_t dst = row * (int64_t)C;
-  if (slot < 0 || slot >= p.n_shift) {
-    // A slot outside the pool: the row's outputs are NaN and no shift row is touched.
-    const _Float16 nan = (_Float16)__builtin_nanf("");
-    for (int c = tid; c < C; c += kThreads) {
-      p.x_out[dst + c] = nan;
-#pragma unroll
-      for (int i = 0; i < NMIX; ++i) p.out[i][dst + c] = nan;
-    }
-    return;
-  }
-  const bool has_sec = t > 0 || T > 1;
-  // the second row: the previous one, or (t = 0) the sequence's last one; itself if none
-  const int64_t srow2 = t > 0 ? row - 1 : (T > 1 ? row + (T - 1) : row);
-  const int64_t sec = srow2 * (int64_t)C;
-  const int64_t sdst = slot * (int64_t)C;
-  auto col = [&](int n) {
-    const int c = (tid + n * kThreads) * 8;
-    return c < C ? c : C - 8;
-  };
-  // every load first (the shift row only where it is read), then the arithmetic
-  h8 xc[NV], rc[NV], xs[NV], rs[NV], wp[NV], bp[NV], mp[NV][NMIX], old[NV];
-#pragma unroll
-  for (int n = 0; n < NV; ++n) {
-    const int cl = col(n);
-    xc[n] = ld8(p.x + dst + cl);
-    xs[n] = ld8(p.x + sec + cl);
-    wp[n] = ld8(p.weight + cl);
-    bp[n] = ld8(p.bias + cl);
-#pragma unroll
-    for (int i = 0; i < NMIX; ++i) mp[n][i] = ld8(p.mix[i] + cl);
-  }
-  if (p.residual) {
-#pragma unroll
-    for (int n = 0; n < NV; ++n) {
-      rc[n] = ld8(p.residual + dst + col(n));
-      rs[n] = ld8(p.residual + sec + col(n));
-    }
-  }
-  if (t == 0) {
-#pragma unroll
-    for (int n = 0; n < NV; ++n) old[n] = ld8(p.shift + sdst + col(n));
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  float vc[NV][8], vs[NV][8], sc = 0.0f, ss = 0.0f;
-#pragma unroll
-  for (int n = 0; n < NV; ++n) {
-    const bool in = (tid + n * kThreads) * 8 < C;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      vc[n][e] = (float)xc[n].v[e];
-      vs[n][e] = (float)xs[n].v[e];
-    }
-    if (p.residual) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vc[n][e] = vc[n][e] + (float)rc[n].v[e];
-        vs[n][e] = vs[n][e] + (float)rs[n].v[e];
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sc += in ? vc[n][e] : 0.0f;
-      ss += in ? vs[n][e] : 0.0f;
-    }
-  }
-  block_sum2_ln<kWaves>(sc, ss, red[0]);
-  const float mc = sc / (float)C, ms = ss / (float)C;
-  float qc = 0.0f, qs = 0.0f;
-#pragma unroll
-  for (int n = 0; n < NV; ++n) {
-    if ((tid + n * kThreads) * 8 < C) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float dc = vc[n][e] - mc, ds = vs[n][e] - ms;
-        qc = __builtin_fmaf(dc, dc, qc);
-        qs = __builtin_fmaf(ds, ds, qs);
-      }
-    }
-  }
-  block_sum2_ln<kWaves>(qc, qs, red[1]);
-  const float rc_std = rsqrtf(qc / (float)C + p.eps), rs_std = rsqrtf(qs / (float)C + p.eps);
-#pragma unroll
-  for (int n = 0; n < NV; ++n) {
-    const int c0 = (tid + n * kThreads) * 8;
-    if (c0 >= C) continue;
-    // (element-wise selects: a select of whole h8 values goes through scratch memory)
-    h8 yc, xo, prev, snew;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float wt = (float)wp[n].v[e], bs = (float)bp[n].v[e];
-      yc.v[e] = f16_of(__builtin_fmaf((vc[n][e] - mc) * rc_std, wt, bs));
-      const _Float16 ys = f16_of(__builtin_fmaf((vs[n][e] - ms) * rs_std, wt, bs));
-      xo.v[e] = (_Float16)vc[n][e];
-      prev.v[e] = t > 0 ? ys : old[n].v[e];
-      snew.v[e] = has_sec ? ys : yc.v[e];
-    }
-    st8(p.x_out + dst + c0, xo);
-#pragma unroll
-    for (int i = 0; i < NMIX; ++i) {
-      h8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float yv = (float)yc.v[e];
-        o.v[e] = f16_of(__builtin_fmaf((float)prev.v[e] - yv, (float)mp[n][i].v[e], yv));
-      }
-      st8(p.out[i] + dst + c0, o);
-    }
-    if (t == 0) st8(p.shift + sdst + c0, snew);
-  }
-}
-
-// The same operation over runs of up to kLnRun consecutive rows of one sequence per
-// workgroup (runs never cross a sequence): the LayerNorm weight, bias and mix vectors are
+// Residual add + LayerNorm + token shift over runs of up to kLnRun consecutive rows of one
+// sequence per workgroup (runs never cross a sequence): the LayerNorm weight, bias and mix vectors are
 // loaded once per run instead of once per row, and each row's LayerNorm output is the next
 // row's "previous token" straight from registers, so a run of n rows normalises n + 1 rows
 // (the row before the run, or for the sequence's first run its last row, which goes to the
-// shift pool) instead of 2n.  Each row's arithmetic is the row kernel's, in the same order.
+// shift pool) instead of 2n.  Each row's arithmetic is layer_norm_kernel's, in the same order.
 // Measured at 2304 rows x 4096 (256 decode rows + 4 chunks of 512): 31.1 us with 6 lerps and
-// 16.9 us with 1 (6.1 / 5.6 TB/s), against 34.1 / 20.9 us for the row kernel above (runs of
+// 16.9 us with 1 (6.1 / 5.6 TB/s), against 34.1 / 20.9 us for one row per workgroup (runs of
 // 8 rows: 31.1 / 18.3 us).
 constexpr int kLnRun = 4;
 
@@ -666,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void ln_shift_runs_kernel(LnShiftArgs p) 
       if (p.residual) ra[n] = ld8(p.residual + o + col(n));
     }
   };
-  // LayerNorm of the loaded row (the row kernel's arithmetic and order): y and x + residual
+  // LayerNorm of the loaded row (layer_norm_kernel's arithmetic and order): y and x + residual
   auto ln_row = [&](float* rd, h8 (&y)[NV], h8 (&xo)[NV]) __attribute__((always_inline)) {
     float v[NV][8], sum = 0.0f;
 #pragma unroll
