@@ -127,7 +127,58 @@ def capture(step_fn, n_steps, stream):
     return g
 
 
-def model_decode(dev, steps, warmup=3, frag=True, eager=False, keep_cpu_model=None):
+def op_surface_decode(model, dev, steps, warmup=3):
+    """The same config-3 decode step composed only of the reference's op surface
+    (vkwr.model_executor.OpDecodeEngine: vkwr._ops wrappers, token-shift rows gathered
+    with index_select and written back with index_copy_, WKV through the slot-pool op)
+    on a row-major 160-slot pool: device time of one step captured into a HIP graph and
+    replayed, and the eager step (host dispatch of ~400 op calls included)."""
+    from vkwr_amd import capi
+    from vkwr.model_executor import OpDecodeEngine, RWKV7State
+
+    cfg, B = model.cfg, 128
+    state = RWKV7State(cfg, 160, dev, std=0.1, seed=1, layout=capi.WKV_STATE_STD)
+    eng = OpDecodeEngine(model)
+    g = torch.Generator().manual_seed(3)
+    slots = torch.randperm(160, generator=g)[:B].to(torch.int32).to(dev)
+    tokens = torch.randint(0, cfg.vocab, (B,), generator=g, dtype=torch.int32).to(dev)
+    for _ in range(warmup):
+        eng.step(state, tokens, slots)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(steps):
+            eng.step(state, tokens, slots)
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_eager = ev0.elapsed_time(ev1) / steps
+    graph = capture(lambda i: eng.step(state, tokens, slots), 1, stream)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    del graph, state, eng
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
+            "ms_per_step_eager": round(ms_eager, 4), "tokens_per_s_eager": round(B / (ms_eager * 1e-3), 1),
+            "steps": steps,
+            "path": "OpDecodeEngine: reference op wrappers only (add_layer_norm_tmix_mix6_f16, linear_f16_orig, "
+                    "linear_wag(v)_rank_in/out_f16, add_vec, tmix_kk_a_gate, wkv_forward_slots_fp32, "
+                    "tmix_lnx_rkvres_xg, add_layer_norm_cmix_mix_f16, cmix_sparse_down_relu_rows, "
+                    "add_last_layer_norm_f16), shift rows gathered / scattered with index_select / index_copy_",
+            "timing": "ms_per_step: one step captured as a HIP graph and replayed (device time); "
+                      "ms_per_step_eager: op calls issued from Python every step"}
+
+
+def model_decode(dev, steps, warmup=3, frag=True, eager=False, keep_cpu_model=None, op_steps=0):
     """the RWKV-7 1.5B-shape decode step (L=24, C=2048, random fp16
     weights) for 128 sequences at T=1 from a 160-slot state pool.  One step is captured
     into a HIP graph and replayed `steps` times (the recurrent state advances every
@@ -171,11 +222,14 @@ def model_decode(dev, steps, warmup=3, frag=True, eager=False, keep_cpu_model=No
         torch.cuda.synchronize()
         del graph
     ms = ev0.elapsed_time(ev1) / steps
+    del eng, state
+    torch.cuda.empty_cache()
+    op = op_surface_decode(model, dev, op_steps) if op_steps > 0 else None
     if keep_cpu_model is not None:
         keep_cpu_model.append(cpu_model_copy(model))
     nbytes = gbytes_per_step(cfg, B)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {
+    out = {
         "workload": "RWKV-7 1.5B-shape decode step (BASELINE config 3): L=24, C=2048, H=32, F=8192, "
                     "ranks w/a/v/g 96/96/64/256, V=65536, bs=128, T=1, random-init fp16 weights, "
                     "fp32 WKV state in a 160-slot pool",
@@ -190,6 +244,9 @@ def model_decode(dev, steps, warmup=3, frag=True, eager=False, keep_cpu_model=No
         "timing": ("eager launches" if eager else "one decode step captured as a HIP graph, replayed") +
                   "; HIP events on the launch stream",
     }
+    if op is not None:
+        out["op_surface_step"] = op
+    return out
 
 
 def prefill_c2(dev, steps, warmup=100):
@@ -689,7 +746,8 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.only:
-        run = {"decode": lambda: model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm, eager=args.eager),
+        run = {"decode": lambda: model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm, eager=args.eager,
+                                              op_steps=0 if args.eager else args.model_steps),
                "prefill": lambda: prefill_c2(dev, args.prefill_calls),
                "serve": lambda: serve_mixed_7b(dev, args.serve_steps),
                "sampling": lambda: sampling_bs128(dev, args.sampling_calls),
@@ -841,7 +899,7 @@ def main():
         del inputs
         torch.cuda.empty_cache()
         result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm,
-                                                   keep_cpu_model=keep)
+                                                   keep_cpu_model=keep, op_steps=args.model_steps)
         torch.cuda.empty_cache()
         log("config 3 decode step done")
     if args.prefill_calls > 0 and not args.eager:
