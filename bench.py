@@ -170,9 +170,9 @@ def op_surface_decode(model, dev, steps, warmup=3):
     return {"ms_per_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
             "ms_per_step_eager": round(ms_eager, 4), "tokens_per_s_eager": round(B / (ms_eager * 1e-3), 1),
             "steps": steps,
-            "path": "OpDecodeEngine: reference op wrappers only (add_layer_norm_tmix_mix6_f16, linear_f16_orig, "
+            "path": "OpDecodeEngine: reference op wrappers only (add_layer_norm_tmix_mix6_f16, linear_f16_orig, relu_square, "
                     "linear_wag(v)_rank_in/out_f16, add_vec, tmix_kk_a_gate, wkv_forward_slots_fp32, "
-                    "tmix_lnx_rkvres_xg, add_layer_norm_cmix_mix_f16, cmix_sparse_down_relu_rows, "
+                    "tmix_lnx_rkvres_xg, add_layer_norm_cmix_mix_f16, "
                     "add_last_layer_norm_f16), shift rows gathered / scattered with index_select / index_copy_",
             "timing": "ms_per_step: one step captured as a HIP graph and replayed (device time); "
                       "ms_per_step_eager: op calls issued from Python every step"}

@@ -21,37 +21,37 @@ pytestmark = pytest.mark.gpu
 LOGIT_TOL = 5e-2
 
 
-def _setup(gpu, preset, B, P, seed=0, wkv="slots"):
+def _setup(gpu, preset, B, P, seed=0, wkv="slots", ffn="dense"):
     from vkwr_amd import capi
     from vkwr.model_executor import OpDecodeEngine, RWKV7Config, RWKV7Model, RWKV7State
     cfg = RWKV7Config.preset(preset)
     model = RWKV7Model(cfg, gpu, seed=seed)
     state = RWKV7State(cfg, P, gpu, std=0.1, seed=seed + 1, layout=capi.WKV_STATE_STD)
-    eng = OpDecodeEngine(model, wkv=wkv)
+    eng = OpDecodeEngine(model, wkv=wkv, ffn=ffn)
     g = torch.Generator().manual_seed(seed)
     slots = torch.randperm(P, generator=g)[:B].to(torch.int32).to(gpu)
     return cfg, model, state, eng, slots, g
 
 
-@pytest.mark.parametrize("wkv", ["slots", "gather"])
-def test_tiny_op_step_matches_cpu_oracle_over_steps(gpu, wkv):
-    cfg, model, state, eng, slots, g = _setup(gpu, "tiny", B=4, P=9, wkv=wkv)
+@pytest.mark.parametrize("wkv,ffn", [("slots", "dense"), ("gather", "dense"), ("slots", "sparse")])
+def test_tiny_op_step_matches_cpu_oracle_over_steps(gpu, wkv, ffn):
+    cfg, model, state, eng, slots, g = _setup(gpu, "tiny", B=4, P=9, wkv=wkv, ffn=ffn)
     wkv_s = state.wkv.cpu()
     wkv0 = wkv_s.clone()
-    att, ffn = state.att_shift.cpu().clone(), state.ffn_shift.cpu().clone()
-    att0, ffn0 = att.clone(), ffn.clone()
-    wkv_r, att_r, ffn_r = wkv_s.clone(), att.clone(), ffn.clone()
+    att, ffn_s = state.att_shift.cpu().clone(), state.ffn_shift.cpu().clone()
+    att0, ffn0 = att.clone(), ffn_s.clone()
+    wkv_r, att_r, ffn_r = wkv_s.clone(), att.clone(), ffn_s.clone()
     for step in range(3):
         tokens = torch.randint(0, cfg.vocab, (4,), generator=g, dtype=torch.int32)
         logits = eng.step(state, tokens.to(gpu), slots).float().cpu()
-        ref = model_ref.decode_step(model, wkv_s, att, ffn, tokens, slots.cpu(), round_fp16=True)
+        ref = model_ref.decode_step(model, wkv_s, att, ffn_s, tokens, slots.cpu(), round_fp16=True)
         ref32 = model_ref.decode_step(model, wkv_r, att_r, ffn_r, tokens, slots.cpu(), round_fp16=False)
         assert logits.shape == (4, cfg.vocab)
         assert (logits - ref).abs().max() <= 1e-2, (step, float((logits - ref).abs().max()))
         assert (logits - ref32).abs().max() <= LOGIT_TOL, (step, float((logits - ref32).abs().max()))
         assert (state.wkv.cpu() - wkv_s).abs().max() <= 1e-3
         assert (state.att_shift.cpu().float() - att.float()).abs().max() <= 1e-2
-        assert (state.ffn_shift.cpu().float() - ffn.float()).abs().max() <= 1e-2
+        assert (state.ffn_shift.cpu().float() - ffn_s.float()).abs().max() <= 1e-2
     others = [s for s in range(9) if s not in slots.cpu().tolist()]
     assert torch.equal(state.wkv.cpu()[:, others], wkv0[:, others])
     assert torch.equal(state.att_shift.cpu()[:, others], att0[:, others])
@@ -77,20 +77,21 @@ def test_op_step_wkv_slot_op_equals_gather_dense_scatter(gpu):
         assert torch.equal(x, y)
 
 
-def test_1p5b_op_step_bs128_logits(gpu):
+@pytest.mark.parametrize("ffn", ["dense", "sparse"])
+def test_1p5b_op_step_bs128_logits(gpu, ffn):
     """BASELINE config 3 at full shape through the op surface: L=24, C=2048, bs=128, one
     decode step, logits and states against the float32 composition (torch on the GPU)."""
-    cfg, model, state, eng, slots, g = _setup(gpu, "1.5b", B=128, P=160)
+    cfg, model, state, eng, slots, g = _setup(gpu, "1.5b", B=128, P=160, ffn=ffn)
     tokens = torch.randint(0, cfg.vocab, (128,), generator=g, dtype=torch.int32).to(gpu)
     wkv = state.wkv.clone()
     wkv0 = wkv.clone()
-    att, ffn = state.att_shift.clone(), state.ffn_shift.clone()
+    att_s, ffn_s = state.att_shift.clone(), state.ffn_shift.clone()
     logits = eng.step(state, tokens, slots).float()
     torch.cuda.synchronize()
     with torch.no_grad():
-        ref = model_ref.decode_step(model, wkv, att, ffn, tokens, slots, round_fp16=False)
+        ref = model_ref.decode_step(model, wkv, att_s, ffn_s, tokens, slots, round_fp16=False)
     err = (logits - ref).abs().max().item()
-    print(f"config 3 op-surface step: logits max-abs {err:.3g}", flush=True)
+    print(f"config 3 op-surface step ({ffn} FFN): logits max-abs {err:.3g}", flush=True)
     assert err <= LOGIT_TOL, err
     sl = slots.long()
     assert (state.wkv[:, sl] - wkv[:, sl]).abs().max().item() <= 2.5e-2

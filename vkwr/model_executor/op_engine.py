@@ -20,7 +20,8 @@ vkwr/model_executor is empty) calls.  Per layer:
     o = linear_f16_orig(tmix_lnx_rkvres_xg(y, r, new_k, v, ...), Wo)
   channel mix
     x_out2, xk = add_layer_norm_cmix_mix_f16(o, x_out, shift, ...)
-    x = cmix_sparse_down_relu_rows(linear_f16_orig(xk, key), value_fc)   (relu^2 fused)
+    x = linear_f16_orig(relu_square(linear_f16_orig(xk, key)), value)          (ffn="dense"), or
+    x = cmix_sparse_down_relu_rows(linear_f16_orig(xk, key), value_fc)         (ffn="sparse")
   head
     logits = linear_f16_orig(add_last_layer_norm_f16(x, res, ...), head)
 
@@ -30,7 +31,9 @@ before the op and written back with index_copy_ after it.  The ops allocate
 their outputs, as the reference's do (the caching allocator serves them; under
 a HIP graph capture they come from the graph's pool).  The only weight the ops
 want in another layout is the FFN value, which cmix_sparse_* takes as [F, C]:
-it is transposed once when the engine is built.
+with ffn="sparse" it is transposed once when the engine is built.  At 128 rows
+the dense form is the faster one: its down projection streams the [N, K] weight,
+where cmix_sparse_down_relu_rows gathers [K, N] fragments column by column.
 """
 import torch
 
@@ -47,13 +50,15 @@ class OpDecodeEngine:
 
     wkv="slots" steps the WKV state through the slot-pool op (one launch per layer);
     wkv="gather" gathers the batch's states with index_select, calls the reference's
-    dense wkv_forward_fp32 and scatters them back with index_copy_."""
+    dense wkv_forward_fp32 and scatters them back with index_copy_.  ffn selects the
+    channel mix's down projection: "dense" (relu_square, then linear_f16_orig) or
+    "sparse" (cmix_sparse_down_relu_rows)."""
 
-    def __init__(self, model, wkv="slots"):
-        assert wkv in ("slots", "gather")
-        self.model, self.cfg, self.wkv = model, model.cfg, wkv
+    def __init__(self, model, wkv="slots", ffn="dense"):
+        assert wkv in ("slots", "gather") and ffn in ("dense", "sparse")
+        self.model, self.cfg, self.wkv, self.ffn = model, model.cfg, wkv, ffn
         # cmix_sparse_* take the FFN value weight as [F, C] (value_fc); the model keeps [C, F]
-        self.value_fc = [L["value"].t().contiguous() for L in model.layers]
+        self.value_fc = [L["value"].t().contiguous() for L in model.layers] if ffn == "sparse" else None
 
     def step(self, state, tokens, slots):
         """One decode step for B = len(tokens) sequences: tokens, slots int32 [B] on the
@@ -110,6 +115,9 @@ class OpDecodeEngine:
             res, xk2 = NORM.add_layer_norm_cmix_mix_f16(o, res, ffn, L["ln2_w"], L["ln2_b"], L["x_k_ffn"])
             state.ffn_shift[l].index_copy_(0, sl, ffn)
             pre = LIN.linear_f16_orig(xk2, L["key"])
-            x = MIX.cmix_sparse_down_relu_rows(B, 1, C, F, pre, self.value_fc[l])
+            if self.ffn == "dense":
+                x = LIN.linear_f16_orig(MIX.relu_square(pre), L["value"])
+            else:
+                x = MIX.cmix_sparse_down_relu_rows(B, 1, C, F, pre, self.value_fc[l])
         h = NORM.add_last_layer_norm_f16(x, res, m.ln_out_w, m.ln_out_b)
         return LIN.linear_f16_orig(h, m.head)

@@ -65,9 +65,34 @@ struct Batch {
   Prob p[kMaxProblems];
 };
 
+// A-operand activations.  Each workgroup applies them to every A element it reads, so a
+// batch re-evaluates them once per column tile; they use the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32) instead of the libm forms (tanhf is a few dozen instructions): the
+// rank-out batch of a 128-row decode step took 13.1 us with tanhf and 8.6 us with no
+// activation.  The result is rounded to fp16 before the product, so their relative error
+// (about 2e-6: 1.9e-6 for tanh and 0.9e-6 for sigmoid in a float32 emulation against
+// float64, plus an ulp or two of the hardware exp2 and reciprocal) only moves the fp16
+// rounding of an activated operand now and then (5e-5 of them in that emulation).
+//   tanh(x) = sign(x) (1 - 2 / (1 + e^{2|x|})), and x - x^3/3 + 2x^5/15 for |x| < 1/16 (where
+//   the subtraction would cancel; the next term, 17x^7/315, is below 1e-8 relative there);
+//   sigmoid(x) = 1 / (1 + e^{-x}).
+__device__ __forceinline__ float tanh_act(float x) {
+  const float ax = fabsf(x);
+  if (ax < 0.0625f) {
+    const float x2 = x * x;
+    return x * __builtin_fmaf(x2, __builtin_fmaf(x2, 0.13333333333f, -0.33333333333f), 1.0f);
+  }
+  const float e = __builtin_amdgcn_exp2f(ax * 2.8853900817779268f);  // e^{2|x|}
+  return __builtin_copysignf(__builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f), x);
+}
+
+__device__ __forceinline__ float sigmoid_act(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
 __device__ __forceinline__ float act_in(float x, int act) {
-  if (act == VKWR_GEMM_ACT_TANH) return tanhf(x);
-  if (act == VKWR_GEMM_ACT_SIGMOID) return sigmoidf(x);
+  if (act == VKWR_GEMM_ACT_TANH) return tanh_act(x);
+  if (act == VKWR_GEMM_ACT_SIGMOID) return sigmoid_act(x);
   if (act == VKWR_GEMM_ACT_RELU_SQUARE) {
     const float r = fmaxf(x, 0.0f);
     return r * r;
@@ -907,8 +932,10 @@ __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan p
 //
 // At M <= 128 every weight byte is used M times, so the launch streams the weights
 // once and is bound by how many bytes each CU keeps in flight.  A workgroup owns a
-// (32 TM) x (32 TN) output tile over the whole of K; its 4 waves take the 64-deep k blocks
-// w, w + 4, ... (an in-workgroup K split: no workspace, no second kernel), and each wave
+// (32 TM) x (32 TN) output tile over the whole of K -- or, when the tiles alone leave CUs
+// idle (the low-rank input projections, [K,N] weights with long K), over one of `splits`
+// K parts, writing fp32 partials that splitk_reduce_kernel adds in part order; its 4
+// waves take the 64-deep k blocks w, w + 4, ... (an in-workgroup K split), and each wave
 // stages its blocks through two private LDS buffers with the DMA form of the vector
 // load (global_load_lds_dwordx4, no VGPR staging): one instruction moves 8 whole
 // 128-byte rows (64 k of a row is one cache line), chunk c of row r landing at slot
@@ -944,11 +971,17 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
   for (int i = 1; i < kMaxProblems; ++i)
     if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
   const Prob& P = bt.p[pi];
-  const int lt = t - P.tile_begin;
+  const int ntiles = P.tiles_m * P.tiles_n;
+  const int lt0 = t - P.tile_begin;
+  const int split = lt0 / ntiles;  // K part (split-major: the parts of a tile run apart in time)
+  const int lt = lt0 - split * ntiles;
   const int m0 = (lt / P.tiles_n) * (32 * TM), n0 = (lt % P.tiles_n) * (32 * TN);
   const int M = P.m, N = P.n, K = P.k, a_act = P.a_act;
+  // this workgroup's K range [kbeg, kbeg + klen); klen is a multiple of 8
+  const int kbeg = split * P.k_per_split;
+  const int klen = min(K - kbeg, P.k_per_split);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nkb = (K + kRmBK - 1) / kRmBK;
+  const int nkb = (klen + kRmBK - 1) / kRmBK;
   const int nb = nkb > w ? (nkb - w + kRmNW - 1) / kRmNW : 0;  // this wave's k blocks
 
   // DMA instruction j of a stage fills slots 64 j + lane: row (64 j + lane) >> 3, chunk
@@ -958,13 +991,13 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
 #pragma unroll
   for (int j = 0; j < TM * 4; ++j) {
     const int sl = 64 * j + lane, r = sl >> 3, c = (sl & 7) ^ ((r >> 1) & 7);
-    ao[j] = (uint32_t)(((int64_t)min(m0 + r, M - 1) * K + c * 8) * 2);
+    ao[j] = (uint32_t)(((int64_t)min(m0 + r, M - 1) * K + kbeg + c * 8) * 2);
   }
 #pragma unroll
   for (int j = 0; j < kBDma; ++j) {
     const int sl = 64 * j + lane, r = sl >> 3, c = (sl & 7) ^ ((r >> 1) & 7);
     if constexpr (kKN) bo[j] = (uint32_t)(min(n0 + c * 8, N - 8) * 2);  // the k row is added per block
-    else bo[j] = (uint32_t)(((int64_t)min(n0 + r, N - 1) * K + c * 8) * 2);
+    else bo[j] = (uint32_t)(((int64_t)min(n0 + r, N - 1) * K + kbeg + c * 8) * 2);
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sm[w][0][0]);
@@ -972,22 +1005,23 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
   const void* const bbase = uniform_ptr(P.b);
   auto dma = [&](int buf, int kb) __attribute__((always_inline)) {
     const uint32_t la = lds0 + (uint32_t)(buf * kStage * 2), lb = la + kA * 2;
-    // k past K: the chunk offset is clamped to the row's last chunk (read, then zeroed)
+    // k past the part's end: the chunk offset is clamped to the part's last chunk (read,
+    // then zeroed)
     const int k0 = kb * kRmBK;
 #pragma unroll
     for (int j = 0; j < TM * 4; ++j) {
       const int c = ((64 * j + lane) & 7) ^ ((((64 * j + lane) >> 3) >> 1) & 7);
-      const int kk = min(k0 + c * 8, K - 8) - c * 8;
+      const int kk = min(k0 + c * 8, klen - 8) - c * 8;
       dma16_m0(abase, ao[j] + (uint32_t)(kk * 2), la + j * 1024);
     }
 #pragma unroll
     for (int j = 0; j < kBDma; ++j) {
       if constexpr (kKN) {
         const int r = (64 * j + lane) >> 3;
-        dma16_m0(bbase, bo[j] + (uint32_t)((int64_t)(min(k0 + r, K - 1)) * N * 2), lb + j * 1024);
+        dma16_m0(bbase, bo[j] + (uint32_t)((int64_t)(kbeg + min(k0 + r, klen - 1)) * N * 2), lb + j * 1024);
       } else {
         const int c = ((64 * j + lane) & 7) ^ ((((64 * j + lane) >> 3) >> 1) & 7);
-        const int kk = min(k0 + c * 8, K - 8) - c * 8;
+        const int kk = min(k0 + c * 8, klen - 8) - c * 8;
         dma16_m0(bbase, bo[j] + (uint32_t)(kk * 2), lb + j * 1024);
       }
     }
@@ -1008,7 +1042,7 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int ch = 2 * kk + lh;
-      const bool kin = kb * kRmBK + ch * 8 < K;
+      const bool kin = kb * kRmBK + ch * 8 < klen;
       hv8 fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -1081,6 +1115,18 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
     if (row >= M || col >= N) continue;
     const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int64_t idx = (int64_t)row * N + col;
+    if (P.splits > 1) {  // fp32 partial of this K part; splitk_reduce_kernel finishes
+      float* const o = P.ws + (int64_t)split * M * N + idx;
+      if (P.vec_out && col + 8 <= N) {
+        *reinterpret_cast<f4*>(o) = s0;
+        *reinterpret_cast<f4*>(o + 4) = s1;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (col + e < N) o[e] = sv[e];
+      }
+      continue;
+    }
     if (P.vec_out && col + 8 <= N) {
       hv8 o;
 #pragma unroll
@@ -1381,7 +1427,34 @@ bool rm_config(const Batch& bt, int max_m, Config& cfg) {
       break;
     }
   }
-  if (pick < 0) return false;  // too few tiles: the K-split kernel fills the CUs better
+  if (pick < 0) {
+    // Too few tiles for the CUs whole: split K over workgroups (parts of at least one 64-deep
+    // block per wave, at most 16 parts).  Take the largest tile shape whose split fills the
+    // CUs, else the shape that comes closest.
+    int64_t best = 0;
+    for (int c = 0; c < 3; ++c) {
+      const int bm = shapes[c][0], bn = shapes[c][1];
+      if (bm == 64 && max_m <= 32) continue;
+      if (kn && bn != 64) continue;
+      const int nw = (bm == 32 && bn == 32) ? 8 : 4;
+      int64_t wgs = 0;
+      for (int i = 0; i < bt.n; ++i) {
+        const Prob& P = bt.p[i];
+        if (P.m == 0 || P.n == 0) continue;
+        const int64_t t = (int64_t)((P.m + bm - 1) / bm) * ((P.n + bn - 1) / bn);
+        wgs += t * std::max(1, std::min(16, P.k / (kRmBK * nw)));
+      }
+      if (wgs >= cus) {
+        pick = c;
+        break;
+      }
+      if (wgs > best) {
+        best = wgs;
+        pick = c;
+      }
+    }
+    if (pick < 0) return false;
+  }
   cfg = Config{shapes[pick][0], shapes[pick][1], false, true, kn == 1};
   return true;
 }
@@ -1447,18 +1520,36 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
     return ws;
   }
   if (cfg.rm) {
-    int begin = 0;
+    // K parts only when the batch's tiles leave CUs idle: enough parts to give every CU a
+    // workgroup, each a multiple of 64 deep and at least one 64-deep block per wave.
+    const int nw = (cfg.bm == 32 && cfg.bn == 32) ? 8 : 4;
+    int tiles = 0;
     for (int i = 0; i < bt.n; ++i) {
       Prob& P = bt.p[i];
       const bool empty = P.m == 0 || P.n == 0;
       P.tiles_m = empty ? 0 : (P.m + cfg.bm - 1) / cfg.bm;
       P.tiles_n = empty ? 0 : (P.n + cfg.bn - 1) / cfg.bn;
+      tiles += P.tiles_m * P.tiles_n;
+    }
+    const int cus = device_cus();
+    int64_t ws = 0;
+    int begin = 0;
+    for (int i = 0; i < bt.n; ++i) {
+      Prob& P = bt.p[i];
       P.splits = 1;
       P.k_per_split = P.k;
+      if (tiles > 0 && tiles < cus && P.tiles_m * P.tiles_n > 0 && P.k > 0) {
+        int s = std::min(16, (cus + tiles - 1) / tiles);
+        s = std::max(1, std::min(s, P.k / (kRmBK * nw)));
+        const int kps = ((P.k + s - 1) / s + kRmBK - 1) / kRmBK * kRmBK;
+        P.splits = (P.k + kps - 1) / kps;
+        P.k_per_split = P.splits > 1 ? kps : P.k;
+        if (P.splits > 1) ws += (int64_t)P.splits * P.m * P.n * 4;
+      }
       P.tile_begin = begin;
-      begin += P.tiles_m * P.tiles_n;
+      begin += P.tiles_m * P.tiles_n * P.splits;
     }
-    return 0;
+    return ws;
   }
   int tiles = 0;
   for (int i = 0; i < bt.n; ++i) {
@@ -1711,7 +1802,12 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
     else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, false>), dim3(wgs), dim3(256), 0, s, bt);
     else if (cfg.bn == 64) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, false>), dim3(wgs), dim3(256), 0, s, bt);
     else hipLaunchKernelGGL((gemm_rm_kernel<1, 1, false>), dim3(wgs), dim3(512), 0, s, bt);
-    return check_launch(fn);
+    if (int e = check_launch(fn)) return e;
+    if (any_split) {
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_wgs(bt), bt.n), dim3(256), 0, s, bt);
+      if (int e = check_launch(fn)) return e;
+    }
+    return VKWR_OK;
   }
   if (cfg.big) {
     BigPlan pl;
