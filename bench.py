@@ -67,7 +67,7 @@ def parse_args():
                     help="timed calls per shape of the op-surface GEMMs at M=1 and M=128 (0: skip)")
     ap.add_argument("--fp16-steps", type=int, default=200,
                     help="steps of the fp16-state WKV decode op at the config-1 shape (0: skip the fp16 section)")
-    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling", "ops", "fp16", "c1"],
+    ap.add_argument("--only", choices=["decode", "prefill", "serve", "sampling", "ops", "fp16", "c1", "gemm7b"],
                     help="run one section alone and print its JSON object (for profiler runs); with --eager "
                          "the decode steps are launched directly")
     return ap.parse_args()
@@ -554,6 +554,30 @@ def ops_small_m(dev, calls, warmup=3):
             "frag_path_us": round(us_frag, 2), "vs_frag": round(us / us_frag, 3)}
         del wf
         torch.cuda.empty_cache()
+    # the rest of the 1.5B layer's op-surface GEMMs at M = 128: the low-rank adapters (one op
+    # each, 4 problems) and the [K,N] activation-sparse FFN down projection
+    from vkwr._ops.v1 import v1_rank_ops as RK
+    Mr, Cr, Fr, Rw, Ra, Rg, Rv = 128, 2048, 8192, 96, 96, 64, 256
+    rn = lambda *sh, sd=1.0: (torch.randn(*sh, device=dev, generator=g) * sd).half()  # noqa: E731
+    xs = [rn(Mr, Cr) for _ in range(4)]
+    ins = [[rn(r, Cr, sd=0.02) for r in (Rw, Ra, Rg, Rv)] for _ in range(16)]  # 16 x 1.1 MiB
+    us = timed(lambda i: RK.linear_wagv_rank_in_f16(Mr, Cr, Rw, Ra, Rg, Rv, *xs, *ins[i % 16]), calls)
+    out["m128_linear_wagv_rank_in_f16"] = {"us": round(us, 2), "note": "4 problems, K=2048, N=96/96/64/256"}
+    lows = [rn(Mr, r) for r in (Rw, Ra, Rg, Rv)]
+    outs_w = [[rn(Cr, r, sd=0.1) for r in (Rw, Ra, Rg, Rv)] for _ in range(16)]
+    v, vf, v0 = rn(Mr, Cr), rn(Mr, Cr), rn(Cr)
+    us = timed(lambda i: RK.linear_wagv_rank_out_f16(Mr, Cr, Rw, Ra, Rg, Rv, *lows, *outs_w[i % 16], v, vf, v0), calls)
+    out["m128_linear_wagv_rank_out_f16"] = {"us": round(us, 2),
+                                            "note": "4 problems, N=2048, K=96/96/64/256, tanh / sigmoid on A, "
+                                                    "value residual"}
+    del ins, outs_w
+    pre = rn(Mr, 1, Fr)
+    vfc = copies((Fr, Cr))
+    us = timed(lambda i: MX.cmix_sparse_down_relu_rows(Mr, 1, Cr, Fr, pre, vfc[i % len(vfc)]), calls)
+    out["m128_cmix_sparse_down_relu_rows_C2048_F8192"] = {
+        "us": round(us, 2), "note": "[K,N] value_fc: each MFMA fragment gathered with 2-byte LDS reads"}
+    del vfc
+    torch.cuda.empty_cache()
     return {
         "workload": "vkwr_v1_linear ops through torch.ops at M=1 ([K,N] weights, linear_f16) and M=128 "
                     "([N,K] weights, linear_f16_orig), weights cold (rotated over >= 512 MiB of copies); "
@@ -619,6 +643,59 @@ def serve_mixed_7b(dev, steps, warmup=1):
                     "beside it",
         "timing": "eager launches, HIP events around the timed steps (the side stream joins the timed one)",
     }
+
+
+def gemm_7b_shapes(dev, calls=10, warmup=3):
+    """The large-M GEMM kernel (vkwr_gemm_f16) against torch.mm (hipBLASLt) on the GEMM
+    shapes of one 7B mixed step (2304 rows; the head over 260), plain epilogue, random fp16
+    operands.  torch.mm gets the weight as a contiguous [K, N] matrix (no transposed view),
+    this kernel the nn.Linear [N, K] weight.  Each form: `calls` calls captured into one
+    HIP graph, replayed once after an untimed replay; HIP events on the replay stream."""
+    from vkwr_amd import capi
+
+    g = torch.Generator(device=dev).manual_seed(13)
+    stream = torch.cuda.Stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        gr = capture(lambda i: fn(), calls, stream)
+        gr.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            gr.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        del gr
+        return ev0.elapsed_time(ev1) / calls * 1e3  # us
+
+    R = 2304
+    shapes = [("r/k/v + rank-in inputs", R, 3 * 4096 + 896, 4096), ("FFN key", R, 16384, 4096),
+              ("FFN value", R, 4096, 16384), ("o projection", R, 4096, 4096), ("head", 260, 65536, 4096),
+              ("rank-out w2 (K 128)", R, 4096, 128), ("rank-out g2 (K 512)", R, 4096, 512)]
+    out = {}
+    for name, M, N, K in shapes:
+        a = torch.randn(M, K, device=dev, generator=g).half()
+        w = (torch.randn(N, K, device=dev, generator=g) * 0.02).half()
+        wt = w.t().contiguous()
+        c = torch.empty(M, N, dtype=torch.float16, device=dev)
+        c2 = torch.empty(M, N, dtype=torch.float16, device=dev)
+        probs = [capi.gemm_problem(a, w, c)]
+        ws = torch.empty(max(capi.gemm_workspace_bytes(probs), 1), dtype=torch.uint8, device=dev)
+        us = timed(lambda: capi.gemm(probs, ws))
+        us_lib = timed(lambda: torch.mm(a, wt, out=c2))
+        fl = 2 * M * N * K
+        out[name] = {"M": M, "N": N, "K": K, "us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                     "hipblaslt_us": round(us_lib, 2), "hipblaslt_TFLOP/s": round(fl / us_lib / 1e6, 1),
+                     "vs_hipblaslt": round(us / us_lib, 3)}
+        del a, w, wt, c, c2, ws
+    torch.cuda.empty_cache()
+    return {"shapes": out,
+            "timing": "each form's calls captured into one HIP graph; HIP events on the replay stream, mean per call",
+            "note": "torch.mm in fp16 dispatches to hipBLASLt on this image; weights [K, N] contiguous for it"}
 
 
 def cpu_baseline(target_s):
@@ -752,7 +829,8 @@ def main():
                "serve": lambda: serve_mixed_7b(dev, args.serve_steps),
                "sampling": lambda: sampling_bs128(dev, args.sampling_calls),
                "ops": lambda: ops_small_m(dev, args.ops_calls),
-               "fp16": lambda: wkv_fp16_family(dev, args.fp16_steps)}.get(args.only)
+               "fp16": lambda: wkv_fp16_family(dev, args.fp16_steps),
+               "gemm7b": lambda: gemm_7b_shapes(dev)}.get(args.only)
         if run is None:  # "c1": the config-1 step alone (the sections below are skipped)
             args.model_steps = args.prefill_calls = args.serve_steps = 0
             args.sampling_calls = args.ops_calls = args.fp16_steps = 0
@@ -910,6 +988,7 @@ def main():
         log("fp16-state WKV done")
     if args.serve_steps > 0 and not args.eager:
         result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
+        result["serve_mixed_7b"]["gemm_shapes_vs_hipblaslt"] = gemm_7b_shapes(dev)
         log("config 4 mixed step done")
     if args.sampling_calls > 0 and not args.eager:
         result["sampling_bs128"] = sampling_bs128(dev, args.sampling_calls)

@@ -83,6 +83,7 @@ def test_pack_kn_equals_pack_of_transpose(gpu):
 # (M, N, K): each line exercises one tile configuration of the launcher
 CONFIG_SHAPES = [
     (128, 65536, 128),   # >= 1024 tiles of 64x64: 128x64 tiles, 4 waves
+    (64, 65536, 256),    # the same with one row block half empty
     (128, 8192, 256),    # 64x64 tiles, KS 2
     (128, 4096, 128),    # 64x64 tiles, KS 1
     (128, 2048, 512),    # 32x32 tiles, KS 4
@@ -112,6 +113,22 @@ def test_frag_gemm_vs_oracle(gpu, M, N, K):
     ref, abs_sum = R.gemm(a, w, "nk")
     check(torch.from_numpy(dense[:M, :N].copy()), ref, ACC * abs_sum, f"frag {M}x{N}x{K}")
     assert not dense[:M, N:].any()  # pad columns = epilogue(0) = 0
+
+
+def test_frag_gemm_head_rows_do_not_depend_on_batch(gpu):
+    """Each wave takes the same k blocks and the wave partials are added in the same order
+    whatever the batch, so the first 64 rows of the M = 128 head product equal the M = 64
+    product bit for bit."""
+    from vkwr_amd import capi
+    N, K = 65536, 2048
+    a, w = h(128, K), h(N, K, scale=0.05)
+    pw = pack(w, gpu, N, K)
+    c128 = torch.empty(128, N, dtype=torch.float16, device=gpu)
+    c64 = torch.empty(64, N, dtype=torch.float16, device=gpu)
+    capi.frag_gemm([capi.frag_problem(pack(a, gpu, 128, K), pw, c128, 128, N, K)])
+    capi.frag_gemm([capi.frag_problem(pack(a[:64], gpu, 64, K), pw, c64, 64, N, K)])
+    torch.cuda.synchronize()
+    assert torch.equal(c128[:64], c64)
 
 
 @pytest.mark.parametrize("epi", ["relu2", "tanh", "sigmoid"])
