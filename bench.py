@@ -575,7 +575,7 @@ def ops_small_m(dev, calls, warmup=3):
     vfc = copies((Fr, Cr))
     us = timed(lambda i: MX.cmix_sparse_down_relu_rows(Mr, 1, Cr, Fr, pre, vfc[i % len(vfc)]), calls)
     out["m128_cmix_sparse_down_relu_rows_C2048_F8192"] = {
-        "us": round(us, 2), "note": "[K,N] value_fc: each MFMA fragment gathered with 2-byte LDS reads"}
+        "us": round(us, 2), "note": "[K,N] value_fc: each workgroup streams 128-byte pieces of 4 KiB k rows"}
     del vfc
     torch.cuda.empty_cache()
     return {

@@ -399,6 +399,33 @@ def test_big_gemm_batch_with_empty_problem_and_oracle(gpu):
 
 
 @pytest.mark.parametrize("M,K,N", [
+    (128, 1024, 8192),   # 64x64 tiles for both layouts (256 tiles)
+    (64, 512, 16384),    # the same with one row tile
+    (100, 2048, 8200),   # ragged M and N
+])
+def test_small_m_kn_fragments_equal_nk_bitwise(gpu, M, K, N):
+    """Where both weight layouts get the same 64x64 tiles of the small-M kernel, its [K,N]
+    fragments (transposing LDS reads) and [N,K] fragments (plain 16-byte reads) feed the
+    matrix cores the same operand values in the same lanes and order, so the two layouts of
+    one weight give the same bits (a wrong lane layout of the transposing read would not).
+    The other [K,N] shapes are checked against the oracle in test_gemm_vs_oracle."""
+    from vkwr_amd import capi
+    g = torch.Generator(device=gpu).manual_seed(M + K + N)
+    a = torch.randn(M, K, device=gpu, generator=g).half()
+    w = (torch.randn(N, K, device=gpu, generator=g) * 0.02).half()
+    out = []
+    for b, layout in ((w, capi.GEMM_B_NK), (w.t().contiguous(), capi.GEMM_B_KN)):
+        c = torch.full((M, N), float("nan"), dtype=torch.float16, device=gpu)
+        p = [capi.gemm_problem(a, b, c, b_layout=layout, a_act=capi.ACT_RELU_SQUARE)]
+        ws = torch.empty(max(capi.gemm_workspace_bytes(p), 1), dtype=torch.uint8, device=gpu)
+        capi.gemm(p, ws)
+        out.append(c)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out[0]).any()
+    assert torch.equal(out[0], out[1])
+
+
+@pytest.mark.parametrize("M,K,N", [
     (1024, 16384, 2048),   # 32 tiles, long K: every tile split into 8 k-parts
     (2304, 16384, 4096),   # the 7B FFN value shape: 144 tiles of 256 stages, layered split
                            # (144 stages per CU: [0, 144) of every tile, [144, 256) of 112 tiles

@@ -941,7 +941,7 @@ __global__ __launch_bounds__(256) void gemm_big_fixup_kernel(Batch bt, BigPlan p
 // 128-byte rows (64 k of a row is one cache line), chunk c of row r landing at slot
 // r*8 + (c ^ ((r >> 1) & 7)) so that the fragment reads (ds_read_b128, 8 consecutive k
 // of one row per lane) are conflict-free.  A [K,N] weight is staged as k-rows of 64
-// columns and its fragments gathered with 2-byte LDS reads (8 per fragment).  The wave
+// columns and its fragments read with the transposing LDS read (two per fragment).  The wave
 // issues the next block's DMA before computing on the current one; the waits are
 // explicit, the DMA being invisible to the compiler.  After the loop the 4 wave
 // partials are added in wave order through LDS and each thread finishes 8 consecutive
@@ -1057,12 +1057,28 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         if constexpr (kKN) {
-          const int n = 32 * j + lr, cn = n >> 3, e0 = n & 7;
+          // gfx950's transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group,
+          // element t of lane j's result is element j % 4 of the 8 bytes that lane 4t + j/4
+          // of the group read.  Each lane reads 4 consecutive columns of one k row (lane s of
+          // group g: k row k0 + s/4, columns n0 + 4 (s % 4) ..), so lane j receives 4
+          // consecutive k of column n0 + j; two reads give the 8 k of an MFMA operand.
+          // Group g of the wave: columns n0 = 32 j + 16 (g & 1), k half g >> 1 (the
+          // 32x32x16 operand's lane layout).
+          const int grp = lane >> 4, sl = lane & 15;
+          const int n = 32 * j + 16 * (grp & 1) + 4 * (sl & 3), cn = n >> 3, e0 = n & 7;
+          typedef short sv4 __attribute__((ext_vector_type(4)));
+          sv4 part[2];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int r = 16 * kk + 8 * lh + e;  // k row of the block
-            fb[j][e] = sb[(r * 8 + (cn ^ ((r >> 1) & 7))) * 8 + e0];
+          for (int hf = 0; hf < 2; ++hf) {
+            const int r = 16 * kk + 8 * (grp >> 1) + 4 * hf + (sl >> 2);  // k row of the block
+            part[hf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (VK_LDS sv4*)((VK_LDS _Float16*)sb + (r * 8 + (cn ^ ((r >> 1) & 7))) * 8 + e0));
           }
+          // (one shuffle: assigned element by element, the fragment was compiled into copies of
+          // element 0 of each read)
+          typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+          fb[j] = __builtin_shufflevector(__builtin_bit_cast(hv4, part[0]), __builtin_bit_cast(hv4, part[1]), 0, 1,
+                                          2, 3, 4, 5, 6, 7);
         } else {
           const int r = 32 * j + lr;
           fb[j] = *reinterpret_cast<const hv8*>(sb + (r * 8 + (ch ^ ((r >> 1) & 7))) * 8);
