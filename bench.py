@@ -407,10 +407,12 @@ def wkv_fp16_family(dev, steps, seq_calls=20, warmup=5):
         "fp16_TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
         "calls": seq_calls,
         "workload": "B=8, T=1024, H=32, fp16 state, inputs drawn as in config 0; 256 (sequence, head) "
-                    "chains of 1024 dependent tokens (latency-bound: 256 waves on 256 CUs)"}
+                    "chains of 1024 dependent tokens (latency-bound: 256 waves on 1024 SIMDs)",
+        "kernel": "wkv7_fp16_seq_kernel<false>: T > 1 with at most 4 x CUs chains"}
     del r, w, k, v, a, b, st, yp
     torch.cuda.empty_cache()
-    out["kernel"] = "wkv7_fp16_kernel<false> (vkwr_amd/csrc/wkv.hip): one wave64 per (sequence, head)"
+    out["kernel"] = ("wkv7_fp16_kernel<false> (T = 1) and wkv7_fp16_seq_kernel<false> (T > 1, few chains), "
+                     "vkwr_amd/csrc/wkv.hip: one wave64 per (sequence, head)")
     out["timing"] = "decode: HIP graph of the steps, HIP events on the replay stream; prefill: eager calls"
     return out
 

@@ -451,7 +451,11 @@ def test_rows_kernel_unaligned_inputs_match_oracle(gpu, T):
 
 # ---------------------------------------------------------------- fp16 family
 
-FP16_CASES = [(1, 1, 1), (1, 4, 1), (2, 8, 2), (4, 4, 4), (1, 16, 2), (3, 7, 3)]
+# T > 1 with at most 4 x CUs (sequence, head) chains runs the latency-scheduled sequence
+# kernel (two tokens per loop trip, a trailing odd token); 33 x 32 chains run the
+# one-wave-per-chain kernel that T = 1 uses.  Both must give the oracle's bits.
+FP16_CASES = [(1, 1, 1), (1, 4, 1), (2, 8, 2), (4, 4, 4), (1, 16, 2), (3, 7, 3),
+              (1, 2, 1), (2, 3, 2), (2, 64, 4), (33, 3, 32)]
 
 
 @pytest.mark.parametrize("variant", ["seq", "seq_w0", "one", "one_w0", "legacy_seq", "legacy_one"])

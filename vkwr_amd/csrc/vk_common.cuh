@@ -28,13 +28,13 @@ constexpr float kTwoNeg41 = 4.547473508864641e-13f;
 // 2^x from correctly rounded operations only: range reduction by rint, the
 // degree-7 Taylor polynomial of 2^f = e^{f ln 2} on |f| <= 1/2 in Horner form
 // with FMA, then an exact power-of-two scale.  Max relative error ~6e-8.
-// Results below 2^-126 return 0 (the decay only adds them to 1).
+// Results below 2^-126 return 0 (the decay only adds them to 1).  Written without
+// branches (the special cases are selected at the end, from the same arithmetic
+// on a clamped argument), so that it can be scheduled among other work.
 __device__ __forceinline__ float exp2_det(float x) {
-  if (x != x) return x;
-  if (x >= 128.0f) return __builtin_huge_valf();
-  if (x < -126.0f) return 0.0f;
-  const float n = __builtin_rintf(x);
-  const float f = x - n;
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -127.0f), 128.0f);  // NaN -> -127 (replaced below)
+  const float n = __builtin_rintf(xc);
+  const float f = xc - n;
   float p = 1.525273380405984e-05f;
   p = __builtin_fmaf(p, f, 1.5403530393381608e-04f);
   p = __builtin_fmaf(p, f, 1.3333558146428443e-03f);
@@ -43,7 +43,10 @@ __device__ __forceinline__ float exp2_det(float x) {
   p = __builtin_fmaf(p, f, 2.402265069591007e-01f);
   p = __builtin_fmaf(p, f, 6.931471805599453e-01f);
   p = __builtin_fmaf(p, f, 1.0f);
-  return __builtin_ldexpf(p, (int)n);
+  float r = __builtin_ldexpf(p, (int)n);
+  r = x < -126.0f ? 0.0f : r;
+  r = x >= 128.0f ? __builtin_huge_valf() : r;
+  return x != x ? x : r;
 }
 
 // Per-channel decay d = exp(-e^{-1/2} * sigmoid(w)), written in the reference's

@@ -1300,6 +1300,188 @@ __global__ __launch_bounds__(64) void wkv7_fp16_kernel(Fp16Args p) {
   }
 }
 
+// The same recurrence for T > 1 when the (sequence, head) chains are few (at most one
+// wave per SIMD; config 2's shape has 256), scheduled for a lone wave whose latency nothing
+// else hides.  The arithmetic and the order of every sum are wkv7_fp16_kernel's; what moves
+// is when each part runs:
+//  - token t+1's sa chain (sum over columns of a[j] * s[j] with the state just updated)
+//    runs inside token t's update loop, column by column, beside token t's y chain, so the
+//    two dependent chains overlap instead of the sa chain running alone before the update;
+//  - the loop body has no branch (token indices past the end are clamped and the values
+//    they stage are never used), so the next token's decay (two exp2 and a division) is
+//    scheduled among the chains' FMAs;
+//  - inputs are fetched from global memory three tokens ahead and staged in LDS two ahead.
+template <bool kLegacy>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void wkv7_fp16_seq_kernel(
+    Fp16Args p) {
+  __shared__ f4 st[512];  // one head's fp16 state (8 KiB); then two buffers of token vectors
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const int T = p.T;
+  const size_t tok0 = (size_t)bi * T * p.C + (size_t)h * kHead + lane;
+  _Float16* S = p.state + (size_t)bh * (kHead * kHead);
+
+  const int sub = lane & 7;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int row = 8 * c + (lane >> 3);
+    const int q = sub ^ ((row >> 1) & 7);
+    dma16(S + row * kHead + q * 8, &st[c * 64]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int sw = (lane >> 1) & 7;
+  h2 s[32];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const f4 x = st[lane * 8 + (q ^ sw)];
+    const h2* hx = reinterpret_cast<const h2*>(&x);
+    s[4 * q + 0] = hx[0];
+    s[4 * q + 1] = hx[1];
+    s[4 * q + 2] = hx[2];
+    s[4 * q + 3] = hx[3];
+  }
+  __syncthreads();
+
+  const uint32_t el = (uint32_t)p.elapsed[bi];
+  const uint32_t chan = (uint32_t)(h * kHead + lane);
+  float w0f = 0.0f;
+  if (!kLegacy && p.w0 != nullptr) w0f = (float)p.w0[chan];
+  auto wdelta = [&](_Float16 xw, int t) {
+    float wf = (float)xw;
+    uint32_t phase;
+    if constexpr (kLegacy) {
+      phase = el + (uint32_t)t;
+    } else {
+      if (p.w0 != nullptr) wf = wf + w0f;
+      phase = el + chan + (uint32_t)t;
+    }
+    return w_delta(wf, phase);
+  };
+  struct Tok {
+    _Float16 r, w, k, v, a, b;
+  };
+  auto fetch = [&](int t) {
+    const size_t o = tok0 + (size_t)(t < T ? t : T - 1) * p.C;
+    return Tok{p.r[o], p.w[o], p.k[o], p.v[o], p.a[o], p.b[o]};
+  };
+  _Float16* vec = reinterpret_cast<_Float16*>(st);
+  auto stage = [&](int buf, const Tok& x, _Float16 wd) {
+    _Float16* vb = vec + buf * (5 * kHead);
+    vb[lane] = x.r;
+    vb[kHead + lane] = wd;
+    vb[2 * kHead + lane] = x.k;
+    vb[3 * kHead + lane] = x.a;
+    vb[4 * kHead + lane] = x.b;
+  };
+
+  const Tok x0 = fetch(0), x1 = fetch(1);
+  Tok x2 = fetch(2);
+  stage(0, x0, wdelta(x0.w, 0));
+  stage(1, x1, wdelta(x1.w, 1));
+  _Float16 v_cur = x0.v, v_next = x1.v;
+  __syncthreads();
+  // token 0's sa chain
+  _Float16 sa;
+  {
+    const h2* A = reinterpret_cast<const h2*>(vec + 3 * kHead);
+    h2 sa2 = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      if constexpr (kLegacy) {
+        sa2 = sa2 + A[m] * s[m];
+      } else {
+        sa2 = __builtin_elementwise_fma(A[m], s[m], sa2);
+      }
+    }
+    sa = sa2.x + sa2.y;
+  }
+
+  // one token: xs holds token t+2's inputs (fetched an iteration ago), xl receives t+3's
+  auto token = [&](int t, const Tok& xs, Tok& xl) {
+    xl = fetch(t + 3);
+    const int cb = t & 1;
+    const h2* V = reinterpret_cast<const h2*>(vec + cb * (5 * kHead));
+    const h2* An = reinterpret_cast<const h2*>(vec + (cb ^ 1) * (5 * kHead) + 3 * kHead);
+    const _Float16 wd2 = wdelta(xs.w, t + 2);
+    const h2 sav = {sa, sa};
+    const h2 vv = {v_cur, v_cur};
+    h2 y2 = {(_Float16)0.0f, (_Float16)0.0f};
+    h2 sn2 = {(_Float16)0.0f, (_Float16)0.0f};
+    // all five token vectors into registers at once (broadcast LDS reads), so that no FMA
+    // of the chains waits on an LDS read issued just before it
+    h2 Rv[32], Wv[32], Kv[32], Bvv[32], Av[32];
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      Rv[m] = V[m];
+      Wv[m] = V[32 + m];
+      Kv[m] = V[64 + m];
+      Bvv[m] = V[128 + m];
+      Av[m] = An[m];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      const h2 R = Rv[m], W = Wv[m], K = Kv[m], Bv = Bvv[m];
+      if constexpr (kLegacy) {
+        const h2 t1 = s[m] * W;
+        const h2 t2 = K * vv;
+        const h2 t3 = t1 + t2;
+        const h2 t4 = sav * Bv;
+        const h2 t5 = t3 + t4;
+        s[m] = s[m] + t5;
+        y2 = y2 + s[m] * R;
+        sn2 = sn2 + Av[m] * s[m];
+      } else {
+        const h2 in1 = __builtin_elementwise_fma(sav, Bv, s[m]);
+        const h2 in2 = __builtin_elementwise_fma(K, vv, in1);
+        s[m] = __builtin_elementwise_fma(s[m], W, in2);
+        y2 = __builtin_elementwise_fma(s[m], R, y2);
+        sn2 = __builtin_elementwise_fma(Av[m], s[m], sn2);
+      }
+    }
+    p.y[tok0 + (size_t)t * p.C] = y2.x + y2.y;
+    sa = sn2.x + sn2.y;
+    __builtin_amdgcn_sched_barrier(0);  // keeps the next token's sa chain among these FMAs
+    // every lane has read buffer cb (single-wave workgroup): token t+2 replaces token t
+    __syncthreads();
+    stage(cb, xs, wd2);
+    v_cur = v_next;
+    v_next = xs.v;
+    __syncthreads();
+  };
+  // two tokens per trip, the two register sets swapping roles, so that no copy of a set
+  // waits for loads issued in the same token
+  Tok x3;
+  int t = 0;
+  for (; t + 1 < T; t += 2) {
+    token(t, x2, x3);
+    token(t + 1, x3, x2);
+  }
+  if (t < T) token(t, x2, x3);
+
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    f4 x;
+    h2* hx = reinterpret_cast<h2*>(&x);
+    hx[0] = s[4 * q + 0];
+    hx[1] = s[4 * q + 1];
+    hx[2] = s[4 * q + 2];
+    hx[3] = s[4 * q + 3];
+    st[lane * 8 + (q ^ sw)] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int row = 8 * c + (lane >> 3);
+    const int q = sub ^ ((row >> 1) & 7);
+    *reinterpret_cast<f4*>(S + row * kHead + q * 8) = st[c * 64 + lane];
+  }
+}
+
 __global__ __launch_bounds__(256) void advance_i32_kernel(int32_t* x, int64_t n, int32_t amount) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) x[i] = (int32_t)((uint32_t)x[i] + (uint32_t)amount);
@@ -1453,10 +1635,14 @@ static int launch_fp16(const char* fn, bool legacy, int B, int T, int C, int H, 
              reinterpret_cast<const _Float16*>(w0), reinterpret_cast<const _Float16*>(k),
              reinterpret_cast<const _Float16*>(v), reinterpret_cast<const _Float16*>(a),
              reinterpret_cast<const _Float16*>(b), reinterpret_cast<_Float16*>(y), elapsed_t};
+  // T > 1 with at most one wave per SIMD: the latency-scheduled form (same arithmetic)
+  const bool seq = T > 1 && (int64_t)B * H <= 4 * (int64_t)device_cus();
   if (legacy) {
-    hipLaunchKernelGGL(wkv7_fp16_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+    if (seq) hipLaunchKernelGGL(wkv7_fp16_seq_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL(wkv7_fp16_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
   } else {
-    hipLaunchKernelGGL(wkv7_fp16_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+    if (seq) hipLaunchKernelGGL(wkv7_fp16_seq_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL(wkv7_fp16_kernel<false>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
   }
   return check_launch(fn);
 }
