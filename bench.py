@@ -292,7 +292,21 @@ def prefill_c2(dev, steps, warmup=100):
     # waves x 80 v_mfma_f32_16x16x4_f32 (2048 flops each), 4 x 16 for the chunk matrices, 36 for
     # W^T (includes the W^T power series and padded tokens, so it is not a roofline numerator)
     mfma_flops = Bp * H * ((Tp + 15) // 16) * (4 * 80 + 4 * 16 + 36) * 2048
-    del r, w, k, v, a, b, pool, y
+    # the reference-order (bit-exact) form of the same prefill: wkv_forward_seq_fp32 on a
+    # dense state (one chain per dot product, token by token)
+    st = pool[slots.long()].clone()
+    seq = lambda: ops.wkv_forward_seq_fp32(Bp, Tp, C, H, st, r, w, k, v, a, b)  # noqa: E731
+    for _ in range(5):
+        seq()
+    torch.cuda.synchronize()
+    seq_calls = 10
+    ev0.record()
+    for _ in range(seq_calls):
+        seq()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_seq = ev0.elapsed_time(ev1) / seq_calls
+    del r, w, k, v, a, b, pool, y, st
     torch.cuda.empty_cache()
     tflops = alg_flops / (ms * 1e-3) / 1e12
     return {
@@ -318,6 +332,11 @@ def prefill_c2(dev, steps, warmup=100):
                                      "padded tokens and the W^T power series included); not a roofline"},
         "kernel": "wkv7_fp32_chunk_kernel (one 512-lane workgroup per (sequence, head): 4 state waves + 4 "
                   "waves preparing later chunks; 16-token chunks on v_mfma_f32_16x16x4_f32)",
+        "reference_order_seq_fp32": {
+            "ms_per_call": round(ms_seq, 4), "tokens_per_s": round(Bp * Tp / (ms_seq * 1e-3), 1),
+            "ns_per_token_step": round(ms_seq * 1e6 / Tp, 1), "calls": seq_calls,
+            "what": "wkv_forward_seq_fp32 on a dense [8,32,64,64] state, same inputs: the bit-exact "
+                    "reference-order path (wkv7_fp32_seq_lat_kernel, one wave per (sequence, head))"},
     }
 
 

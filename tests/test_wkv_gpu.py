@@ -109,6 +109,8 @@ FP32_CASES = [
     (1, 33, 2, "realistic", 0.1),    # row-split kernel: two full 16-token chunks + a 1-token tail
     (2, 47, 3, "baseline", 0.1),     # ... odd tail inside the last chunk
     (16, 20, 32, "realistic", 0.1),  # B*H = 512: one workgroup per (sequence, head), 2 rows per lane
+    (1, 2, 1, "realistic", 0.1),     # modes 1-3: the latency-scheduled kernel's shortest sequence
+    (33, 3, 32, "realistic", 0.1),   # ... B*H = 1056 > 4 x CUs: the many-waves kernel
 ]
 
 

@@ -232,6 +232,132 @@ __global__ __launch_bounds__(64) void wkv7_fp32_seq_kernel(Fp32Args p) {
   store_state_fp32(S, st, s, lane);
 }
 
+// The same recurrence and order for T > 1 when the (sequence, head) chains are few (at most
+// one wave per SIMD), scheduled for a lone wave whose latency nothing else hides.  Every
+// value is computed as in wkv7_fp32_seq_kernel; what moves is when:
+//  - token t+1's sa chain (sum over j of s[j] * a_{t+1}[j], in j order, on the state just
+//    updated by token t) runs inside token t's update loop beside the y chain, column by
+//    column, instead of alone at the start of token t+1;
+//  - the token vectors are read from LDS eight columns ahead of their use (the compiler
+//    would otherwise issue each read just before the FMAs that consume it);
+//  - the loop body has no branch (token indices past the end are clamped, the values
+//    they stage are never used), the decay of token t+2 is computed among the FMAs, and
+//    inputs are fetched three tokens ahead, two tokens per loop trip with two register sets.
+template <bool kSlots>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void wkv7_fp32_seq_lat_kernel(
+    Fp32Args p) {
+  __shared__ f4 st[512];
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int bi = bh / p.H;
+  const int h = bh - bi * p.H;
+  const int T = p.T;
+  const size_t tok0 = (size_t)bi * T * p.C + (size_t)h * kHead + lane;
+  float* S = state_block<kSlots>(p, bi, h);
+  if (S == nullptr) {
+    for (int t = 0; t < T; ++t) p.y[tok0 + (size_t)t * p.C] = (_Float16)__builtin_nanf("");
+    return;
+  }
+  struct Tok {
+    _Float16 r, w, k, v, a, b;
+  };
+  auto fetch = [&](int t) {
+    const size_t o = tok0 + (size_t)(t < T ? t : T - 1) * p.C;
+    return Tok{p.r[o], p.w[o], p.k[o], p.v[o], p.a[o], p.b[o]};
+  };
+  const Tok x0 = fetch(0), x1 = fetch(1);
+  Tok x2 = fetch(2);
+  float s[kHead];
+  load_state_fp32(S, st, s, lane);
+  float* vec = reinterpret_cast<float*>(st);
+  auto stage = [&](int buf, const Tok& x, float d) {
+    float* vb = vec + buf * (5 * kHead);
+    vb[lane] = (float)x.r;
+    vb[kHead + lane] = d;
+    vb[2 * kHead + lane] = (float)x.k;
+    vb[3 * kHead + lane] = (float)x.a;
+    vb[4 * kHead + lane] = (float)x.b;
+  };
+  stage(0, x0, decay((float)x0.w));
+  stage(1, x1, decay((float)x1.w));
+  float v_cur = (float)x0.v, v_next = (float)x1.v;
+  __syncthreads();
+  float sa = 0.0f;
+  {
+    const f4* A4 = reinterpret_cast<const f4*>(vec) + 48;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const f4 a4 = A4[q];
+      sa = __builtin_fmaf(s[4 * q + 0], a4.x, sa);
+      sa = __builtin_fmaf(s[4 * q + 1], a4.y, sa);
+      sa = __builtin_fmaf(s[4 * q + 2], a4.z, sa);
+      sa = __builtin_fmaf(s[4 * q + 3], a4.w, sa);
+    }
+  }
+
+  // one token: xs holds token t+2's inputs (fetched an iteration ago), xl receives t+3's
+  auto token = [&](int t, const Tok& xs, Tok& xl) {
+    xl = fetch(t + 3);
+    const int cb = t & 1;
+    const f4* V4 = reinterpret_cast<const f4*>(vec + cb * (5 * kHead));
+    const f4* An4 = reinterpret_cast<const f4*>(vec + (cb ^ 1) * (5 * kHead)) + 48;
+    const float vi = v_cur;
+    float acc = 0.0f, sn = 0.0f, d2 = 0.0f;
+    // group g: columns 8g .. 8g+7 (two f4 of each vector)
+    f4 R[2][2], D[2][2], K[2][2], Bv[2][2], A[2][2];
+    auto rd = [&](int g, int set) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int q = 2 * g + u;
+        R[set][u] = V4[q];
+        D[set][u] = V4[16 + q];
+        K[set][u] = V4[32 + q];
+        Bv[set][u] = V4[64 + q];
+        A[set][u] = An4[q];
+      }
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int set = g & 1;
+      if (g + 1 < 8) rd(g + 1, set ^ 1);
+      if (g == 2) d2 = decay((float)xs.w);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 8 * g + 4 * u + e;
+          float x = s[j] * D[set][u][e];
+          x = __builtin_fmaf(sa, Bv[set][u][e], x);
+          x = __builtin_fmaf(K[set][u][e], vi, x);
+          s[j] = x;
+          acc = __builtin_fmaf(x, R[set][u][e], acc);
+          sn = __builtin_fmaf(x, A[set][u][e], sn);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("" : "+v"(acc));
+    p.y[tok0 + (size_t)t * p.C] = (_Float16)acc;
+    sa = sn;
+    // every lane has read buffer cb (single-wave workgroup): token t+2 replaces token t
+    __syncthreads();
+    stage(cb, xs, d2);
+    v_cur = v_next;
+    v_next = (float)xs.v;
+    __syncthreads();
+  };
+  Tok x3;
+  int t = 0;
+  for (; t + 1 < T; t += 2) {
+    token(t, x2, x3);
+    token(t + 1, x3, x2);
+  }
+  if (t < T) token(t, x2, x3);
+  __syncthreads();
+  store_state_fp32(S, st, s, lane);
+}
+
 // ---- row-split prefill (T > 1): one 256-lane workgroup per (sequence, head).
 //
 // The rows of the state are independent recurrences; only the two per-row dot
@@ -1044,6 +1170,9 @@ void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
       hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 1>), dim3(2 * B * p.H), dim3(256), 0, stream, ra);
     else
       hipLaunchKernelGGL((wkv7_fp32_rows_kernel<kSlots, 2>), dim3(B * p.H), dim3(256), 0, stream, ra);
+  } else if ((int64_t)B * p.H <= 4 * (int64_t)device_cus()) {
+    // few chains: at most one wave per SIMD, the latency-scheduled form (same bits)
+    hipLaunchKernelGGL(wkv7_fp32_seq_lat_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   } else {
     hipLaunchKernelGGL(wkv7_fp32_seq_kernel<kSlots>, dim3(B * p.H), dim3(64), 0, stream, p);
   }
