@@ -432,7 +432,8 @@ def test_small_m_kn_fragments_equal_nk_bitwise(gpu, M, K, N):
                            # whole, the other 32 in 16-stage pieces)
     (2304, 8192, 4096),    # 144 tiles of 128 stages: per 72, layered with 8-stage pieces
     (4096, 16384, 6400),   # 400 tiles: 256 whole, the other 144 layered (tile indices offset by 256)
-    (2304, 4096, 16384),   # the 7B FFN key shape: 2 whole rounds + a 64-tile tail split in 4
+    (2304, 4096, 8192),    # 288 tiles: one whole round + a 32-tile tail split in 6
+    (2304, 4096, 16384),   # the 7B FFN key shape: 768 whole 192-row tiles (three rounds, no split)
 ])
 def test_big_gemm_split_tail(gpu, M, K, N):
     """Tail tiles split into k-parts or balanced pieces (fp32 partials, ordered fixup): against the row-major

@@ -47,7 +47,7 @@ def _run_ws(probs, gpu):
     # (m, n, k, epilogue, problems, [K,N] weights): a K-split batch, then a smaller one
     [(128, 1024, 8192, capi.EPI_NONE, 1, False), (40, 1024, 2048, capi.EPI_BIAS, 3, False)],
     # the large-M kernel's split last round (stream-K partials), then a smaller split batch
-    [(500, 4096, 1024, capi.EPI_RELU_SQUARE, 1, False), (64, 1024, 4096, capi.EPI_NONE, 2, False)],
+    [(500, 4096, 2048, capi.EPI_RELU_SQUARE, 1, False), (64, 1024, 4096, capi.EPI_NONE, 2, False)],
     # the GEMV kernel's K parts ([K,N] weights, M <= 4), then a smaller one
     [(3, 4096, 4096, capi.EPI_NONE, 1, True), (1, 2048, 2048, capi.EPI_BIAS, 2, True)],
 ])

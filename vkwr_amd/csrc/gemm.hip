@@ -1602,9 +1602,11 @@ int64_t plan(Batch& bt, Config cfg, int target_wgs) {
 // Tiles (256x256) of a large-M batch and its stream-K split; returns the workspace bytes.
 // The plan for tile rows BM: tile fields of the batch's problems, and the split of the last
 // round; returns its estimated time (us).  Time model: a tile's k-stage ~1.7 us when every CU
-// is busy (0.86 of that for 192 rows, as measured: the operand bytes per MAC are higher), plus
-// ~2 stages of prologue and epilogue per workgroup; a split tile costs its S fp32 partials
-// written and read back at ~5 TB/s.  Batches of unequal K (the low-rank outputs: K = 512 and
+// is busy (0.80 of that for 192 rows: 0.77 measured on the 7B FFN key, 768 tiles in three
+// whole rounds against 576 in two rounds and a split tail; the operand bytes per MAC are
+// higher), plus ~2 stages of prologue and epilogue per workgroup; a split tile costs its S
+// fp32 partials written and read back at ~5 TB/s, and a split plan the ramp of its two
+// extra launches (~3 us each).  Batches of unequal K (the low-rank outputs: K = 512 and
 // 128, their time in the epilogue stores) are scored by how fully the last round of tiles
 // fills the CUs instead (returned as a negative fill fraction).
 double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
@@ -1627,7 +1629,7 @@ double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
   }
   pl = BigPlan{BM, T, 0, 1, 0, 0, 0, 0, nullptr};
   const int G = device_cus();
-  const double stage = 1.7 * (BM == 192 ? 0.86 : 1.0), over = 2.0 * stage;
+  const double stage = 1.7 * (BM == 192 ? 0.80 : 1.0), over = 2.0 * stage, split_launches = 6.0;
   if (!uniform_k) return -(double)T / ((double)((T + G - 1) / G) * G);
   const int nst = k_all / kBigBK;
   const double rounds_whole = (double)((T + G - 1) / G);
@@ -1638,7 +1640,8 @@ double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
   int best_s = 1;
   for (int S = 2; S <= 8 && nst / S >= 8; ++S) {
     const double rounds = (double)((R * S + G - 1) / G);
-    const double t = full + rounds * ((double)nst / S * stage + over) + (double)R * S * 2 * BM * kBigBM * 4 / 5e6;
+    const double t = full + rounds * ((double)nst / S * stage + over) + (double)R * S * 2 * BM * kBigBM * 4 / 5e6 +
+                     split_launches;
     if (t < best) {
       best = t;
       best_s = S;
@@ -1652,7 +1655,8 @@ double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
     int g = std::gcd(b, L);
     if (L > 0 && b > 0 && g >= 8) {
       const int R3 = R - (G - R), pieces = R + (G - R) + R3 * (L / g);
-      const double t = full + per * stage + (2 + b / g) * over + (double)pieces * 2 * BM * kBigBM * 4 / 5e6;
+      const double t =
+          full + per * stage + (2 + b / g) * over + (double)pieces * 2 * BM * kBigBM * 4 / 5e6 + split_launches;
       if (t < best) {
         best = t;
         lay_per = per;
