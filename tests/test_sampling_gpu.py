@@ -62,6 +62,10 @@ CASES = [
     (4, 65532, 1.0, 7, 1.0),          # padding lanes at the end of the row
     (4, 100000, 1.0, 100, 0.9),       # above 65536: scratch-buffer mode
     (2, 1048576, 1.5, -1, 0.5),       # the largest vocabulary allowed
+    # the first window from the lane maxima: q = ceil(top_k / 16) lanes per wave
+    (4, 65536, 1.0, 1024, 1.0),       # q = 64: every lane of every wave
+    (4, 65536, 0.9, 1, 0.5),          # q = 1, with a mass limit
+    (4, 65536, 0.8, 17, 0.99),        # q = 2
 ]
 
 
@@ -89,11 +93,13 @@ def test_untruncated_flat_row(gpu):
     assert _check_draws(toks, logits, 77, 0, 1.0, 0, 1.0) <= 1
 
 
-@pytest.mark.parametrize("V,top_k,top_p", [(65536, 2000, 1.0), (65536, -1, 0.5), (100000, 3000, 0.9)])
+@pytest.mark.parametrize("V,top_k,top_p", [(65536, 2000, 1.0), (65536, -1, 0.5), (100000, 3000, 0.9),
+                                         (65536, 40, 1.0), (65536, 5, 0.9)])
 def test_large_ties(gpu, V, top_k, top_p):
     # a few large logits over a flat floor: the threshold lands on a value shared by
     # tens of thousands of entries, so the kept weight of every tied entry is the
     # compensation share and the search ends over more entries than it compacts
+    # (top_k 40: the lane maxima's window is the whole floor; top_k 5: the 10 peaks tie)
     ops = _ops()
     B = 4
     logits = torch.zeros(B, V)
@@ -105,6 +111,22 @@ def test_large_ties(gpu, V, top_k, top_p):
         # steps of the tied entries are below the margin: near-boundary draws are
         # common here, each one still checked against its CDF interval
         _check_draws(toks, logits, 11, call, 1.0, top_k, top_p)
+
+
+@pytest.mark.parametrize("top_k,top_p", [(40, 1.0), (40, 0.9), (500, 1.0)])
+def test_tied_top_values(gpu, top_k, top_p):
+    # 300 equal largest logits spread over the row, above a random floor: the lane maxima
+    # of every wave include the tied value, so the first window is that single value,
+    # shared by more entries than top_k (kept weights: the compensation share)
+    ops = _ops()
+    B, V = 4, 65536
+    logits = _logits(B, V, 21, scale=1.0)
+    for b in range(B):
+        logits[b, (torch.arange(300) * 211 + 7 * b) % V] = 8.0
+    states = ops.setup_rand(13, B)
+    for call in range(2):
+        toks = ops.temperature_topk_topp(logits.to(gpu), states, 1.0, top_k, top_p).cpu()
+        _check_draws(toks, logits, 13, call, 1.0, top_k, top_p)
 
 
 def test_scratch_mode_uses_last_token(gpu):

@@ -211,9 +211,10 @@ struct SampArgs {
 //
 //   1. u = sf((sf(l) - pen) log2e / temperature); its maximum and minimum  (1 barrier)
 //   2. x = 2^(u - u_max) (so x_max = 1 exactly), S = sum x                 (1 barrier)
-//   3. tau by binary search over float bit patterns: block-wide passes (count and
-//      mass of the entries >= the midpoint, 1 barrier each) until the window
-//      [lo, hi] holds at most kCandCap entries; those are compacted into LDS and
+//   3. tau by binary search over float bit patterns, from a first window [L, 1] whose
+//      lower end comes from the lane maxima when top_k <= 1024 (1 barrier; below);
+//      block-wide passes (count and mass of the entries >= the midpoint, 1 barrier
+//      each) until the window [lo, hi] holds at most kCandCap entries; those are compacted into LDS and
 //      wave 0 continues alone (no barriers) until at most kRankCap remain, which it
 //      ranks directly; wave 0 publishes tau and comp                      (1 barrier)
 //   4. kept weights; lane-order scan; owner lane of the draw; its pick (2 barriers)
@@ -345,7 +346,7 @@ __global__ __launch_bounds__(kSampThreads) void sampling_kernel(SampArgs p) {
 
   // 2. x = 2^(u - umax) (v_exp_f32: weights below 2^-126 of the largest count as 0;
   // padding gives 2^-inf = 0)
-  float s = 0.0f;
+  float s = 0.0f, lane_xmax = 0.0f;
 #pragma unroll
   for (int j = 0; j < nslot; ++j) {
     const float4 u = get(j);
@@ -353,6 +354,7 @@ __global__ __launch_bounds__(kSampThreads) void sampling_kernel(SampArgs p) {
                            __builtin_amdgcn_exp2f(u.z - umax), __builtin_amdgcn_exp2f(u.w - umax));
     put(j, x);
     s += (x.x + x.y) + (x.z + x.w);
+    lane_xmax = fmaxf(lane_xmax, fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w)));
   }
   const float lane_sum = s;
   s = wave_sum(s);
@@ -386,8 +388,57 @@ __global__ __launch_bounds__(kSampThreads) void sampling_kernel(SampArgs p) {
         m_hi1 = M;
       }
     };
+    // Window count: wc = this lane's entries in [lo, hi], at = the lane-order index of its
+    // first one, n = the block total.  Valid while `counted` (lo and hi unchanged since).
+    int wc = 0, at = 0, n = 0;
+    bool counted = false;
+    const auto window_count = [&]() {
+      const float lof = fbits(lo), hif = fbits(hi);
+      wc = 0;
+#pragma unroll
+      for (int j = 0; j < nslot; ++j) {
+        const float4 x = get(j);
+        const float e[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wc += (e[q] >= lof && e[q] <= hif) ? 1 : 0;
+      }
+      const int wincl = wave_incl_scan_i(wc, lane);
+      publish(sh, par, wv, lane, 0.0f, 0.0f, __builtin_amdgcn_readlane(wincl, 63), 0);
+      at = wincl - wc;
+      for (int w = 0; w < wv; ++w) at += sh.ia[par][w];
+      n = sum_ia(sh, par);
+      par ^= 1;
+      counted = true;
+    };
+    if (J > 0 && p.top_k <= kSampThreads) {
+      // A first window from the lane maxima.  In each wave, the q-th largest of its 64 lane
+      // maxima (q = ceil(top_k / 16); one lane per step, so ties count once per lane) is at
+      // or below q distinct entries of the wave; the smallest of the 16 such values, L, has
+      // at least 16 q >= top_k entries at or above it.  So notsmall(L): tau >= L, and the
+      // window [L, 1] usually holds a few hundred entries, where the bisection from the
+      // smallest entry would take three block-wide passes to get below kCandCap.
+      const int q = (p.top_k + kSampWaves - 1) / kSampWaves;
+      float lm = lane_xmax, lw = 0.0f;
+      for (int i = 0; i < q; ++i) {
+        lw = wave_max(lm);
+        const uint64_t hit = ballot(lm == lw);  // nonzero: lw is some lane's value
+        if (lane == (int)__builtin_ctzll(hit)) lm = -1.0f;
+      }
+      publish(sh, par, wv, lane, lw, 0.0f, 0, 0);
+      float L = sh.fa[par][0];
+#pragma unroll
+      for (int w = 1; w < kSampWaves; ++w) L = fminf(L, sh.fa[par][w]);
+      par ^= 1;
+      const uint32_t Lb = __builtin_bit_cast(uint32_t, L);
+      if (L > 0.0f && Lb > lo) {
+        lo = Lb;
+        window_count();
+        cnt_lo = n;  // #(x >= lo); cnt_hi1 = 0 (nothing exceeds 1 = the maximum)
+      }
+    }
     // block-wide passes over every entry
     while (lo < hi && cnt_lo - cnt_hi1 > kCandCap) {
+      counted = false;
       const uint32_t mid = lo + (hi - lo + 1u) / 2u;
       const float v = fbits(mid);
       int c = 0;
@@ -414,21 +465,7 @@ __global__ __launch_bounds__(kSampThreads) void sampling_kernel(SampArgs p) {
     if (lo < hi) {
       // compact the window [lo, hi] (at most kCandCap entries; lo > 0, so padding
       // never falls in it) into LDS in lane order
-      const float lof = fbits(lo), hif = fbits(hi);
-      int wc = 0;
-#pragma unroll
-      for (int j = 0; j < nslot; ++j) {
-        const float4 x = get(j);
-        const float e[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) wc += (e[q] >= lof && e[q] <= hif) ? 1 : 0;
-      }
-      const int wincl = wave_incl_scan_i(wc, lane);
-      publish(sh, par, wv, lane, 0.0f, 0.0f, __builtin_amdgcn_readlane(wincl, 63), 0);
-      int at = wincl - wc;
-      for (int w = 0; w < wv; ++w) at += sh.ia[par][w];
-      const int n = sum_ia(sh, par);
-      par ^= 1;
+      if (!counted) window_count();
 #pragma unroll
       for (int j = 0; j < nslot; ++j) {
         const float4 x = get(j);
