@@ -282,3 +282,59 @@ def test_7b_layer_shape_mixed_step_against_oracle(gpu):
     from vkwr.model_executor import RWKV7Config
     cfg = RWKV7Config(2, 4096, 16384, 128, 128, 96, 480, 65536)
     _mixed_vs_oracle(gpu, cfg, P=2048, Bd=256, Bp=4, T=512, seed=30, state_tol=1e-2)
+
+
+def test_7b_full_depth_mixed_step_decode_rows_against_oracle(gpu):
+    """BASELINE config 4 at full depth (the 7B preset, L=32) on its 2048-slot pool: one step
+    of 256 decode rows + 4 prefill chunks x 512 tokens, the decode rows' logits and states
+    against one reference decode step (the chunks' own reference, 512 sequential full-depth
+    steps, is left to the L=2 test above; here they only have to be finite and leave the
+    untouched slots alone).
+
+    Bound: at 32 layers the fp16 roundings of the intermediates -- the reference's own
+    storage types, which oracle/model_ref reproduces with round_fp16=True -- move the logits
+    by ~0.1 from the float32 composition on these random weights (measured 0.096, max |logit|
+    ~7), so north_star's 5e-2 cannot hold for any fp16 pipeline here, the reference's
+    included.  The engine must stay within 5e-2 or 1.25 x that oracle-to-oracle distance,
+    whichever is larger, of the float32 model (logits, and the same for the state drift
+    relative to max |S|)."""
+    from oracle import model_ref
+    from vkwr_amd import capi
+    from vkwr.model_executor import MixedEngine, RWKV7Config, RWKV7Model, RWKV7State
+    cfg = RWKV7Config.preset("7b")
+    P, Bd, Bp, T = 2048, 256, 4, 512
+    model = RWKV7Model(cfg, gpu, seed=40)
+    state = RWKV7State(cfg, P, gpu, std=0.1, seed=41, layout=capi.WKV_STATE_STD)
+    g = torch.Generator().manual_seed(42)
+    perm = torch.randperm(P, generator=g)
+    sd, sp = perm[:Bd].to(torch.int32), perm[Bd:Bd + Bp].to(torch.int32)
+    td = torch.randint(0, cfg.vocab, (Bd,), generator=g, dtype=torch.int32)
+    tp = torch.randint(0, cfg.vocab, (Bp, T), generator=g, dtype=torch.int32)
+    dl = sd.long().to(gpu)
+    wkv, att, ffn = (t[:, dl].clone() for t in (state.wkv, state.att_shift, state.ffn_shift))
+    probe = [int(perm[-1]), int(perm[-2])]
+    probe0 = state.wkv[:, probe].clone()
+    eng = MixedEngine(model, Bd + Bp * T, max_seqs=Bd + Bp)
+    logits = eng.step(state, decode=(td.to(gpu), sd.to(gpu)), prefill=[(tp.to(gpu), sp.to(gpu))]).float()
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(logits).all())
+    m32 = _f32_model(model)
+    with torch.no_grad():
+        w16, a16, f16 = wkv.clone(), att.clone(), ffn.clone()
+        ref16 = model_ref.decode_step(m32, w16, a16, f16, td.to(gpu), torch.arange(Bd, device=gpu), round_fp16=True)
+        ref = model_ref.decode_step(m32, wkv, att, ffn, td.to(gpu), torch.arange(Bd, device=gpu), round_fp16=False)
+        err = (logits[:Bd] - ref).abs().max().item()
+        err16 = (logits[:Bd] - ref16).abs().max().item()
+        err_16_32 = (ref16 - ref).abs().max().item()
+        s_err = ((state.wkv[:, dl] - wkv).abs().max() / wkv.abs().max()).item()
+        s_err16 = ((state.wkv[:, dl] - w16).abs().max() / w16.abs().max()).item()
+        s_16_32 = ((w16 - wkv).abs().max() / wkv.abs().max()).item()
+        shift_err = max((state.att_shift[:, dl] - att).abs().max().item(),
+                        (state.ffn_shift[:, dl] - ffn).abs().max().item())
+    print(f"7B L=32 decode rows: logits max|ref| {ref.abs().max().item():.3g}; max-abs vs float32 {err:.3g}, "
+          f"vs fp16-rounding oracle {err16:.3g} (the two oracles differ by {err_16_32:.3g}); state max-abs / "
+          f"max|S| {s_err:.3g} ({s_err16:.3g} vs fp16-rounding; oracles {s_16_32:.3g} apart); shift rows "
+          f"max-abs {shift_err:.3g}", flush=True)
+    assert err <= max(TOL, 1.25 * err_16_32), (err, err_16_32)
+    assert s_err <= max(1e-2, 1.25 * s_16_32), (s_err, s_16_32)
+    assert torch.equal(state.wkv[:, probe], probe0)
