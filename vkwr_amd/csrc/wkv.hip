@@ -1313,6 +1313,16 @@ __global__ __launch_bounds__(64) void wkv7_fp16_kernel(Fp16Args p) {
   const size_t tok0 = (size_t)bi * p.T * p.C + (size_t)h * kHead + lane;
   _Float16* S = p.state + (size_t)bh * (kHead * kHead);
 
+  // the first token's inputs, the phase and w0 are requested before the state, so their
+  // latency overlaps the state transfer instead of following it
+  const uint32_t el = (uint32_t)p.elapsed[bi];
+  const uint32_t chan = (uint32_t)(h * kHead + lane);
+  const bool has_w0 = !kLegacy && p.w0 != nullptr;
+  // loaded without a branch (p.r stands in when there is no w0), so no wait follows it here
+  const _Float16 w0h = *(has_w0 ? p.w0 + chan : p.r + tok0);
+  _Float16 xr = p.r[tok0], xw = p.w[tok0], xk = p.k[tok0];
+  _Float16 xv = p.v[tok0], xa = p.a[tok0], xb = p.b[tok0];
+
   const int sub = lane & 7;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -1336,14 +1346,7 @@ __global__ __launch_bounds__(64) void wkv7_fp16_kernel(Fp16Args p) {
   }
   __syncthreads();
 
-  const uint32_t el = (uint32_t)p.elapsed[bi];
-  const uint32_t chan = (uint32_t)(h * kHead + lane);
-  float w0f = 0.0f;
-  if (!kLegacy && p.w0 != nullptr) w0f = (float)p.w0[chan];
-
   _Float16* vec = reinterpret_cast<_Float16*>(st);
-  _Float16 xr = p.r[tok0], xw = p.w[tok0], xk = p.k[tok0];
-  _Float16 xv = p.v[tok0], xa = p.a[tok0], xb = p.b[tok0];
   for (int t = 0; t < p.T; ++t) {
     _Float16* vb = vec + (t & 1) * (5 * kHead);
     float wf = (float)xw;
@@ -1351,7 +1354,7 @@ __global__ __launch_bounds__(64) void wkv7_fp16_kernel(Fp16Args p) {
     if constexpr (kLegacy) {
       phase = el + (uint32_t)t;
     } else {
-      if (p.w0 != nullptr) wf = wf + w0f;
+      if (has_w0) wf = wf + (float)w0h;
       phase = el + chan + (uint32_t)t;
     }
     vb[lane] = xr;
