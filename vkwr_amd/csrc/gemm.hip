@@ -956,7 +956,11 @@ constexpr int kRmBK = 64;
 template <int TM, int TN>
 constexpr int rm_waves() { return TM * TN == 1 ? 8 : 4; }
 
-template <int TM, int TN, bool kKN>
+// kAct: some problem of the batch has an A-operand activation.  Without one the fragment
+// reads of a whole k block have no branch between them and the matrix products, so they are
+// all issued before the first product (with the activation's per-element branches in the
+// loop, each product waited for its own two reads).
+template <int TM, int TN, bool kKN, bool kAct>
 __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batch bt) {
   constexpr int kRmNW = rm_waves<TM, TN>();
   static_assert(!kKN || TN == 2, "[K,N] weights are staged as 128-byte k rows of 64 columns");
@@ -976,7 +980,7 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
   const int split = lt0 / ntiles;  // K part (split-major: the parts of a tile run apart in time)
   const int lt = lt0 - split * ntiles;
   const int m0 = (lt / P.tiles_n) * (32 * TM), n0 = (lt % P.tiles_n) * (32 * TN);
-  const int M = P.m, N = P.n, K = P.k, a_act = P.a_act;
+  const int M = P.m, N = P.n, K = P.k, a_act = kAct ? P.a_act : VKWR_GEMM_ACT_NONE;
   // this workgroup's K range [kbeg, kbeg + klen); klen is a multiple of 8
   const int kbeg = split * P.k_per_split;
   const int klen = min(K - kbeg, P.k_per_split);
@@ -1039,16 +1043,18 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
   auto compute = [&](int buf, int kb) __attribute__((always_inline)) {
     const _Float16* sa = &sm[w][buf][0];
     const _Float16* sb = sa + kA;
+    hv8 fa4[4][TM], fb4[4][TN];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int ch = 2 * kk + lh;
       const bool kin = kb * kRmBK + ch * 8 < klen;
-      hv8 fa[TM], fb[TN];
+      hv8 (&fa)[TM] = fa4[kk];
+      hv8 (&fb)[TN] = fb4[kk];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = 32 * i + lr;
         fa[i] = *reinterpret_cast<const hv8*>(sa + (r * 8 + (ch ^ ((r >> 1) & 7))) * 8);
-        if (a_act != VKWR_GEMM_ACT_NONE) {
+        if (kAct && a_act != VKWR_GEMM_ACT_NONE) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) fa[i][e] = (_Float16)act_in((float)fa[i][e], a_act);
         }
@@ -1084,12 +1090,14 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
           fb[j] = *reinterpret_cast<const hv8*>(sb + (r * 8 + (ch ^ ((r >> 1) & 7))) * 8);
         }
       }
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa4[kk][i], fb4[kk][j], acc[i][j], 0, 0, 0);
   };
 
   if (nb > 0) dma(0, w);
@@ -1817,11 +1825,18 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
     return VKWR_OK;
   }
   if (cfg.rm) {
-    if (cfg.kn && cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, true>), dim3(wgs), dim3(256), 0, s, bt);
-    else if (cfg.kn) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, true>), dim3(wgs), dim3(256), 0, s, bt);
-    else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, false>), dim3(wgs), dim3(256), 0, s, bt);
-    else if (cfg.bn == 64) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, false>), dim3(wgs), dim3(256), 0, s, bt);
-    else hipLaunchKernelGGL((gemm_rm_kernel<1, 1, false>), dim3(wgs), dim3(512), 0, s, bt);
+    bool any_act = false;
+    for (int i = 0; i < bt.n; ++i) any_act = any_act || bt.p[i].a_act != VKWR_GEMM_ACT_NONE;
+    auto go_rm = [&](auto act) {
+      constexpr bool kAct = decltype(act)::value;
+      if (cfg.kn && cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, true, kAct>), dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.kn) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, true, kAct>), dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, false, kAct>), dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.bn == 64) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, false, kAct>), dim3(wgs), dim3(256), 0, s, bt);
+      else hipLaunchKernelGGL((gemm_rm_kernel<1, 1, false, kAct>), dim3(wgs), dim3(512), 0, s, bt);
+    };
+    if (any_act) go_rm(std::true_type{});
+    else go_rm(std::false_type{});
     if (int e = check_launch(fn)) return e;
     if (any_split) {
       hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_wgs(bt), bt.n), dim3(256), 0, s, bt);
