@@ -129,8 +129,9 @@ def capture(step_fn, n_steps, stream):
 
 def op_surface_decode(model, dev, steps, warmup=3):
     """The same config-3 decode step composed only of the reference's op surface
-    (vkwr.model_executor.OpDecodeEngine: vkwr._ops wrappers, token-shift rows gathered
-    with index_select and written back with index_copy_, WKV through the slot-pool op)
+    (vkwr.model_executor.OpDecodeEngine: vkwr._ops wrappers, the batch's token-shift rows
+    of every layer gathered with index_select at the start of the step and written back
+    with index_copy_ at its end, WKV through the slot-pool op)
     on a row-major 160-slot pool: device time of one step captured into a HIP graph and
     replayed, and the eager step (host dispatch of ~400 op calls included)."""
     from vkwr_amd import capi
@@ -173,7 +174,8 @@ def op_surface_decode(model, dev, steps, warmup=3):
             "path": "OpDecodeEngine: reference op wrappers only (add_layer_norm_tmix_mix6_f16, linear_f16_orig, relu_square, "
                     "linear_wag(v)_rank_in/out_f16, add_vec, tmix_kk_a_gate, wkv_forward_slots_fp32, "
                     "tmix_lnx_rkvres_xg, add_layer_norm_cmix_mix_f16, "
-                    "add_last_layer_norm_f16), shift rows gathered / scattered with index_select / index_copy_",
+                    "add_last_layer_norm_f16), shift rows of all layers gathered / scattered once per step "
+                    "with index_select / index_copy_",
             "timing": "ms_per_step: one step captured as a HIP graph and replayed (device time); "
                       "ms_per_step_eager: op calls issued from Python every step"}
 

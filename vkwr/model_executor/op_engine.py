@@ -26,8 +26,10 @@ vkwr/model_executor is empty) calls.  Per layer:
     logits = linear_f16_orig(add_last_layer_norm_f16(x, res, ...), head)
 
 The reference ops take a dense token-shift state [B, C] (updated in place), so
-the shift rows of the batch are gathered from the slot pools with index_select
-before the op and written back with index_copy_ after it.  The ops allocate
+the batch's shift rows of every layer are gathered from the slot pools with one
+index_select per pool at the start of the step, each layer's ops update its dense
+[B, C] rows in place, and one index_copy_ per pool writes them back at the end
+(per layer, the four gathers and scatters cost ~18 us of a ~160 us layer).  The ops allocate
 their outputs, as the reference's do (the caching allocator serves them; under
 a HIP graph capture they come from the graph's pool).  The only weight the ops
 want in another layout is the FFN value, which cmix_sparse_* takes as [F, C]:
@@ -74,15 +76,16 @@ class OpDecodeEngine:
         x = m.emb.index_select(0, tokens.long()).view(B, 1, C)
         res = torch.zeros_like(x)
         v_first = None
+        att_all = state.att_shift.index_select(1, sl)  # [L, B, C]: this batch's rows of every layer
+        ffn_all = state.ffn_shift.index_select(1, sl)
         d2 = lambda t: t.view(B, C)  # noqa: E731  (the rank ops take [M, K] matrices)
         d3 = lambda t: t.view(B, 1, C)  # noqa: E731  (the mix and WKV ops take [B, T, C])
         for l, L in enumerate(m.layers):
             first = l == 0
             # ---- time mix
-            att = state.att_shift[l].index_select(0, sl)
             res, xr, xw, xk, xv, xa, xg = NORM.add_layer_norm_tmix_mix6_f16(
-                x, res, att, L["ln1_w"], L["ln1_b"], L["x_r"], L["x_w"], L["x_k"], L["x_v"], L["x_a"], L["x_g"])
-            state.att_shift[l].index_copy_(0, sl, att)
+                x, res, att_all[l], L["ln1_w"], L["ln1_b"], L["x_r"], L["x_w"], L["x_k"], L["x_v"], L["x_a"],
+                L["x_g"])
             r = LIN.linear_f16_orig(xr, L["Wr"])
             k = LIN.linear_f16_orig(xk, L["Wk"])
             v = LIN.linear_f16_orig(xv, L["Wv"])
@@ -111,13 +114,13 @@ class OpDecodeEngine:
             o_in = MIX.tmix_lnx_rkvres_xg(B, 1, C, H, y, r, new_k, v, L["r_k"], L["lnx_w"], L["lnx_b"], d3(g))
             o = LIN.linear_f16_orig(o_in, L["Wo"])
             # ---- channel mix
-            ffn = state.ffn_shift[l].index_select(0, sl)
-            res, xk2 = NORM.add_layer_norm_cmix_mix_f16(o, res, ffn, L["ln2_w"], L["ln2_b"], L["x_k_ffn"])
-            state.ffn_shift[l].index_copy_(0, sl, ffn)
+            res, xk2 = NORM.add_layer_norm_cmix_mix_f16(o, res, ffn_all[l], L["ln2_w"], L["ln2_b"], L["x_k_ffn"])
             pre = LIN.linear_f16_orig(xk2, L["key"])
             if self.ffn == "dense":
                 x = LIN.linear_f16_orig(MIX.relu_square(pre), L["value"])
             else:
                 x = MIX.cmix_sparse_down_relu_rows(B, 1, C, F, pre, self.value_fc[l])
+        state.att_shift.index_copy_(1, sl, att_all)
+        state.ffn_shift.index_copy_(1, sl, ffn_all)
         h = NORM.add_last_layer_norm_f16(x, res, m.ln_out_w, m.ln_out_b)
         return LIN.linear_f16_orig(h, m.head)
