@@ -369,6 +369,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(Batch bt) {
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(Batch bt) {
   __shared__ float wsum[4][64];
   const Prob& P = bt.p[blockIdx.y];
+  {
+    // every field in one round of kernel-argument loads, before the first branch (the
+    // compiler otherwise issued them one dependent round at a time, five in all)
+    const _Float16 *fv = P.v, *fvf = P.vf, *fv0 = P.v0;
+    _Float16* fc = P.c;
+    float* fws = P.ws;
+    const int f0 = P.m, f1 = P.n, f2 = P.epi, f3 = P.splits;
+    asm volatile("" ::"s"(fv), "s"(fvf), "s"(fv0), "s"(fc), "s"(fws), "s"(f0), "s"(f1), "s"(f2), "s"(f3));
+  }
   if (P.splits <= 1) return;
   const int64_t mn = (int64_t)P.m * P.n;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -960,7 +969,8 @@ constexpr int rm_waves() { return TM * TN == 1 ? 8 : 4; }
 // reads of a whole k block have no branch between them and the matrix products, so they are
 // all issued before the first product (with the activation's per-element branches in the
 // loop, each product waited for its own two reads).
-template <int TM, int TN, bool kKN, bool kAct>
+// kMulti: the batch holds more than one problem (the workgroup first finds its own).
+template <int TM, int TN, bool kKN, bool kAct, bool kMulti>
 __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batch bt) {
   constexpr int kRmNW = rm_waves<TM, TN>();
   static_assert(!kKN || TN == 2, "[K,N] weights are staged as 128-byte k rows of 64 columns");
@@ -971,10 +981,25 @@ __global__ __launch_bounds__((64 * rm_waves<TM, TN>())) void gemm_rm_kernel(Batc
   __shared__ __attribute__((aligned(1024))) _Float16 sm[kRmNW][2][kStage];
   const int t = blockIdx.x;
   int pi = 0;
+  if constexpr (kMulti) {
 #pragma unroll
-  for (int i = 1; i < kMaxProblems; ++i)
-    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+    for (int i = 1; i < kMaxProblems; ++i)
+      if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  }
   const Prob& P = bt.p[pi];
+  {
+    // Every field of the problem is requested here, in one round of kernel-argument loads
+    // (the empty asm pins them above the first branch): left alone the compiler issued them
+    // in two dependent rounds after finding the problem, each ~0.3 us before the first
+    // operand load.  A one-problem launch (every op-surface linear call) has no search.
+    const _Float16 *fa = P.a, *fb = P.b, *fv = P.v, *fvf = P.vf, *fv0 = P.v0;
+    _Float16* fc = P.c;
+    float* fws = P.ws;
+    const int f0 = P.m, f1 = P.n, f2 = P.k, f3 = P.a_act, f4_ = P.epi, f5 = P.vec_out, f6 = P.tiles_m,
+              f7 = P.tiles_n, f8 = P.splits, f9 = P.k_per_split, f10 = P.tile_begin;
+    asm volatile("" ::"s"(fa), "s"(fb), "s"(fv), "s"(fvf), "s"(fv0), "s"(fc), "s"(fws), "s"(f0), "s"(f1), "s"(f2),
+                 "s"(f3), "s"(f4_), "s"(f5), "s"(f6), "s"(f7), "s"(f8), "s"(f9), "s"(f10));
+  }
   const int ntiles = P.tiles_m * P.tiles_n;
   const int lt0 = t - P.tile_begin;
   const int split = lt0 / ntiles;  // K part (split-major: the parts of a tile run apart in time)
@@ -1202,15 +1227,28 @@ __device__ __forceinline__ void gv_stage_x(_Float16* xs, const Prob& P, int k0, 
 // [N,K] weights: a wave owns 4 rows over the whole of K; lane l reads chunks l, l + 64, ...
 // of each row (a kilobyte per instruction), and the (row, m) sums are reduced across the
 // wave in a fixed order.
-template <int M>
+template <int M, bool kMulti>
 __global__ __launch_bounds__(256) void gemv_nk_kernel(Batch bt) {
   __shared__ __attribute__((aligned(16))) _Float16 xs[kGvLdsHalfs];
   const int t = blockIdx.x;
   int pi = 0;
+  if constexpr (kMulti) {
 #pragma unroll
-  for (int i = 1; i < kMaxProblems; ++i)
-    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+    for (int i = 1; i < kMaxProblems; ++i)
+      if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  }
   const Prob& P = bt.p[pi];
+  {
+    // every field in one round of kernel-argument loads, before the first branch (one round
+    // in all for a one-problem launch; the compiler otherwise issued dependent rounds)
+    const _Float16 *fa = P.a, *fb = P.b, *fv = P.v, *fvf = P.vf, *fv0 = P.v0;
+    _Float16* fc = P.c;
+    float* fws = P.ws;
+    const int f0 = P.m, f1 = P.n, f2 = P.k, f3 = P.a_act, f4_ = P.epi, f5 = P.vec_out, f6 = P.splits,
+              f7 = P.k_per_split, f8 = P.tile_begin, f9 = P.vec;
+    asm volatile("" ::"s"(fa), "s"(fb), "s"(fv), "s"(fvf), "s"(fv0), "s"(fc), "s"(fws), "s"(f0), "s"(f1), "s"(f2),
+                 "s"(f3), "s"(f4_), "s"(f5), "s"(f6), "s"(f7), "s"(f8), "s"(f9));
+  }
   const int N = P.n, K = P.k;
   const int nr0 = (t - P.tile_begin) * kGvRowsNK;
   gv_stage_x(xs, P, 0, K, K);
@@ -1278,17 +1316,30 @@ __global__ __launch_bounds__(256) void gemv_nk_kernel(Batch bt) {
 // are added in wave order.  With K split over workgroups (P.splits > 1) each part stores
 // fp32 sums to the workspace and splitk_reduce_kernel adds the parts and applies the
 // epilogue.
-template <int M>
+template <int M, bool kMulti>
 __global__ __launch_bounds__(256) void gemv_kn_kernel(Batch bt) {
   __shared__ __attribute__((aligned(16))) _Float16 xs[M * kGvRowsKN];
   __shared__ __attribute__((aligned(16))) float red[4][M][kGvColsKN];
   __shared__ __attribute__((aligned(16))) unsigned short nz[kGvRowsKN];  // wave w's list at w * q16
   const int t = blockIdx.x;
   int pi = 0;
+  if constexpr (kMulti) {
 #pragma unroll
-  for (int i = 1; i < kMaxProblems; ++i)
-    if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+    for (int i = 1; i < kMaxProblems; ++i)
+      if (i < bt.n && t >= bt.p[i].tile_begin) pi = i;
+  }
   const Prob& P = bt.p[pi];
+  {
+    // every field in one round of kernel-argument loads, before the first branch (one round
+    // in all for a one-problem launch; the compiler otherwise issued dependent rounds)
+    const _Float16 *fa = P.a, *fb = P.b, *fv = P.v, *fvf = P.vf, *fv0 = P.v0;
+    _Float16* fc = P.c;
+    float* fws = P.ws;
+    const int f0 = P.m, f1 = P.n, f2 = P.k, f3 = P.a_act, f4_ = P.epi, f5 = P.vec_out, f6 = P.splits,
+              f7 = P.k_per_split, f8 = P.tile_begin, f9 = P.vec;
+    asm volatile("" ::"s"(fa), "s"(fb), "s"(fv), "s"(fvf), "s"(fv0), "s"(fc), "s"(fws), "s"(f0), "s"(f1), "s"(f2),
+                 "s"(f3), "s"(f4_), "s"(f5), "s"(f6), "s"(f7), "s"(f8), "s"(f9));
+  }
   const int N = P.n, K = P.k;
   int lt = t - P.tile_begin;
   const int part = lt % P.splits;
@@ -1809,13 +1860,23 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
   hipStream_t s = (hipStream_t)stream;
   if (cfg.gv) {
     if (cfg.kn) {
-      if (cfg.gv == 1) hipLaunchKernelGGL(gemv_kn_kernel<1>, dim3(wgs), dim3(256), 0, s, bt);
-      else if (cfg.gv == 2) hipLaunchKernelGGL(gemv_kn_kernel<2>, dim3(wgs), dim3(256), 0, s, bt);
-      else hipLaunchKernelGGL(gemv_kn_kernel<4>, dim3(wgs), dim3(256), 0, s, bt);
+      auto go_gv = [&](auto multi) {
+        constexpr bool kM = decltype(multi)::value;
+        if (cfg.gv == 1) hipLaunchKernelGGL((gemv_kn_kernel<1, kM>), dim3(wgs), dim3(256), 0, s, bt);
+        else if (cfg.gv == 2) hipLaunchKernelGGL((gemv_kn_kernel<2, kM>), dim3(wgs), dim3(256), 0, s, bt);
+        else hipLaunchKernelGGL((gemv_kn_kernel<4, kM>), dim3(wgs), dim3(256), 0, s, bt);
+      };
+      if (bt.n > 1) go_gv(std::true_type{});
+      else go_gv(std::false_type{});
     } else {
-      if (cfg.gv == 1) hipLaunchKernelGGL(gemv_nk_kernel<1>, dim3(wgs), dim3(256), 0, s, bt);
-      else if (cfg.gv == 2) hipLaunchKernelGGL(gemv_nk_kernel<2>, dim3(wgs), dim3(256), 0, s, bt);
-      else hipLaunchKernelGGL(gemv_nk_kernel<4>, dim3(wgs), dim3(256), 0, s, bt);
+      auto go_gv = [&](auto multi) {
+        constexpr bool kM = decltype(multi)::value;
+        if (cfg.gv == 1) hipLaunchKernelGGL((gemv_nk_kernel<1, kM>), dim3(wgs), dim3(256), 0, s, bt);
+        else if (cfg.gv == 2) hipLaunchKernelGGL((gemv_nk_kernel<2, kM>), dim3(wgs), dim3(256), 0, s, bt);
+        else hipLaunchKernelGGL((gemv_nk_kernel<4, kM>), dim3(wgs), dim3(256), 0, s, bt);
+      };
+      if (bt.n > 1) go_gv(std::true_type{});
+      else go_gv(std::false_type{});
     }
     if (int e = check_launch(fn)) return e;
     if (any_split) {
@@ -1827,16 +1888,24 @@ int gemm_run(const char* fn, Batch& bt, const Config& cfg, void* workspace, void
   if (cfg.rm) {
     bool any_act = false;
     for (int i = 0; i < bt.n; ++i) any_act = any_act || bt.p[i].a_act != VKWR_GEMM_ACT_NONE;
-    auto go_rm = [&](auto act) {
-      constexpr bool kAct = decltype(act)::value;
-      if (cfg.kn && cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, true, kAct>), dim3(wgs), dim3(256), 0, s, bt);
-      else if (cfg.kn) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, true, kAct>), dim3(wgs), dim3(256), 0, s, bt);
-      else if (cfg.bm == 64) hipLaunchKernelGGL((gemm_rm_kernel<2, 2, false, kAct>), dim3(wgs), dim3(256), 0, s, bt);
-      else if (cfg.bn == 64) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, false, kAct>), dim3(wgs), dim3(256), 0, s, bt);
-      else hipLaunchKernelGGL((gemm_rm_kernel<1, 1, false, kAct>), dim3(wgs), dim3(512), 0, s, bt);
+    auto go_rm = [&](auto act, auto multi) {
+      constexpr bool kAct = decltype(act)::value, kM = decltype(multi)::value;
+      if (cfg.kn && cfg.bm == 64)
+        hipLaunchKernelGGL((gemm_rm_kernel<2, 2, true, kAct, kM>), dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.kn) hipLaunchKernelGGL((gemm_rm_kernel<1, 2, true, kAct, kM>), dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.bm == 64)
+        hipLaunchKernelGGL((gemm_rm_kernel<2, 2, false, kAct, kM>), dim3(wgs), dim3(256), 0, s, bt);
+      else if (cfg.bn == 64)
+        hipLaunchKernelGGL((gemm_rm_kernel<1, 2, false, kAct, kM>), dim3(wgs), dim3(256), 0, s, bt);
+      else hipLaunchKernelGGL((gemm_rm_kernel<1, 1, false, kAct, kM>), dim3(wgs), dim3(512), 0, s, bt);
     };
-    if (any_act) go_rm(std::true_type{});
-    else go_rm(std::false_type{});
+    if (bt.n > 1) {
+      if (any_act) go_rm(std::true_type{}, std::true_type{});
+      else go_rm(std::false_type{}, std::true_type{});
+    } else {
+      if (any_act) go_rm(std::true_type{}, std::false_type{});
+      else go_rm(std::false_type{}, std::false_type{});
+    }
     if (int e = check_launch(fn)) return e;
     if (any_split) {
       hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_wgs(bt), bt.n), dim3(256), 0, s, bt);
