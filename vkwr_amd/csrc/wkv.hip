@@ -44,6 +44,29 @@ struct Fp32Args {
   _Float16* y;
 };
 
+// Kernel-argument pinning.  Left alone the compiler requested a kernel's arguments in
+// dependent rounds of scalar loads around the slot lookup -- four before a decode step's
+// state load, each ~0.3 us on every wave's path.  Passing every field through an empty asm
+// above the first branch makes every later use wait on one round.  The asm is not volatile
+// and names no memory, so the slot lookup after it still counts as unclobbered and stays a
+// scalar load (a volatile asm may write memory: the lookup then became a vector load, slower
+// than the rounds it saved).  A pointer that comes out of an asm has lost its address space;
+// passing it through as a global-space pointer keeps its loads and stores global rather
+// than flat ones.
+template <class T>
+__device__ __forceinline__ void pin_ptr(T*& ptr) {
+  auto g = (__attribute__((address_space(1))) T*)ptr;
+  asm("" : "+s"(g));
+  ptr = (T*)g;
+}
+__device__ __forceinline__ void pin_int(int& x) { asm("" : "+s"(x)); }
+
+__device__ __forceinline__ void pin_args(Fp32Args& p) {
+  pin_int(p.T), pin_int(p.C), pin_int(p.H), pin_int(p.n_slots);
+  pin_ptr(p.state), pin_ptr(p.slots), pin_ptr(p.r), pin_ptr(p.w), pin_ptr(p.k), pin_ptr(p.v);
+  pin_ptr(p.a), pin_ptr(p.b), pin_ptr(p.y);
+}
+
 // ---- fp32 state staging: HBM <-> LDS (swizzled) <-> VGPRs, one column half
 // per phase (see the State I/O note above).  `st` is the 8 KiB tile.  kNT: the
 // state is loaded and stored with the non-temporal cache policy.
@@ -177,6 +200,7 @@ __device__ __forceinline__ float* state_block(const Fp32Args& p, int bi, int h) 
 template <bool kSlots, bool kNT>
 __global__ __launch_bounds__(64, 4) void wkv7_fp32_step_kernel(Fp32Args p) {
   __shared__ f4 st[512];
+  pin_args(p);
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int bi = bh / p.H;
@@ -418,6 +442,7 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // (state tables larger than the memory-side cache).
 template <bool kNT>
 __global__ __launch_bounds__(64) void wkv7_fp32_step_rows_kernel(Fp32Args p) {
+  pin_args(p);
   const int lane = threadIdx.x, g = lane & 7, q = lane >> 3;
   const int bh = blockIdx.x;
   const int bi = bh / p.H;
@@ -1187,12 +1212,12 @@ void launch_fp32(const Fp32Args& p, int B, hipStream_t stream, bool rows) {
 // never leave registers and the per-head reductions are wave reductions.
 struct FusedArgs {
   int C, H, n_slots;
+  int out_frag;  // (beside the other ints: one 16-byte scalar load for the four)
   float* pool;
   const int32_t* slots;
   const _Float16 *r, *w, *k, *v, *a12, *g;
   const _Float16 *k_k, *a0, *k_a, *r_k, *ln_w, *ln_b;
   _Float16* out;
-  int out_frag;
 };
 
 // kIlv: the pool is in the interleaved layout (vkwr_amd.h VKWR_WKV_STATE_ILV):
@@ -1205,6 +1230,11 @@ template <bool kIlv>
 __global__ __launch_bounds__(64, 4) void wkv7_decode_fused_kernel(FusedArgs p) {
   __shared__ f4 st[512];
   __shared__ float vb[5 * kHead];  // the token's channel vectors, staged before the state phase
+  // every argument in one round of scalar loads, above the first branch (as pin_args)
+  pin_int(p.C), pin_int(p.H), pin_int(p.n_slots), pin_int(p.out_frag);
+  pin_ptr(p.pool), pin_ptr(p.slots), pin_ptr(p.r), pin_ptr(p.w), pin_ptr(p.k), pin_ptr(p.v), pin_ptr(p.a12);
+  pin_ptr(p.g), pin_ptr(p.k_k), pin_ptr(p.a0), pin_ptr(p.k_a), pin_ptr(p.r_k), pin_ptr(p.ln_w), pin_ptr(p.ln_b);
+  pin_ptr(p.out);
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int bi = bh / p.H;
@@ -1306,6 +1336,10 @@ struct Fp16Args {
 template <bool kLegacy>
 __global__ __launch_bounds__(64) void wkv7_fp16_kernel(Fp16Args p) {
   __shared__ f4 st[512];  // one head's fp16 state (8 KiB); reused for token vectors
+  // every argument in one round of scalar loads, above the first branch (as pin_args)
+  pin_int(p.T), pin_int(p.C), pin_int(p.H);
+  pin_ptr(p.state), pin_ptr(p.r), pin_ptr(p.w), pin_ptr(p.w0), pin_ptr(p.k), pin_ptr(p.v), pin_ptr(p.a);
+  pin_ptr(p.b), pin_ptr(p.y), pin_ptr(p.elapsed);
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int bi = bh / p.H;
@@ -1730,8 +1764,8 @@ extern "C" int vkwr_wkv7_decode_fused_f16(int B, int C, int H, float* pool, int 
   VK_REQUIRE(pool && slots && r && w && k && v && a12 && g && k_k && a0 && k_a && r_k && ln_w && ln_b && out,
              "%s: null pointer", fn);
   auto h = [](const uint16_t* x) { return reinterpret_cast<const _Float16*>(x); };
-  FusedArgs p{C, H, n_slots, pool, slots, h(r), h(w), h(k), h(v), h(a12), h(g),
-              h(k_k), h(a0), h(k_a), h(r_k), h(ln_w), h(ln_b), reinterpret_cast<_Float16*>(out), out_frag};
+  FusedArgs p{C, H, n_slots, out_frag, pool, slots, h(r), h(w), h(k), h(v), h(a12), h(g),
+              h(k_k), h(a0), h(k_a), h(r_k), h(ln_w), h(ln_b), reinterpret_cast<_Float16*>(out)};
   if (state_layout == VKWR_WKV_STATE_ILV)
     hipLaunchKernelGGL(wkv7_decode_fused_kernel<true>, dim3(B * H), dim3(64), 0, (hipStream_t)stream, p);
   else
