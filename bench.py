@@ -15,6 +15,7 @@ Prints one JSON line (rank 0).  `--gpus N` with N > 1 is refused: this build
 measures one GPU.
 """
 import argparse
+import traceback
 import json
 import os
 import sys
@@ -996,39 +997,51 @@ def main():
         "cpu_baseline": None,
     }
     keep = [] if not args.no_cpu_baseline else None
+
+    def section(fn, done):
+        """Runs one secondary section; a Python-level failure (out of memory, a failed check) is
+        recorded in its place and the line is still printed."""
+        try:
+            out = fn()
+        except Exception as e:  # noqa: BLE001
+            traceback.print_exc()
+            out = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.empty_cache()
+        log(done)
+        return out
+
     if args.model_steps > 0 and not args.eager:
         del inputs
         torch.cuda.empty_cache()
-        result["decode_1p5b_bs128"] = model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm,
-                                                   keep_cpu_model=keep, op_steps=args.model_steps)
-        torch.cuda.empty_cache()
-        log("config 3 decode step done")
+        result["decode_1p5b_bs128"] = section(
+            lambda: model_decode(dev, args.model_steps, frag=not args.rowmajor_gemm, keep_cpu_model=keep,
+                                 op_steps=args.model_steps), "config 3 decode step done")
     if args.prefill_calls > 0 and not args.eager:
-        result["prefill_c2"] = prefill_c2(dev, args.prefill_calls)
-        log("config 2 prefill done")
+        result["prefill_c2"] = section(lambda: prefill_c2(dev, args.prefill_calls), "config 2 prefill done")
     if args.fp16_steps > 0 and not args.eager:
-        result["wkv_fp16_family"] = wkv_fp16_family(dev, args.fp16_steps)
-        log("fp16-state WKV done")
+        result["wkv_fp16_family"] = section(lambda: wkv_fp16_family(dev, args.fp16_steps),
+                                            "fp16-state WKV done")
     if args.serve_steps > 0 and not args.eager:
-        result["serve_mixed_7b"] = serve_mixed_7b(dev, args.serve_steps)
-        result["serve_mixed_7b"]["gemm_shapes_vs_hipblaslt"] = gemm_7b_shapes(dev)
-        log("config 4 mixed step done")
+        def serve():
+            out = serve_mixed_7b(dev, args.serve_steps)
+            out["gemm_shapes_vs_hipblaslt"] = gemm_7b_shapes(dev)
+            return out
+        result["serve_mixed_7b"] = section(serve, "config 4 mixed step done")
     if args.sampling_calls > 0 and not args.eager:
-        result["sampling_bs128"] = sampling_bs128(dev, args.sampling_calls)
-        log("sampling done")
+        result["sampling_bs128"] = section(lambda: sampling_bs128(dev, args.sampling_calls),
+                                           "sampling done")
     if args.ops_calls > 0 and not args.eager:
-        result["ops_small_m"] = ops_small_m(dev, args.ops_calls)
-        log("op-surface GEMMs done")
+        result["ops_small_m"] = section(lambda: ops_small_m(dev, args.ops_calls), "op-surface GEMMs done")
     if not args.no_cpu_baseline:
         cb = cpu_baseline(args.cpu_seconds)
         log("CPU baseline, config 1 done")
         per = {"config1_decode_step": dict(cb)}
-        if "prefill_c2" in result:
-            per["config2_prefill"] = result["prefill_c2"]["cpu_baseline"] = cpu_baseline_prefill()
-            log("CPU baseline, config 2 done")
+        if "error" not in result.get("prefill_c2", {"error": None}):
+            per["config2_prefill"] = result["prefill_c2"]["cpu_baseline"] = section(
+                cpu_baseline_prefill, "CPU baseline, config 2 done")
         if keep:
-            per["config3_decode_1p5b"] = result["decode_1p5b_bs128"]["cpu_baseline"] = \
-                cpu_baseline_decode(keep.pop())
+            per["config3_decode_1p5b"] = result["decode_1p5b_bs128"]["cpu_baseline"] = section(
+                lambda: cpu_baseline_decode(keep.pop()), "CPU baseline, config 3 done")
         cb["per_config"] = per
         result["cpu_baseline"] = cb
     print(json.dumps(result), flush=True)
