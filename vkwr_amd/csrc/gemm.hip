@@ -63,6 +63,11 @@ struct Prob {
 struct Batch {
   int n;
   Prob p[kMaxProblems];
+  // Large-M batches of unequal K (whole tiles, every problem's tile count a multiple of 8):
+  // each XCD takes an equal share of every problem's tiles, longest K first (order[] holds
+  // the problems in decreasing K).  0: the XCD-contiguous tile order.
+  int xbal;
+  int order[kMaxProblems];
 };
 
 // A-operand activations.  Each workgroup applies them to every A element it reads, so a
@@ -832,12 +837,29 @@ __device__ __forceinline__ void big_tile_run(_Float16 (&sm)[2][2][kBigTile], con
   }
 }
 
+// Unequal-K batch (bt.xbal): XCD x (workgroup b runs on XCD b % 8) takes tiles x T_p / 8 ..
+// (x + 1) T_p / 8 - 1 of every problem p, the longest-K problem's first.  In the
+// XCD-contiguous order each XCD would hold one problem's tiles, and the XCDs holding the
+// long-K tiles (the 7B rank-out batch: K = 512 for g2, 128 for the others) would run for
+// several times as long as the rest.
+__device__ __forceinline__ int big_balanced_tile(const Batch& bt, int b) {
+  const int x = b & 7;
+  int idx = b >> 3;
+  for (int q = 0; q < bt.n; ++q) {
+    const Prob& P = bt.p[bt.order[q]];
+    const int share = P.tiles_m * P.tiles_n / 8;
+    if (idx < share) return P.tile_begin + x * share + idx;
+    idx -= share;
+  }
+  return 0;  // not reached: the grid has one workgroup per tile
+}
+
 // Whole tiles: workgroup b takes logical tile (XCD-contiguous order) of the first `tiles`.
 // kEpi >= 0: every problem of the batch has that epilogue; -1: each its own.
 template <int BM, int kEpi>
 __global__ __launch_bounds__(256, 1) void gemm_big_kernel(Batch bt, int tiles) {
   __shared__ __attribute__((aligned(1024))) _Float16 sm[2][2][kBigTile];  // [buffer][A/B]: 128 KiB
-  const int L = xcd_contiguous(blockIdx.x, tiles);
+  const int L = bt.xbal ? big_balanced_tile(bt, blockIdx.x) : xcd_contiguous(blockIdx.x, tiles);
   int m0, n0;
   const Prob& P = bt.p[big_tile<BM>(bt, L, m0, n0)];
   big_tile_run<BM, false, kEpi>(sm, P, m0, n0, 0, P.k / kBigBK, nullptr);
@@ -1689,7 +1711,18 @@ double plan_big_bm(Batch& bt, BigPlan& pl, int BM) {
   pl = BigPlan{BM, T, 0, 1, 0, 0, 0, 0, nullptr};
   const int G = device_cus();
   const double stage = 1.7 * (BM == 192 ? 0.80 : 1.0), over = 2.0 * stage, split_launches = 6.0;
-  if (!uniform_k) return -(double)T / ((double)((T + G - 1) / G) * G);
+  if (!uniform_k) {
+    // whole tiles; spread every problem's tiles evenly over the XCDs where the counts allow
+    bool even = true;
+    for (int i = 0; i < bt.n; ++i) {
+      bt.order[i] = i;
+      even = even && (bt.p[i].tiles_m * bt.p[i].tiles_n) % 8 == 0;
+    }
+    std::stable_sort(bt.order, bt.order + bt.n, [&](int a, int b) { return bt.p[a].k > bt.p[b].k; });
+    bt.xbal = even ? 1 : 0;
+    return -(double)T / ((double)((T + G - 1) / G) * G);
+  }
+  bt.xbal = 0;
   const int nst = k_all / kBigBK;
   const double rounds_whole = (double)((T + G - 1) / G);
   double best = rounds_whole * (nst * stage + over);
@@ -1762,6 +1795,7 @@ int build_batch(const char* fn, int n, const vkwr_gemm_problem* pr, Batch& bt, C
   VK_REQUIRE(n >= 1 && n <= kMaxProblems, "%s: 1..%d problems per launch (got %d)", fn, kMaxProblems, n);
   VK_REQUIRE(pr != nullptr, "%s: null problem list", fn);
   bt.n = n;
+  bt.xbal = 0;
   int max_m = 0, min_n = 1 << 30;
   for (int i = 0; i < n; ++i) {
     const vkwr_gemm_problem& q = pr[i];
