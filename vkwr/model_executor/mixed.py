@@ -121,8 +121,8 @@ class MixedEngine:
         decode engine's frag GEMM; as an A-operand activation every column tile of this GEMM
         recomputed them, 56 of the 103 us of g2 at the 7B shape)."""
         s, gp = self, capi.gemm_problem
-        # g2 (the longest K) first: its tiles start in the first round and the short ones
-        # fill in behind them
+        # (the large-M GEMM gives every XCD an equal share of each problem's tiles, longest K
+        # first, whatever the order of the batch)
         ps = [gp(s.g1[:R], W["g2"], s.g[:R]),
               gp(s.w1[:R], W["w2"], s.w[:R], epilogue=capi.EPI_BIAS, v0=L["w0"]),
               gp(s.a1[:R], W["a2"], s.a12[:R])]
