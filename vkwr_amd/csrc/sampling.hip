@@ -474,10 +474,14 @@ __global__ __launch_bounds__(kSampThreads) void sampling_kernel(SampArgs p) {
         for (int q = 0; q < 4; ++q) {
           // the window test again, on the bit patterns (the same test for
           // non-negative floats), so that the compiler does not keep the first
-          // sweep's results alive across the barrier
+          // sweep's results alive across the barrier.  A few hundred of the row's
+          // entries are in the window, so most (slot, element) positions hold none in
+          // any lane of the wave: the wave skips those (a uniform branch on the ballot).
           const bool in = __builtin_bit_cast(uint32_t, e[q]) - lo <= hi - lo;
-          sh.cand[in ? min(at, kCandCap) : kCandCap + lane] = e[q];
-          at += in ? 1 : 0;
+          if (ballot(in) != 0) {
+            sh.cand[in ? min(at, kCandCap) : kCandCap + lane] = e[q];
+            at += in ? 1 : 0;
+          }
         }
       }
       __syncthreads();
